@@ -1,0 +1,191 @@
+"""Benchmark of the MI355X optimizer step (BASELINE config 2 on one GPU).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one optimizer step over the 5B-preset SwiGLU stage window
+(W_gate, W_up [6144, 3072] and W_down [3072, 6144]; N = 56,623,104 FP32
+masters): clear the overflow flag, run the non-finite detector over the FP16
+gradients, then the fused unscale + AdamW + FP16 export kernel, then read the
+skip decision and advance the loss scale and clocks.  Inputs are synthetic
+(seeded), resident in HBM before the timed region.
+
+Prints one JSON line.  `value` is whole-step throughput in Gparams/s;
+`roofline` is the fused AdamW kernel's algorithmic bandwidth (28 bytes per
+parameter) over its average launch time, measured with HIP events on the
+launch stream; `cpu_baseline` times torch.optim.AdamW(foreach=False) -- the
+library the reference's AdamW group runs -- on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_PARAM = 28  # read g16 2 + w 4 + m 4 + v 4; write w 4 + m 4 + v 4 + export 2
+CONFIG2_SHAPES = [(6144, 3072), (6144, 3072), (3072, 6144)]  # W_gate, W_up, W_down (nn.Linear storage)
+LOSS_SCALE = 65536.0
+HYPER = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+
+# ------------------------------------------------------------ workloads --
+def config2_window(device, seed=0):
+    """FP32 masters N(0, .02) for the three SwiGLU matrices of one stage."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    return [torch.randn(s, generator=gen, device=device) * 0.02 for s in CONFIG2_SHAPES]
+
+
+def config2_grads(device, step_seed, shapes=CONFIG2_SHAPES, scale=LOSS_SCALE):
+    """FP16 gradients: fp16(N(0, 1e-4) * 2^16), one seeded draw per step."""
+    gen = torch.Generator(device=device).manual_seed(step_seed)
+    return [(torch.randn(s, generator=gen, device=device) * 1e-4 * scale).half() for s in shapes]
+
+
+def config3_embedding_grad(step_seed, rows=65536, cols=3072, tokens=4 * 1024, s=1.1,
+                           device="cpu"):
+    """BF16 tied-embedding gradient: N(0, 1e-3) on Zipf(1.1)-sampled rows, zero elsewhere."""
+    gen = torch.Generator().manual_seed(step_seed)
+    ranks = torch.arange(1, rows + 1, dtype=torch.float64)
+    probs = ranks.pow(-s)
+    ids = torch.multinomial(probs / probs.sum(), tokens, replacement=True, generator=gen)
+    active = torch.unique(ids)
+    g = torch.zeros(rows, cols, dtype=torch.bfloat16)
+    g[active] = (torch.randn(active.numel(), cols, generator=gen) * 1e-3).to(torch.bfloat16)
+    return g.to(device), active
+
+
+# --------------------------------------------------------------- timing --
+def time_gpu(steps, warmup):
+    from morph_amd import DynamicLossScale, FusedAdamW
+    from morph_amd import kernels
+
+    device = torch.device("cuda", 0)
+    masters = config2_window(device)
+    grads = config2_grads(device, 1000)
+    n = sum(p.numel() for p in masters)
+    scaler = DynamicLossScale(LOSS_SCALE, growth_interval=2000)
+    opt = FusedAdamW(masters, **HYPER, loss_scale=scaler, export_dtype=torch.float16)
+    stream = torch.cuda.current_stream(device)
+
+    # Events around the AdamW launch only (same stream, so they bracket that kernel).
+    orig_launch = kernels.AdamwBatch.launch
+    kernel_events = []
+
+    def timed_launch(self, hps, skip_flag=None, stream=None):
+        s = stream or torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        orig_launch(self, hps, skip_flag, stream)
+        e1.record(s)
+        kernel_events.append((e0, e1))
+
+    for _ in range(warmup):
+        assert opt.step(grads)
+    torch.cuda.synchronize()
+    kernels.AdamwBatch.launch = timed_launch
+    try:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            applied = opt.step(grads)
+            assert applied
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    finally:
+        kernels.AdamwBatch.launch = orig_launch
+    kernel_ms = [a.elapsed_time(b) for a, b in kernel_events]
+    avg_kernel_s = sum(kernel_ms) / len(kernel_ms) / 1e3
+    return dict(n=n, elapsed=elapsed, avg_kernel_s=avg_kernel_s, kernel_ms=kernel_ms,
+                scale=scaler.scale, stream=stream)
+
+
+def cpu_baseline(seconds=10.0):
+    """torch.optim.AdamW(foreach=False) on config 2's masters, on this host's cores.
+
+    The oracle's restatement of the reference CPU path: gradients unscaled from
+    FP16 (g.float() / scale, streamtrain/disk.py:447) then the library AdamW the
+    reference's HybridMuonAdamW runs (streamtrain/optimizer.py:40).  Runs whole
+    steps until `seconds` have passed (at least 2) and reports the median.
+    """
+    from oracle import reference as R
+    threads = min(16, R.cpu_threads())
+    torch.set_num_threads(threads)
+    masters = config2_window("cpu")
+    grads16 = config2_grads("cpu", 1000)
+    params = [torch.nn.Parameter(m) for m in masters]
+    opt = torch.optim.AdamW(params, **HYPER, foreach=False)
+    times = []
+    start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - start < seconds and len(times) < 20):
+        t0 = time.perf_counter()
+        for p, g in zip(params, grads16):
+            p.grad = g.float() / LOSS_SCALE
+        opt.step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    n = sum(p.numel() for p in params)
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return dict(value=round(n / med / 1e9, 4), unit="Gparams/s", cores=threads, kind="port",
+                sample=f"config 2 window (N={n}), {len(times)} whole steps, median; "
+                       f"torch.optim.AdamW(foreach=False) after FP16 unscale; CPU: {cpu}")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this "
+              "build (the optimizer step shards by contiguous ranges across GPUs, see the "
+              "design notes, but no multi-GPU run is part of it)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    r = time_gpu(args.steps, args.warmup)
+    n = r["n"]
+    ms_per_step = r["elapsed"] / args.steps * 1e3
+    achieved = BYTES_PER_PARAM * n / r["avg_kernel_s"] / 1e9
+    line = {
+        "metric": "AdamW Gparams/s + achieved HBM GB/s vs peak, 5B SwiGLU window, 1 MI355X",
+        "value": round(n * args.steps / r["elapsed"] / 1e9, 3),
+        "unit": "Gparams/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "config 2: 5B-preset SwiGLU stage window, FP32 masters, "
+                               "FP16 grads x 2^16 loss scale, detector + fused AdamW + FP16 export",
+                   "params": n, "shapes": CONFIG2_SHAPES, "grad_dtype": "f16",
+                   "export_dtype": "f16", **{k: v for k, v in HYPER.items()},
+                   "loss_scale": LOSS_SCALE},
+        "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "adamw_multi_kernel<F16,F16>",
+                     "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
+                     "bytes_per_launch": BYTES_PER_PARAM * n},
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

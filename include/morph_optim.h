@@ -1,0 +1,155 @@
+/*
+ * morph_optim.h -- C ABI of the MI355X (gfx950) mixed-precision optimizer step.
+ *
+ * This is the boundary below MORPH's Python optimizer API.  The Python side
+ * (morph_amd.optimizer / morph_amd.disk) keeps the reference signatures and
+ * calls these entry points through ctypes; no torch type crosses the boundary.
+ *
+ * Conventions shared by every entry point:
+ *   - Tensor pointers are device pointers owned by the caller.  The library
+ *     allocates nothing and keeps no state between calls, so calls are
+ *     re-entrant from several host threads.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
+ *     void*; NULL means the legacy default stream).  Ordering between calls
+ *     comes only from the stream.
+ *   - Return 0 (MORPH_OK) or a negative MORPH_E* code; morph_strerror()
+ *     names it.  A negative return means nothing was enqueued.
+ *
+ * Reference interfaces replaced (paths relative to the MORPH repository):
+ *   streamtrain/disk.py:203-223         DiskState.update chunk arithmetic
+ *   streamtrain/state_cache.py:103-140  CachedDiskState.update (same arithmetic)
+ *   streamtrain/optimizer.py:34-70      HybridMuonAdamW (Muon loop + AdamW group)
+ *   streamtrain/optimizer.py:13-22      orthogonalize (Newton-Schulz quintic)
+ *   streamtrain/optimizer.py:49-51      non-finite gradient gate
+ *   streamtrain/disk.py:482-488         overflow detection that drives
+ *                                       DynamicLossScale.overflow (precision.py:9-11)
+ *   torch/optim/adam.py:347-547         _single_tensor_adam, the AdamW group's
+ *                                       arithmetic (torch.optim.AdamW foreach=False)
+ */
+#ifndef MORPH_OPTIM_H
+#define MORPH_OPTIM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MORPH_ABI_VERSION 1
+
+/* Element types of gradient / export buffers. */
+enum morph_dtype {
+  MORPH_DTYPE_NONE = -1, /* no buffer (export disabled) */
+  MORPH_DTYPE_F32 = 0,
+  MORPH_DTYPE_F16 = 1,
+  MORPH_DTYPE_BF16 = 2
+};
+
+enum morph_status {
+  MORPH_OK = 0,
+  MORPH_EINVAL = -1,    /* null pointer, negative size, bad count */
+  MORPH_EDTYPE = -2,    /* unsupported dtype combination */
+  MORPH_ELAUNCH = -3,   /* the HIP launch itself failed */
+  MORPH_ERANGE = -4,    /* size exceeds what the entry point supports */
+  MORPH_EWORKSPACE = -5 /* workspace missing or too small */
+};
+
+/*
+ * Per-call AdamW constants.  Every field is computed on the host in double
+ * precision exactly as the reference computes it and rounded once to fp32,
+ * which is what torch's CPU kernels do with a Python scalar operand
+ * (torch/optim/adam.py:416-419, 457, 476, 528-547; streamtrain/disk.py:210-214).
+ *
+ * Per element, in this order (matching torch CPU op by op):
+ *   g  = grad / scale                 (or grad * inv_scale when scale is 2^k: identical bits)
+ *   g  = g * clip                     if MORPH_HP_APPLY_CLIP            (disk.py:210)
+ *   p  = p * decay                    if MORPH_HP_APPLY_DECAY           (adam.py:416-419)
+ *   m  = fma(lerp_weight, g - m, m)   torch lerp, weight < 0.5          (adam.py:457)
+ *      = fma(lerp_weight - 1, g - m, g)   if MORPH_HP_LERP_LARGE
+ *   v  = v * beta2;  v = fma(one_minus_beta2 * g, g, v)   torch addcmul  (adam.py:476)
+ *   d  = sqrt(v) / bias_correction2_sqrt + eps                           (adam.py:544)
+ *   p  = p + (neg_step_size * m) / d  torch addcdiv                      (adam.py:547)
+ *   out = round-to-nearest-even(p) to the export dtype (when out != NULL)
+ */
+typedef struct morph_adamw_hp {
+  float scale;
+  float inv_scale;
+  float clip;
+  float decay;
+  float lerp_weight;
+  float beta2;
+  float one_minus_beta2;
+  float bias_correction2_sqrt;
+  float neg_step_size;
+  float eps;
+  uint32_t flags;
+  uint32_t reserved;
+} morph_adamw_hp;
+
+#define MORPH_HP_DIVIDE_SCALE 1u /* scale is not a power of two: divide */
+#define MORPH_HP_APPLY_CLIP 2u
+#define MORPH_HP_APPLY_DECAY 4u /* weight_decay != 0 */
+#define MORPH_HP_LERP_LARGE 8u  /* lerp_weight >= 0.5 */
+
+/* One tensor of a multi-tensor AdamW launch. */
+typedef struct morph_adamw_tensor {
+  const void* grad;   /* grad_dtype elements */
+  float* param;       /* FP32 master, updated in place */
+  float* exp_avg;     /* FP32 first moment, in place */
+  float* exp_avg_sq;  /* FP32 second moment, in place */
+  void* out;          /* out_dtype export copy, or NULL */
+  int64_t numel;
+  int32_t hp_index;   /* index into the hps[] array of the call */
+  int32_t reserved;
+} morph_adamw_tensor;
+
+int morph_abi_version(void);
+const char* morph_strerror(int status);
+
+/* Sets *d_flag = 0 with a one-thread kernel (safe inside stream capture). */
+int morph_flag_clear(uint32_t* d_flag, void* stream);
+
+/*
+ * Non-finite detector.  Writes 1 to *d_flag if any of the n elements of
+ * `grad` (dtype F32/F16/BF16) is +-inf or NaN; never writes 0, so several
+ * calls OR into one flag.  Replaces the reference's non-finite decision:
+ * optimizer.py:49-51 (torch.isfinite(p.grad).all()) and disk.py:466-468 +
+ * 485 (math.isfinite of the FP64 gradient norm, which is non-finite exactly
+ * when some gradient element is).
+ */
+int morph_nonfinite_or(const void* grad, int dtype, int64_t n, uint32_t* d_flag,
+                       void* stream);
+/* Same over `count` tensors of one dtype, in one launch. */
+int morph_nonfinite_or_multi(const void* const* grads, const int64_t* numels, int count,
+                             int dtype, uint32_t* d_flag, void* stream);
+
+/*
+ * Fused AdamW step over one tensor: unscale + clip + decoupled decay + m/v
+ * update with bias correction + master update + optional FP16/BF16 export,
+ * one pass over HBM (28 bytes/parameter for an FP16 grad with FP16 export).
+ * If d_skip != NULL and *d_skip != 0 when the kernel runs, nothing is
+ * written (the conditional skip of a step whose gradients overflowed).
+ * Replaces disk.py:209-215 / state_cache.py:121-126 and the per-parameter
+ * body of torch/optim/adam.py:347-547.
+ */
+int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp_avg,
+                      float* exp_avg_sq, void* out, int out_dtype, int64_t n,
+                      const morph_adamw_hp* hp, const uint32_t* d_skip, void* stream);
+
+/*
+ * Multi-tensor form: `count` tensors (any count; the library splits it
+ * into launches of at most 32 tensors) sharing one grad and one export dtype.
+ * Each tensor selects its constants by hp_index into hps[0..n_hp).  This is
+ * the whole AdamW group of HybridMuonAdamW (optimizer.py:40, 62) or one
+ * stage window in one launch.
+ */
+int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dtype,
+                      int out_dtype, const morph_adamw_hp* hps, int n_hp,
+                      const uint32_t* d_skip, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MORPH_OPTIM_H */

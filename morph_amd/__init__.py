@@ -1,0 +1,10 @@
+"""MI355X-native mixed-precision optimizer step for MORPH's streamed trainer.
+
+Python host code over hand-written gfx950 HIP kernels reached through the C
+ABI in include/morph_optim.h.  There is no CPU fallback: every entry point
+requires the built library (python -m morph_amd.build) and GPU tensors.
+"""
+from .precision import DynamicLossScale
+from .optimizer import FusedAdamW
+
+__all__ = ["DynamicLossScale", "FusedAdamW"]

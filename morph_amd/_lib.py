@@ -1,0 +1,110 @@
+"""ctypes binding of libmorph_optim.so (the C ABI in include/morph_optim.h).
+
+The shared library is built in-tree by morph_amd.build into morph_amd/lib/.
+It links the same HIP runtime soname torch carries (libamdhip64.so.7), so
+torch is imported first: the dynamic loader then resolves the library's HIP
+calls to the runtime torch already loaded, and torch's streams and device
+pointers are valid in both.  There is no fallback: when the library is missing
+every entry point raises.
+"""
+import ctypes
+from pathlib import Path
+
+import torch  # noqa: F401  (must load the HIP runtime before the library)
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmorph_optim.so"
+ABI_VERSION = 1
+
+DTYPE_NONE, DTYPE_F32, DTYPE_F16, DTYPE_BF16 = -1, 0, 1, 2
+HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
+
+# Every symbol include/morph_optim.h declares.
+EXPORTS = (
+    "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
+    "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
+)
+
+
+class MorphError(RuntimeError):
+    """A negative status returned by the C ABI."""
+
+
+class AdamwHP(ctypes.Structure):
+    """morph_adamw_hp."""
+    _fields_ = [(name, ctypes.c_float) for name in (
+        "scale", "inv_scale", "clip", "decay", "lerp_weight", "beta2",
+        "one_minus_beta2", "bias_correction2_sqrt", "neg_step_size", "eps")] + [
+        ("flags", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+class AdamwTensor(ctypes.Structure):
+    """morph_adamw_tensor."""
+    _fields_ = [("grad", ctypes.c_void_p), ("param", ctypes.c_void_p),
+                ("exp_avg", ctypes.c_void_p), ("exp_avg_sq", ctypes.c_void_p),
+                ("out", ctypes.c_void_p), ("numel", ctypes.c_int64),
+                ("hp_index", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is missing: build the HIP library first "
+                "(python -m morph_amd.build); morph_amd has no CPU fallback")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+        sig = {
+            "morph_abi_version": ([], i32),
+            "morph_strerror": ([i32], ctypes.c_char_p),
+            "morph_flag_clear": ([vp, vp], i32),
+            "morph_nonfinite_or": ([vp, i32, i64, vp, vp], i32),
+            "morph_nonfinite_or_multi": ([vp, vp, i32, i32, vp, vp], i32),
+            "morph_adamw_fused": ([vp, i32, vp, vp, vp, vp, i32, i64, ctypes.POINTER(AdamwHP),
+                                   vp, vp], i32),
+            "morph_adamw_multi": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
+                                   ctypes.POINTER(AdamwHP), i32, vp, vp], i32),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(handle, name)
+            fn.argtypes, fn.restype = args, res
+        version = handle.morph_abi_version()
+        if version != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def check(status):
+    if status != 0:
+        raise MorphError(f"morph status {status}: {lib().morph_strerror(status).decode()}")
+
+
+def dtype_code(dtype):
+    if dtype is None:
+        return DTYPE_NONE
+    try:
+        return {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16,
+                torch.bfloat16: DTYPE_BF16}[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, float16 or bfloat16")
+
+
+def stream_handle(stream=None):
+    """Raw hipStream_t of a torch stream (default: the current one)."""
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def require_device_tensor(t, name):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must live on the GPU (got {t.device}); morph_amd has no CPU path")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")

@@ -1,0 +1,321 @@
+// Fused mixed-precision AdamW step for gfx950 (MI355X).
+//
+// One pass over HBM per parameter: read grad (fp16/bf16/fp32), master, m, v;
+// write master, m, v and the optional fp16/bf16 export copy.  That is 28 bytes
+// per parameter for an fp16 grad with fp16 export, the algorithmic minimum.
+//
+// Arithmetic follows torch's _single_tensor_adam (torch/optim/adam.py:414-419,
+// 457, 476, 528-547) and DiskState.update (streamtrain/disk.py:209-215) op for
+// op; the host supplies each fp32 constant already rounded (morph_adamw_hp).
+//
+// Layout and launch shape.  A launch covers up to kMaxTensors tensors.  Each
+// workgroup (256 lanes = 4 wave64) owns one contiguous chunk of kPerBlock
+// elements of one tensor; lane i of the group moves 4 consecutive elements per
+// access (one 128-bit load of each FP32 stream, one 64-bit load of a 16-bit
+// grad), and consecutive lanes cover consecutive 16-byte pieces, so every
+// wave-wide access is one contiguous 1 KiB (FP32) or 512 B (16-bit) segment.
+// kUnroll accesses per lane are issued before any arithmetic so each lane
+// keeps several 128-bit loads in flight.  Chunks map to workgroups in address
+// order; the dispatcher spreads consecutive workgroups round-robin over the 8
+// XCDs, which is what a pure stream with no reuse wants.
+#include "common.h"
+
+#ifndef MORPH_ADAMW_UNROLL
+#define MORPH_ADAMW_UNROLL 4
+#endif
+#ifndef MORPH_ADAMW_NT
+#define MORPH_ADAMW_NT 1
+#endif
+
+namespace morph {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = MORPH_ADAMW_UNROLL;
+constexpr bool kNT = MORPH_ADAMW_NT != 0;
+constexpr int kPerBlock = kBlock * 4 * kUnroll;
+constexpr int kMaxTensors = 24;
+constexpr int kMaxHp = 8;
+// A tensor is cut into segments of at most this many elements so block
+// counts stay far inside the 32-bit grid limits.
+constexpr int64_t kMaxSegment = int64_t(1) << 30;
+
+struct TensorArg {
+  const void* grad;
+  float* p;
+  float* m;
+  float* v;
+  void* out;
+  int64_t n;
+  int32_t hp;
+  int32_t first_block;
+  int32_t vector_ok;
+  int32_t pad;
+};
+
+struct LaunchArgs {
+  TensorArg t[kMaxTensors];
+  morph_adamw_hp hp[kMaxHp];
+  int32_t count;
+};
+
+__device__ __forceinline__ void adamw_update(float g, float& p, float& m, float& v,
+                                             const morph_adamw_hp& hp) {
+  const uint32_t fl = hp.flags;
+  // Unscale: g / scale.  For scale = 2^k the product with 2^-k is the same
+  // correctly rounded real number, so the cheaper multiply is bit-identical.
+  g = (fl & MORPH_HP_DIVIDE_SCALE) ? __fdiv_rn(g, hp.scale) : g * hp.inv_scale;
+  if (fl & MORPH_HP_APPLY_CLIP) g = g * hp.clip;
+  if (fl & MORPH_HP_APPLY_DECAY) p = p * hp.decay;
+  if (fl & MORPH_HP_LERP_LARGE)
+    m = __fmaf_rn(hp.lerp_weight - 1.0f, g - m, g);
+  else
+    m = __fmaf_rn(hp.lerp_weight, g - m, m);
+  v = __fmaf_rn(hp.one_minus_beta2 * g, g, v * hp.beta2);
+  const float d = __fdiv_rn(__fsqrt_rn(v), hp.bias_correction2_sqrt) + hp.eps;
+  p = p + __fdiv_rn(hp.neg_step_size * m, d);
+}
+
+// ---- grad loads: 4 consecutive elements -----------------------------------
+template <typename GT>
+__device__ __forceinline__ void load_grad4(const void* g, int64_t e, float (&x)[4]);
+
+template <>
+__device__ __forceinline__ void load_grad4<F32>(const void* g, int64_t e, float (&x)[4]) {
+  const f32x4 t = load_stream<kNT>(reinterpret_cast<const f32x4*>(static_cast<const float*>(g) + e));
+  x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+}
+template <typename H>
+__device__ __forceinline__ void load_half4(const void* g, int64_t e, float (&x)[4]) {
+  const u32x2 t = load_stream<kNT>(reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(g) + e));
+  x[0] = to_float<H>(t.x & 0xFFFFu);
+  x[1] = to_float<H>(t.x >> 16);
+  x[2] = to_float<H>(t.y & 0xFFFFu);
+  x[3] = to_float<H>(t.y >> 16);
+}
+template <>
+__device__ __forceinline__ void load_grad4<F16>(const void* g, int64_t e, float (&x)[4]) { load_half4<F16>(g, e, x); }
+template <>
+__device__ __forceinline__ void load_grad4<BF16>(const void* g, int64_t e, float (&x)[4]) { load_half4<BF16>(g, e, x); }
+
+template <typename GT>
+__device__ __forceinline__ float load_grad1(const void* g, int64_t i) {
+  if constexpr (std::is_same_v<GT, F32>) return static_cast<const float*>(g)[i];
+  else return to_float<GT>(static_cast<const uint16_t*>(g)[i]);
+}
+
+// ---- export stores ----------------------------------------------------------
+template <typename OT>
+__device__ __forceinline__ void store_out4(void* out, int64_t e, const f32x4& p) {
+  if constexpr (std::is_same_v<OT, NoOut>) {
+    return;
+  } else if constexpr (std::is_same_v<OT, F32>) {
+    store_stream<kNT>(reinterpret_cast<f32x4*>(static_cast<float*>(out) + e), p);
+  } else {
+    u32x2 t;
+    t.x = from_float<OT>(p.x) | (from_float<OT>(p.y) << 16);
+    t.y = from_float<OT>(p.z) | (from_float<OT>(p.w) << 16);
+    store_stream<kNT>(reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + e), t);
+  }
+}
+
+template <typename OT>
+__device__ __forceinline__ void store_out1(void* out, int64_t i, float p) {
+  if constexpr (std::is_same_v<OT, NoOut>) {
+    return;
+  } else if constexpr (std::is_same_v<OT, F32>) {
+    static_cast<float*>(out)[i] = p;
+  } else {
+    static_cast<uint16_t*>(out)[i] = (uint16_t)from_float<OT>(p);
+  }
+}
+
+template <typename GT, typename OT>
+__device__ __forceinline__ void chunk_vector(const TensorArg& T, const morph_adamw_hp& hp,
+                                             int64_t base) {
+  const int tid = threadIdx.x;
+  f32x4 P[kUnroll], M[kUnroll], V[kUnroll];
+  float G[kUnroll][4];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t e = base + (int64_t)(u * kBlock + tid) * 4;
+    load_grad4<GT>(T.grad, e, G[u]);
+    P[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.p + e));
+    M[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.m + e));
+    V[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.v + e));
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float p = P[u][k], m = M[u][k], v = V[u][k];
+      adamw_update(G[u][k], p, m, v, hp);
+      P[u][k] = p; M[u][k] = m; V[u][k] = v;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t e = base + (int64_t)(u * kBlock + tid) * 4;
+    store_stream<kNT>(reinterpret_cast<f32x4*>(T.p + e), P[u]);
+    store_stream<kNT>(reinterpret_cast<f32x4*>(T.m + e), M[u]);
+    store_stream<kNT>(reinterpret_cast<f32x4*>(T.v + e), V[u]);
+    if (T.out != nullptr) store_out4<OT>(T.out, e, P[u]);
+  }
+}
+
+template <typename GT, typename OT>
+__device__ __forceinline__ void chunk_scalar(const TensorArg& T, const morph_adamw_hp& hp,
+                                             int64_t begin, int64_t end) {
+  for (int64_t i = begin + threadIdx.x; i < end; i += kBlock) {
+    float p = T.p[i], m = T.m[i], v = T.v[i];
+    adamw_update(load_grad1<GT>(T.grad, i), p, m, v, hp);
+    T.p[i] = p;
+    T.m[i] = m;
+    T.v[i] = v;
+    if (T.out != nullptr) store_out1<OT>(T.out, i, p);
+  }
+}
+
+template <typename GT, typename OT>
+__global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const LaunchArgs a,
+                                                             const uint32_t* __restrict__ skip) {
+  // Conditional skip: a flagged (overflowed) step leaves every byte untouched.
+  if (skip != nullptr && *skip != 0u) return;
+  const int b = blockIdx.x;
+  int ti = 0;
+  while (ti + 1 < a.count && a.t[ti + 1].first_block <= b) ++ti;
+  const TensorArg& T = a.t[ti];
+  const morph_adamw_hp& hp = a.hp[T.hp];
+  const int64_t base = (int64_t)(b - T.first_block) * kPerBlock;
+  if (T.vector_ok && base + kPerBlock <= T.n)
+    chunk_vector<GT, OT>(T, hp, base);
+  else
+    chunk_scalar<GT, OT>(T, hp, base, base + kPerBlock < T.n ? base + kPerBlock : T.n);
+}
+
+template <typename GT, typename OT>
+int launch(const LaunchArgs& a, int blocks, const uint32_t* skip, hipStream_t s) {
+  hipLaunchKernelGGL((adamw_multi_kernel<GT, OT>), dim3(blocks), dim3(kBlock), 0, s, a, skip);
+  return launch_status();
+}
+
+template <typename GT>
+int launch_out(int out_dtype, const LaunchArgs& a, int blocks, const uint32_t* skip,
+               hipStream_t s) {
+  switch (out_dtype) {
+    case MORPH_DTYPE_NONE: return launch<GT, NoOut>(a, blocks, skip, s);
+    case MORPH_DTYPE_F32: return launch<GT, F32>(a, blocks, skip, s);
+    case MORPH_DTYPE_F16: return launch<GT, F16>(a, blocks, skip, s);
+    case MORPH_DTYPE_BF16: return launch<GT, BF16>(a, blocks, skip, s);
+    default: return MORPH_EDTYPE;
+  }
+}
+
+int dispatch(int grad_dtype, int out_dtype, const LaunchArgs& a, int blocks,
+             const uint32_t* skip, hipStream_t s) {
+  switch (grad_dtype) {
+    case MORPH_DTYPE_F32: return launch_out<F32>(out_dtype, a, blocks, skip, s);
+    case MORPH_DTYPE_F16: return launch_out<F16>(out_dtype, a, blocks, skip, s);
+    case MORPH_DTYPE_BF16: return launch_out<BF16>(out_dtype, a, blocks, skip, s);
+    default: return MORPH_EDTYPE;
+  }
+}
+
+int dtype_bytes(int dtype) {
+  switch (dtype) {
+    case MORPH_DTYPE_F32: return 4;
+    case MORPH_DTYPE_F16:
+    case MORPH_DTYPE_BF16: return 2;
+    default: return 0;
+  }
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+}  // namespace morph
+
+using namespace morph;
+
+extern "C" int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dtype,
+                                 int out_dtype, const morph_adamw_hp* hps, int n_hp,
+                                 const uint32_t* d_skip, void* stream) {
+  if (count < 0 || (count > 0 && (tensors == nullptr || hps == nullptr)) || n_hp < 0)
+    return MORPH_EINVAL;
+  const int gb = dtype_bytes(grad_dtype);
+  if (gb == 0) return MORPH_EDTYPE;
+  if (out_dtype != MORPH_DTYPE_NONE && dtype_bytes(out_dtype) == 0) return MORPH_EDTYPE;
+  const int ob = out_dtype == MORPH_DTYPE_NONE ? 0 : dtype_bytes(out_dtype);
+  // Validate everything before the first launch so an error enqueues nothing.
+  for (int i = 0; i < count; ++i) {
+    const morph_adamw_tensor& t = tensors[i];
+    if (t.numel < 0 || t.hp_index < 0 || t.hp_index >= n_hp) return MORPH_EINVAL;
+    if (t.numel > 0 && (t.grad == nullptr || t.param == nullptr || t.exp_avg == nullptr ||
+                        t.exp_avg_sq == nullptr))
+      return MORPH_EINVAL;
+  }
+  hipStream_t s = as_stream(stream);
+  LaunchArgs a;
+  int hp_src[kMaxHp];
+  int blocks = 0;
+  a.count = 0;
+  int n_local_hp = 0;
+  auto flush = [&]() -> int {
+    if (a.count == 0) return MORPH_OK;
+    const int rc = dispatch(grad_dtype, out_dtype, a, blocks, d_skip, s);
+    a.count = 0;
+    n_local_hp = 0;
+    blocks = 0;
+    return rc;
+  };
+  for (int i = 0; i < count; ++i) {
+    const morph_adamw_tensor& t = tensors[i];
+    void* out = (out_dtype == MORPH_DTYPE_NONE) ? nullptr : t.out;
+    for (int64_t off = 0; off < t.numel; off += kMaxSegment) {
+      const int64_t n = t.numel - off < kMaxSegment ? t.numel - off : kMaxSegment;
+      int local = -1;
+      for (int k = 0; k < n_local_hp; ++k)
+        if (hp_src[k] == t.hp_index) local = k;
+      if (a.count == kMaxTensors || (local < 0 && n_local_hp == kMaxHp)) {
+        const int rc = flush();
+        if (rc != MORPH_OK) return rc;
+        local = -1;
+      }
+      if (local < 0) {
+        local = n_local_hp++;
+        hp_src[local] = t.hp_index;
+        a.hp[local] = hps[t.hp_index];
+      }
+      TensorArg& d = a.t[a.count++];
+      d.grad = static_cast<const char*>(t.grad) + off * gb;
+      d.p = t.param + off;
+      d.m = t.exp_avg + off;
+      d.v = t.exp_avg_sq + off;
+      d.out = out ? static_cast<char*>(out) + off * ob : nullptr;
+      d.n = n;
+      d.hp = local;
+      d.first_block = blocks;
+      d.vector_ok = aligned(d.p, 16) && aligned(d.m, 16) && aligned(d.v, 16) &&
+                    aligned(d.grad, 4 * gb) && (d.out == nullptr || aligned(d.out, 4 * ob));
+      d.pad = 0;
+      blocks += (int)((n + kPerBlock - 1) / kPerBlock);
+    }
+  }
+  return flush();
+}
+
+extern "C" int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp_avg,
+                                 float* exp_avg_sq, void* out, int out_dtype, int64_t n,
+                                 const morph_adamw_hp* hp, const uint32_t* d_skip, void* stream) {
+  if (hp == nullptr) return MORPH_EINVAL;
+  morph_adamw_tensor t;
+  t.grad = grad;
+  t.param = param;
+  t.exp_avg = exp_avg;
+  t.exp_avg_sq = exp_avg_sq;
+  t.out = out;
+  t.numel = n;
+  t.hp_index = 0;
+  t.reserved = 0;
+  return morph_adamw_multi(&t, 1, grad_dtype, out_dtype, hp, 1, d_skip, stream);
+}

@@ -1,0 +1,127 @@
+"""Thin Python wrappers of the C ABI that take torch device tensors.
+
+Every function enqueues work on the current torch stream (or `stream`) and
+returns without synchronizing.  Shapes, devices, dtypes and contiguity are
+checked here so that the library only ever sees buffers that match what its
+kernels assume.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import AdamwTensor, check, dtype_code, lib, require_device_tensor, stream_handle
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def new_flag(device=None):
+    """A device uint32 flag (stored as int32; only 0/1 are written)."""
+    return torch.zeros(1, dtype=torch.int32, device=device or torch.cuda.current_device())
+
+
+def flag_clear(flag, stream=None):
+    require_device_tensor(flag, "flag")
+    check(lib().morph_flag_clear(_ptr(flag), stream_handle(stream)))
+
+
+def nonfinite_or(grads, flag, stream=None):
+    """OR into `flag` whether any element of any gradient is +-inf/NaN."""
+    require_device_tensor(flag, "flag")
+    by_dtype = {}
+    for i, g in enumerate(grads):
+        require_device_tensor(g, f"grads[{i}]")
+        by_dtype.setdefault(g.dtype, []).append(g)
+    for dtype, group in by_dtype.items():
+        ptrs = (ctypes.c_void_p * len(group))(*[g.data_ptr() for g in group])
+        sizes = (ctypes.c_int64 * len(group))(*[g.numel() for g in group])
+        check(lib().morph_nonfinite_or_multi(ptrs, sizes, len(group), dtype_code(dtype),
+                                             _ptr(flag), stream_handle(stream)))
+
+
+class AdamwBatch:
+    """A reusable ctypes descriptor array for one multi-tensor AdamW launch.
+
+    Building the descriptor array is the only per-call Python cost that grows
+    with the tensor count, so callers that step the same tensors repeatedly
+    keep one batch and only swap the constants.
+    """
+
+    def __init__(self, params, exp_avgs, exp_avg_sqs, grads, outs=None, hp_index=None):
+        n = len(params)
+        if not (len(exp_avgs) == len(exp_avg_sqs) == len(grads) == n):
+            raise ValueError("params, exp_avgs, exp_avg_sqs and grads must have equal length")
+        outs = list(outs) if outs is not None else [None] * n
+        hp_index = list(hp_index) if hp_index is not None else [0] * n
+        grad_dtypes = {g.dtype for g in grads}
+        if len(grad_dtypes) > 1:
+            raise ValueError(f"one launch takes one gradient dtype, got {grad_dtypes}")
+        out_dtypes = {o.dtype for o in outs if o is not None}
+        if len(out_dtypes) > 1:
+            raise ValueError(f"one launch takes one export dtype, got {out_dtypes}")
+        self.grad_dtype = dtype_code(next(iter(grad_dtypes))) if n else _lib.DTYPE_F32
+        self.out_dtype = dtype_code(next(iter(out_dtypes))) if out_dtypes else _lib.DTYPE_NONE
+        self.array = (AdamwTensor * max(n, 1))()
+        self.count = n
+        self.n_hp = (max(hp_index) + 1) if n else 1
+        keep = []
+        for i in range(n):
+            p, m, v, g, o = params[i], exp_avgs[i], exp_avg_sqs[i], grads[i], outs[i]
+            for name, t in (("param", p), ("exp_avg", m), ("exp_avg_sq", v), ("grad", g)):
+                require_device_tensor(t, f"{name}[{i}]")
+            for name, t in (("param", p), ("exp_avg", m), ("exp_avg_sq", v)):
+                if t.dtype != torch.float32:
+                    raise TypeError(f"{name}[{i}] must be float32, got {t.dtype}")
+            if not (m.numel() == v.numel() == g.numel() == p.numel()):
+                raise ValueError(f"tensor {i}: param/exp_avg/exp_avg_sq/grad sizes differ")
+            if not (p.device == m.device == v.device == g.device):
+                raise ValueError(f"tensor {i}: tensors on different devices")
+            if o is not None:
+                require_device_tensor(o, f"out[{i}]")
+                if o.numel() != p.numel() or o.device != p.device:
+                    raise ValueError(f"tensor {i}: export copy does not match param")
+            d = self.array[i]
+            d.grad, d.param, d.exp_avg, d.exp_avg_sq = (g.data_ptr(), p.data_ptr(),
+                                                        m.data_ptr(), v.data_ptr())
+            d.out = o.data_ptr() if o is not None else None
+            d.numel = p.numel()
+            d.hp_index = hp_index[i]
+            keep.append((p, m, v, g, o))
+        self._keep = keep  # the tensors must outlive the descriptors
+
+    def launch(self, hps, skip_flag=None, stream=None):
+        """Enqueue the step.  hps: sequence of AdamwHP, indexed by hp_index."""
+        if self.count == 0:
+            return
+        if len(hps) < self.n_hp:
+            raise ValueError(f"need {self.n_hp} constant sets, got {len(hps)}")
+        arr = (_lib.AdamwHP * len(hps))(*hps)
+        if skip_flag is not None:
+            require_device_tensor(skip_flag, "skip_flag")
+        check(lib().morph_adamw_multi(self.array, self.count, self.grad_dtype, self.out_dtype,
+                                      arr, len(hps), _ptr(skip_flag), stream_handle(stream)))
+
+
+def adamw_step(param, exp_avg, exp_avg_sq, grad, hp, out=None, skip_flag=None, stream=None):
+    """One fused AdamW step on one tensor (morph_adamw_fused)."""
+    for name, t in (("param", param), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq),
+                    ("grad", grad)):
+        require_device_tensor(t, name)
+    for name, t in (("param", param), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        if t.dtype != torch.float32:
+            raise TypeError(f"{name} must be float32")
+    n = param.numel()
+    if not (exp_avg.numel() == exp_avg_sq.numel() == grad.numel() == n):
+        raise ValueError("param/exp_avg/exp_avg_sq/grad sizes differ")
+    if out is not None:
+        require_device_tensor(out, "out")
+        if out.numel() != n:
+            raise ValueError("export copy size differs from param")
+    if skip_flag is not None:
+        require_device_tensor(skip_flag, "skip_flag")
+    check(lib().morph_adamw_fused(
+        _ptr(grad), dtype_code(grad.dtype), _ptr(param), _ptr(exp_avg), _ptr(exp_avg_sq),
+        _ptr(out), dtype_code(out.dtype) if out is not None else _lib.DTYPE_NONE, n,
+        ctypes.byref(hp), _ptr(skip_flag), stream_handle(stream)))

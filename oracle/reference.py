@@ -1,0 +1,279 @@
+"""CPU oracle for MORPH's mixed-precision optimizer step.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py import this module, and only as the checker or
+the timed CPU baseline.  The product package (morph_amd) never imports it.
+
+Contents, each restating the reference (paths relative to the MORPH repo):
+  * host constant computation -- torch/optim/adam.py:414-419, 528-547 and
+    streamtrain/disk.py:210-214;
+  * LossScale -- streamtrain/precision.py:6-17 (DynamicLossScale);
+  * adamw()/nonfinite_any()/f32_to_f16()/f32_to_bf16() -- ctypes bindings of
+    the C restatement in oracle/morph_oracle.c (element arithmetic);
+  * disk_update_torch() -- streamtrain/disk.py:203-216 run with torch CPU ops;
+  * orthogonalize_fp32()/muon_reference_step() -- streamtrain/optimizer.py:13-22,
+    52-61 in FP32 torch CPU.
+
+Pinning (tests/test_oracle_*.py): the C restatement is checked bit-exact
+against torch.optim.AdamW(foreach=False) and against disk_update_torch; both
+are checked against float64 closed forms of the first step; LossScale against
+the reference's known answers (tests/test_fp16.py:59-72); conversions against
+numpy/torch rounding; orthogonalize against the diagonal closed form of
+tests/test_training.py:50-64 and against invariants.
+"""
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+LIB_PATH = ROOT / "lib" / "libmorph_oracle.so"
+
+DTYPE_NONE, DTYPE_F32, DTYPE_F16, DTYPE_BF16 = -1, 0, 1, 2
+HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
+
+
+class HP(ctypes.Structure):
+    """Mirror of morph_adamw_hp (include/morph_optim.h)."""
+    _fields_ = [(name, ctypes.c_float) for name in (
+        "scale", "inv_scale", "clip", "decay", "lerp_weight", "beta2",
+        "one_minus_beta2", "bias_correction2_sqrt", "neg_step_size", "eps")] + [
+        ("flags", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+def f32(x):
+    """Round a Python float once to binary32, as torch does with a scalar operand."""
+    return float(np.float32(x))
+
+
+def _pow2(x):
+    mantissa, _ = math.frexp(x)
+    return x > 0 and mantissa == 0.5
+
+
+def _hp(scale, clip, decay, apply_decay, lerp_weight, beta2, one_minus_beta2,
+        bc2_sqrt, neg_step_size, eps):
+    flags = 0
+    if not _pow2(scale):
+        flags |= HP_DIVIDE_SCALE
+    if clip is not None:
+        flags |= HP_APPLY_CLIP
+    if apply_decay:
+        flags |= HP_APPLY_DECAY
+    if abs(lerp_weight) >= 0.5:
+        flags |= HP_LERP_LARGE
+    return HP(f32(scale), f32(1.0 / scale), f32(1.0 if clip is None else clip), f32(decay),
+              f32(lerp_weight), f32(beta2), f32(one_minus_beta2), f32(bc2_sqrt),
+              f32(neg_step_size), f32(eps), flags, 0)
+
+
+def torch_adamw_hp(lr, beta1, beta2, eps, weight_decay, step, scale=1.0, clip=None):
+    """Constants of torch's _single_tensor_adam for step `step` (1-based).
+
+    torch/optim/adam.py:414-419: p.mul_(1 - lr * weight_decay) when wd != 0;
+    457: exp_avg.lerp_(grad, 1 - beta1); 476: mul_(beta2).addcmul_(.., 1 - beta2);
+    528-547: bias_correction1 = 1 - beta1 ** step, step_size = lr / bc1,
+    bias_correction2_sqrt = (1 - beta2 ** step) ** 0.5,
+    denom = sqrt(v) / bc2_sqrt + eps, p.addcdiv_(m, denom, value=-step_size).
+    `step` is a float there (state_steps tensor .item()).
+    """
+    step = float(step)
+    bias_correction1 = 1 - beta1 ** step
+    bias_correction2 = 1 - beta2 ** step
+    step_size = lr / bias_correction1
+    bias_correction2_sqrt = bias_correction2 ** 0.5
+    return _hp(scale, clip, 1 - lr * weight_decay, weight_decay != 0, 1 - beta1, beta2,
+               1 - beta2, bias_correction2_sqrt, -step_size, eps)
+
+
+def disk_adamw_hp(step, lr, clip, scale=1.0):
+    """Constants of DiskState.update (streamtrain/disk.py:210-214).
+
+    g = gradient * clip; first.lerp_(g, .1); second.mul_(.999).addcmul_(g, g,
+    value=.001); denominator = sqrt(second) / math.sqrt(1 - .999**step) + 1e-8;
+    weight.mul_(1 - lr*.01).addcdiv_(first, denominator, value=-lr/(1 - .9**step)).
+    Decay is always applied there (wd .01 on every parameter).
+    """
+    return _hp(scale, clip, 1 - lr * .01, True, .1, .999, .001,
+               math.sqrt(1 - .999 ** step), -lr / (1 - .9 ** step), 1e-8)
+
+
+class LossScale:
+    """Restatement of DynamicLossScale (streamtrain/precision.py:6-17)."""
+
+    def __init__(self, scale=128., growth_interval=2000):
+        self.scale = float(scale)
+        self.good_steps = 0
+        self.growth_interval = growth_interval
+
+    def overflow(self):  # precision.py:9-11
+        if self.scale <= 1:
+            raise FloatingPointError('FP16 overflow at minimum loss scale; state unchanged')
+        self.scale = max(1., self.scale / 2)
+        self.good_steps = 0
+
+    def success(self):  # precision.py:12-14
+        self.good_steps += 1
+        if self.good_steps >= self.growth_interval:
+            self.scale = min(self.scale * 2, 65536.)
+            self.good_steps = 0
+
+    def state_dict(self):
+        return dict(scale=self.scale, good_steps=self.good_steps,
+                    growth_interval=self.growth_interval)
+
+
+# ---------------------------------------------------------------- C oracle --
+_lib = None
+
+
+def lib():
+    """Load (building first if needed) the C restatement."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        handle = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float
+        handle.oracle_adamw.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, i64,
+                                        ctypes.POINTER(HP)]
+        handle.oracle_adamw.restype = None
+        handle.oracle_nonfinite_any.argtypes = [vp, ctypes.c_int, i64]
+        handle.oracle_nonfinite_any.restype = ctypes.c_int
+        for name in ("oracle_f32_to_f16", "oracle_f32_to_bf16", "oracle_f16_to_f32"):
+            getattr(handle, name).argtypes = [vp, vp, i64]
+            getattr(handle, name).restype = None
+        handle.oracle_muon_momentum.argtypes = [vp, vp, vp, i64, f, f]
+        handle.oracle_muon_momentum.restype = None
+        handle.oracle_muon_apply.argtypes = [vp, vp, i64, f, f, f]
+        handle.oracle_muon_apply.restype = None
+        _lib = handle
+    return _lib
+
+
+def build():
+    """Compile oracle/morph_oracle.c with the committed Makefile."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", str(ROOT)], check=True)
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data) if a is not None else None
+
+
+def _dtype_code(a):
+    if a.dtype == np.float32:
+        return DTYPE_F32
+    if a.dtype == np.float16:
+        return DTYPE_F16
+    raise TypeError(f"unsupported array dtype {a.dtype}; pass bf16 as uint16 with dtype=DTYPE_BF16")
+
+
+def adamw(grad, w, m, v, hp, out_dtype=DTYPE_NONE, grad_dtype=None):
+    """One AdamW step in place on contiguous float32 arrays w/m/v.
+
+    grad: float32 / float16 array, or uint16 bit patterns with grad_dtype=DTYPE_BF16.
+    Returns the export copy (float16 array, uint16 bf16 bits, float32) or None.
+    """
+    for a in (w, m, v):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    grad = np.ascontiguousarray(grad)
+    if grad_dtype is None:
+        grad_dtype = _dtype_code(grad)
+    n = w.size
+    assert grad.size == n and m.size == n and v.size == n
+    out = None
+    if out_dtype == DTYPE_F16:
+        out = np.empty(n, np.float16)
+    elif out_dtype == DTYPE_BF16:
+        out = np.empty(n, np.uint16)
+    elif out_dtype == DTYPE_F32:
+        out = np.empty(n, np.float32)
+    lib().oracle_adamw(_ptr(grad), grad_dtype, _ptr(w), _ptr(m), _ptr(v), _ptr(out), out_dtype,
+                       n, ctypes.byref(hp))
+    return out
+
+
+def nonfinite_any(grad, dtype=None):
+    grad = np.ascontiguousarray(grad)
+    if dtype is None:
+        dtype = _dtype_code(grad)
+    return bool(lib().oracle_nonfinite_any(_ptr(grad), dtype, grad.size))
+
+
+def f32_to_f16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().oracle_f32_to_f16(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def f32_to_bf16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(x.shape, np.uint16)
+    lib().oracle_f32_to_bf16(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def muon_momentum(grad, momentum, mom_w=.05, nesterov_w=.95):
+    """In place on momentum; returns the Nesterov blend (optimizer.py:58-59)."""
+    u = np.empty_like(grad)
+    lib().oracle_muon_momentum(_ptr(grad), _ptr(momentum), _ptr(u), grad.size, mom_w, nesterov_w)
+    return u
+
+
+def muon_apply(p, update, scale, decay, neg_lr):
+    """In place on p: p = p*decay + (update*scale)*neg_lr (optimizer.py:60-61)."""
+    lib().oracle_muon_apply(_ptr(p), _ptr(update), p.size, scale, decay, neg_lr)
+
+
+# ------------------------------------------------ torch-CPU restatements --
+def disk_update_torch(state, gradient, step, lr, clip, chunk_elements=1048576, fault=None):
+    """DiskState.update's arithmetic on an in-RAM [3, N] float32 array.
+
+    Follows streamtrain/disk.py:207-216 op for op (torch CPU ops on chunk
+    copies, then a stacked write-back); `fault` is called after each partial
+    write as at disk.py:216.  No file I/O: the memmap is replaced by `state`.
+    """
+    import torch
+    size = state.shape[1]
+    flat = gradient.flatten()
+    for start in range(0, size, chunk_elements):
+        end = min(start + chunk_elements, size)
+        weight, first, second = [torch.from_numpy(state[i, start:end].copy()) for i in range(3)]
+        g = flat[start:end] * clip
+        first.lerp_(g, .1)
+        second.mul_(.999).addcmul_(g, g, value=.001)
+        denominator = second.sqrt().div_(math.sqrt(1 - .999 ** step)).add_(1e-8)
+        weight.mul_(1 - lr * .01).addcdiv_(first, denominator, value=-lr / (1 - .9 ** step))
+        state[:, start:end] = np.stack((weight.numpy(), first.numpy(), second.numpy()))
+        if fault is not None:
+            fault('partial_state_write')
+
+
+def orthogonalize_fp32(gradient, steps=5):
+    """streamtrain/optimizer.py:13-22 in FP32 (torch CPU or whatever device gradient is on)."""
+    x = gradient.float()
+    transpose = x.shape[0] > x.shape[1]
+    if transpose:
+        x = x.T
+    x = x / (x.norm() + 1e-7)
+    for _ in range(steps):
+        gram = x @ x.T
+        x = 3.4445 * x + (-4.775 * gram + 2.0315 * (gram @ gram)) @ x
+    return x.T if transpose else x
+
+
+def muon_reference_step(param, grad, momentum, lr, weight_decay):
+    """One Muon update of one matrix, streamtrain/optimizer.py:55-61, FP32 torch."""
+    momentum.lerp_(grad, .05)
+    update = orthogonalize_fp32(grad.lerp(momentum, .95))
+    update *= max(1, param.shape[0] / param.shape[1]) ** .5
+    param.mul_(1 - lr * weight_decay).add_(update, alpha=-lr)
+    return update
+
+
+def cpu_threads():
+    return len(os.sched_getaffinity(0))

@@ -1,0 +1,62 @@
+"""The C-ABI library loads and exports every symbol include/*.h declares (no GPU calls)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    names = []
+    for header in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(morph_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_the_expected_entry_points():
+    from morph_amd._lib import EXPORTS
+    assert set(declared_functions()) == set(EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    from morph_amd import _lib
+    lib = _lib.lib()  # loads; raises ImportError if not built
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_status_strings():
+    from morph_amd import _lib
+    lib = _lib.lib()
+    assert lib.morph_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.morph_strerror(0) == b"ok"
+    for code in (-1, -2, -3, -4, -5):
+        assert lib.morph_strerror(code) not in (b"ok", b"unknown morph status")
+    assert lib.morph_strerror(-99) == b"unknown morph status"
+
+
+def test_argument_validation_happens_before_any_launch():
+    """Invalid calls return a negative status and never reach the GPU."""
+    from morph_amd import _lib
+    lib = _lib.lib()
+    assert lib.morph_flag_clear(None, None) == -1
+    assert lib.morph_nonfinite_or(None, 1, 10, None, None) == -1
+    flag = ctypes.c_uint32(0)
+    assert lib.morph_nonfinite_or(None, 7, 0, ctypes.byref(flag), None) == -2
+    hp = _lib.AdamwHP()
+    assert lib.morph_adamw_fused(None, 1, None, None, None, None, -1, 10, ctypes.byref(hp),
+                                 None, None) == -1
+    assert lib.morph_adamw_fused(None, 9, None, None, None, None, -1, 0, ctypes.byref(hp),
+                                 None, None) == -2
+    assert lib.morph_adamw_multi(None, -1, 1, -1, None, 0, None, None) == -1
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from morph_amd import _lib
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(ImportError, match="no CPU fallback"):
+        _lib.lib()
