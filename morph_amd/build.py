@@ -5,7 +5,9 @@ Flags that matter for results:
                           exactly where torch's CPU kernels round, and fuse
                           only where __fmaf_rn says so;
   -packed-fp32-ops off    no packed FP32 instructions in device code.
-Division and square root stay IEEE correctly rounded (hipcc's default).
+  -fhip-fp32-correctly-rounded-divide-sqrt
+                          fp32 `/` and sqrt lower to IEEE correctly
+                          rounded sequences (hipcc's default, made explicit).
 """
 import os
 import subprocess
@@ -20,7 +22,7 @@ ARCH = os.environ.get("MORPH_OFFLOAD_ARCH", "gfx950")
 
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-    "-ffp-contract=off",
+    "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",
 ]

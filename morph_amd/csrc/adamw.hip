@@ -64,7 +64,7 @@ __device__ __forceinline__ void adamw_update(float g, float& p, float& m, float&
   const uint32_t fl = hp.flags;
   // Unscale: g / scale.  For scale = 2^k the product with 2^-k is the same
   // correctly rounded real number, so the cheaper multiply is bit-identical.
-  g = (fl & MORPH_HP_DIVIDE_SCALE) ? __fdiv_rn(g, hp.scale) : g * hp.inv_scale;
+  g = (fl & MORPH_HP_DIVIDE_SCALE) ? g / hp.scale : g * hp.inv_scale;
   if (fl & MORPH_HP_APPLY_CLIP) g = g * hp.clip;
   if (fl & MORPH_HP_APPLY_DECAY) p = p * hp.decay;
   if (fl & MORPH_HP_LERP_LARGE)
@@ -72,8 +72,8 @@ __device__ __forceinline__ void adamw_update(float g, float& p, float& m, float&
   else
     m = __fmaf_rn(hp.lerp_weight, g - m, m);
   v = __fmaf_rn(hp.one_minus_beta2 * g, g, v * hp.beta2);
-  const float d = __fdiv_rn(__fsqrt_rn(v), hp.bias_correction2_sqrt) + hp.eps;
-  p = p + __fdiv_rn(hp.neg_step_size * m, d);
+  const float d = __builtin_sqrtf(v) / hp.bias_correction2_sqrt + hp.eps;
+  p = p + (hp.neg_step_size * m) / d;
 }
 
 // ---- grad loads: 4 consecutive elements -----------------------------------

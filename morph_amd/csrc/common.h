@@ -2,8 +2,10 @@
 //
 // All arithmetic here must round exactly like torch's CPU kernels do, so the
 // library is compiled with -ffp-contract=off and every fused multiply-add is
-// written out with __fmaf_rn.  Division and square root use the correctly
-// rounded IEEE forms (__fdiv_rn / __fsqrt_rn).
+// written out with __fmaf_rn.  Division (`/`) and square root
+// (__builtin_sqrtf) lower to the correctly rounded IEEE sequences under
+// -fhip-fp32-correctly-rounded-divide-sqrt.  (__fsqrt_rn is NOT used: without
+// OCML_BASIC_ROUNDED_OPERATIONS clang maps it to the 1-ulp hardware sqrt.)
 #pragma once
 
 #include <hip/hip_runtime.h>
