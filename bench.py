@@ -4,10 +4,11 @@ python bench.py [--gpus 1] [--steps K] [--warmup W]
 
 A step is one optimizer step over the 5B-preset SwiGLU stage window
 (W_gate, W_up [6144, 3072] and W_down [3072, 6144]; N = 56,623,104 FP32
-masters): clear the overflow flag, run the non-finite detector over the FP16
-gradients, then the fused unscale + AdamW + FP16 export kernel, then read the
-skip decision and advance the loss scale and clocks.  Inputs are synthetic
-(seeded), resident in HBM before the timed region.
+masters): the non-finite detector over the FP16 gradients, the fused unscale +
+AdamW + FP16 export kernel, and the step close that applies the skip decision
+and advances the loss scale and the clocks -- all on the device, with no host
+round trip between steps.  Inputs are synthetic (seeded), resident in HBM
+before the timed region.
 
 Prints one JSON line.  `value` is whole-step throughput in Gparams/s;
 `roofline` is the fused AdamW kernel's algorithmic bandwidth (28 bytes per
@@ -58,8 +59,8 @@ def config3_embedding_grad(step_seed, rows=65536, cols=3072, tokens=4 * 1024, s=
 
 # --------------------------------------------------------------- timing --
 def time_gpu(steps, warmup):
+    """Steps are enqueued back to back (device-resident skip/scale/clock control)."""
     from morph_amd import DynamicLossScale, FusedAdamW
-    from morph_amd import kernels
 
     device = torch.device("cuda", 0)
     masters = config2_window(device)
@@ -67,38 +68,23 @@ def time_gpu(steps, warmup):
     n = sum(p.numel() for p in masters)
     scaler = DynamicLossScale(LOSS_SCALE, growth_interval=2000)
     opt = FusedAdamW(masters, **HYPER, loss_scale=scaler, export_dtype=torch.float16)
-    stream = torch.cuda.current_stream(device)
-
-    # Events around the AdamW launch only (same stream, so they bracket that kernel).
-    orig_launch = kernels.AdamwBatch.launch
-    kernel_events = []
-
-    def timed_launch(self, hps, skip_flag=None, stream=None):
-        s = stream or torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(s)
-        orig_launch(self, hps, skip_flag, stream)
-        e1.record(s)
-        kernel_events.append((e0, e1))
-
     for _ in range(warmup):
-        assert opt.step(grads)
+        opt.step(grads)
+    opt.resolve()
+    opt.kernel_timer = []
     torch.cuda.synchronize()
-    kernels.AdamwBatch.launch = timed_launch
-    try:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            applied = opt.step(grads)
-            assert applied
-        torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-    finally:
-        kernels.AdamwBatch.launch = orig_launch
-    kernel_ms = [a.elapsed_time(b) for a, b in kernel_events]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step(grads)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    opt.resolve()
+    if opt.skipped_steps:
+        raise RuntimeError(f"{opt.skipped_steps} steps skipped on synthetic finite gradients")
+    kernel_ms = [a.elapsed_time(b) for a, b in opt.kernel_timer]
     avg_kernel_s = sum(kernel_ms) / len(kernel_ms) / 1e3
     return dict(n=n, elapsed=elapsed, avg_kernel_s=avg_kernel_s, kernel_ms=kernel_ms,
-                scale=scaler.scale, stream=stream)
+                scale=scaler.scale, applied=opt.applied_steps)
 
 
 def cpu_baseline(seconds=10.0):
@@ -179,7 +165,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None,
-                     "kernel": "adamw_multi_kernel<F16,F16>",
+                     "kernel": "adamw_multi_kernel<F16,F16,dev>",
                      "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
                      "bytes_per_launch": BYTES_PER_PARAM * n},
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),

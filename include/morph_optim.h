@@ -101,8 +101,53 @@ typedef struct morph_adamw_tensor {
   void* out;          /* out_dtype export copy, or NULL */
   int64_t numel;
   int32_t hp_index;   /* index into the hps[] array of the call */
-  int32_t reserved;
+  int32_t clock_index; /* morph_adamw_multi_dev: index of this tensor's clock */
 } morph_adamw_tensor;
+
+/*
+ * Device-resident step control, for steps enqueued without a host round trip.
+ * Lives in device memory; the host initialises it once (a plain copy) and
+ * reads it back only when it wants the outcome.
+ *
+ * scale/good_steps/growth_interval/scale_cap are DynamicLossScale's state
+ * (streamtrain/precision.py:6-17) kept in double precision, so the device
+ * sequence of scales is bit-identical to the host one.  found_inf is the
+ * detector's output for the step in flight.  fatal is sticky: bit 0 = an
+ * overflow happened at scale <= 1 (the reference raises FloatingPointError
+ * there).  While fatal is set every later step is a no-op, so the state the
+ * host finds equals the reference's state at the point it would have raised.
+ */
+typedef struct morph_step_state {
+  double scale;
+  double scale_cap;
+  int64_t good_steps;
+  int64_t growth_interval;
+  int64_t applied;        /* steps applied */
+  int64_t skipped;        /* steps skipped on overflow */
+  uint32_t found_inf;     /* written by the detector, consumed by morph_step_end */
+  uint32_t fatal;
+  uint32_t last_found_inf;
+  uint32_t dynamic;       /* 1: DynamicLossScale state machine; 0: fixed scale */
+} morph_step_state;
+
+#define MORPH_FATAL_MIN_SCALE 1u
+
+/*
+ * Per-constant-set schedule for morph_adamw_multi_dev.  The step-dependent
+ * constants are looked up by the tensor's device clock t (1-based after the
+ * increment):  neg_step_size = -(lr / bias_correction1[t-1]) in double, then
+ * rounded to fp32 (adam.py:537-539 / disk.py:214); bias_correction2_sqrt =
+ * bias_correction2_sqrt[t-1] (already fp32).  The tables are filled by the
+ * host with the reference's own double expressions (1 - beta1 ** t, ...).
+ * The host keeps every clock below table_len; a tensor whose clock is out of
+ * range is left untouched by the kernel (no out-of-bounds table read).
+ */
+typedef struct morph_adamw_sched {
+  double lr;
+  const double* bias_correction1;      /* device, table_len entries */
+  const float* bias_correction2_sqrt;  /* device, table_len entries */
+  int64_t table_len;
+} morph_adamw_sched;
 
 int morph_abi_version(void);
 const char* morph_strerror(int status);
@@ -147,6 +192,30 @@ int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp
 int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dtype,
                       int out_dtype, const morph_adamw_hp* hps, int n_hp,
                       const uint32_t* d_skip, void* stream);
+
+/*
+ * Device-resident form of morph_adamw_multi.  Each tensor's step t is
+ * d_clocks[clock_index] + 1; the unscale factor comes from d_state->scale; the
+ * step is skipped when d_state->found_inf or d_state->fatal is set.  From
+ * hps[] only the step-independent fields are used (clip, decay, lerp_weight,
+ * beta2, one_minus_beta2, eps, flags minus MORPH_HP_DIVIDE_SCALE); scheds[]
+ * parallels hps[].  Clocks are NOT advanced here: morph_step_end does that.
+ */
+int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad_dtype,
+                          int out_dtype, const morph_adamw_hp* hps,
+                          const morph_adamw_sched* scheds, int n_hp, const int64_t* d_clocks,
+                          const morph_step_state* d_state, void* stream);
+
+/*
+ * Closes a device-resident step (one workgroup): on overflow counts a skip and,
+ * when `dynamic`, applies DynamicLossScale.overflow (or sets fatal bit 0 at
+ * scale <= 1); else counts the step, applies success() when `dynamic`, and
+ * advances the clocks d_clocks[d_clock_list[0..n)] (indices must be distinct).
+ * Then records found_inf in last_found_inf and clears found_inf.  No-op while
+ * fatal is set.
+ */
+int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* d_clock_list,
+                   int n, void* stream);
 
 #ifdef __cplusplus
 }

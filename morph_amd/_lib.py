@@ -22,7 +22,9 @@ HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
 EXPORTS = (
     "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
+    "morph_adamw_multi_dev", "morph_step_end",
 )
+FATAL_MIN_SCALE = 1
 
 
 class MorphError(RuntimeError):
@@ -42,7 +44,22 @@ class AdamwTensor(ctypes.Structure):
     _fields_ = [("grad", ctypes.c_void_p), ("param", ctypes.c_void_p),
                 ("exp_avg", ctypes.c_void_p), ("exp_avg_sq", ctypes.c_void_p),
                 ("out", ctypes.c_void_p), ("numel", ctypes.c_int64),
-                ("hp_index", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                ("hp_index", ctypes.c_int32), ("clock_index", ctypes.c_int32)]
+
+
+class StepState(ctypes.Structure):
+    """morph_step_state (device-resident step control, 64 bytes)."""
+    _fields_ = [("scale", ctypes.c_double), ("scale_cap", ctypes.c_double),
+                ("good_steps", ctypes.c_int64), ("growth_interval", ctypes.c_int64),
+                ("applied", ctypes.c_int64), ("skipped", ctypes.c_int64),
+                ("found_inf", ctypes.c_uint32), ("fatal", ctypes.c_uint32),
+                ("last_found_inf", ctypes.c_uint32), ("dynamic", ctypes.c_uint32)]
+
+
+class AdamwSched(ctypes.Structure):
+    """morph_adamw_sched."""
+    _fields_ = [("lr", ctypes.c_double), ("bias_correction1", ctypes.c_void_p),
+                ("bias_correction2_sqrt", ctypes.c_void_p), ("table_len", ctypes.c_int64)]
 
 
 _lib = None
@@ -68,6 +85,10 @@ def lib():
                                    vp, vp], i32),
             "morph_adamw_multi": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
                                    ctypes.POINTER(AdamwHP), i32, vp, vp], i32),
+            "morph_adamw_multi_dev": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
+                                       ctypes.POINTER(AdamwHP), ctypes.POINTER(AdamwSched), i32,
+                                       vp, vp, vp], i32),
+            "morph_step_end": ([vp, vp, vp, i32, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(handle, name)

@@ -1,0 +1,117 @@
+"""Device-resident step control: loss-scale state, step clocks, bias-correction tables.
+
+With these in HBM the optimizer step needs no host round trip: the detector
+writes found_inf into the state block, the AdamW kernel reads the scale, the
+skip decision and each tensor's clock from it, and morph_step_end advances the
+loss scale and the clocks.  The host mirrors (DynamicLossScale, per-tensor
+step counts) are refreshed only when the caller asks (resolve()).
+"""
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from ._lib import FATAL_MIN_SCALE, AdamwSched, StepState
+from .hyper import to_f32
+from .precision import DynamicLossScale
+
+STATE_BYTES = ctypes.sizeof(StepState)
+FOUND_INF_OFFSET = StepState.found_inf.offset
+
+
+class BiasTables:
+    """bias_correction1[t-1] = 1 - beta1 ** t (double) and
+    bias_correction2_sqrt[t-1] = fp32((1 - beta2 ** t) ** 0.5) for t = 1..len,
+    evaluated with Python floats exactly as torch/optim/adam.py:528-539 does
+    (step is a float there).  Grown by doubling; the old tables stay alive until
+    replaced, and torch's stream-ordered allocator keeps them valid for kernels
+    already enqueued."""
+
+    def __init__(self, beta1, beta2, device, length=4096):
+        self.beta1, self.beta2, self.device = float(beta1), float(beta2), device
+        self.length = 0
+        self.bc1 = self.bc2s = None
+        self.ensure(length)
+
+    def ensure(self, t_max):
+        if t_max <= self.length:
+            return
+        length = max(4096, self.length)
+        while length < t_max:
+            length *= 2
+        b1, b2 = self.beta1, self.beta2
+        bc1 = np.empty(length, np.float64)
+        bc2s = np.empty(length, np.float32)
+        for i in range(length):
+            t = float(i + 1)
+            bc1[i] = 1 - b1 ** t
+            bc2s[i] = to_f32((1 - b2 ** t) ** 0.5)
+        self.bc1 = torch.from_numpy(bc1).to(self.device)
+        self.bc2s = torch.from_numpy(bc2s).to(self.device)
+        self.length = length
+
+    def sched(self, lr):
+        return AdamwSched(float(lr), self.bc1.data_ptr(), self.bc2s.data_ptr(), self.length)
+
+
+class StepControl:
+    """The morph_step_state block and the clocks of one optimizer, on `device`."""
+
+    def __init__(self, device, n_clocks, loss_scale=None):
+        self.device = device
+        self.state = torch.zeros(STATE_BYTES, dtype=torch.uint8, device=device)
+        self.clocks = torch.zeros(max(n_clocks, 1), dtype=torch.int64, device=device)
+        self._host = torch.empty(STATE_BYTES, dtype=torch.uint8, pin_memory=True)
+        self.loss_scale = loss_scale
+        self._initialized = False
+        self.push_scale()
+
+    @property
+    def found_inf_ptr(self):
+        return self.state.data_ptr() + FOUND_INF_OFFSET
+
+    def _scale_fields(self):
+        s = self.loss_scale
+        if isinstance(s, DynamicLossScale) or (hasattr(s, "overflow") and hasattr(s, "success")):
+            return float(s.scale), int(s.good_steps), int(s.growth_interval), 1
+        scale = 1.0 if s is None else float(s)
+        if not (scale > 0 and math.isfinite(scale)):
+            raise ValueError(f"loss scale must be positive and finite, got {scale}")
+        return scale, 0, 1 << 62, 0
+
+    def push_scale(self):
+        """Write the host scaler's state into the device block (keeps counters)."""
+        current = self.read() if self._initialized else StepState()
+        self._initialized = True
+        scale, good, interval, dynamic = self._scale_fields()
+        current.scale, current.good_steps, current.growth_interval = scale, good, interval
+        current.scale_cap = DynamicLossScale.CAP if dynamic else scale
+        current.dynamic = dynamic
+        blob = bytes(current)
+        self.state.copy_(torch.frombuffer(bytearray(blob), dtype=torch.uint8))
+        self._mirrored = (scale, good, interval)
+
+    def scaler_changed(self):
+        return self._scale_fields()[:3] != self._mirrored
+
+    def read(self):
+        """Synchronously copy the state block to the host."""
+        self._host.copy_(self.state)
+        return StepState.from_buffer_copy(self._host.numpy().tobytes())
+
+    def mirror(self, st):
+        """Refresh the host DynamicLossScale from a state read back from the device."""
+        s = self.loss_scale
+        if st.dynamic:
+            s.scale = st.scale
+            s.good_steps = int(st.good_steps)
+        self._mirrored = (st.scale if st.dynamic else self._mirrored[0],
+                          int(st.good_steps) if st.dynamic else self._mirrored[1],
+                          self._mirrored[2])
+
+    @staticmethod
+    def fatal_error(st):
+        if st.fatal & FATAL_MIN_SCALE:
+            return FloatingPointError('FP16 overflow at minimum loss scale; state unchanged')
+        return None

@@ -9,19 +9,29 @@
 // op; the host supplies each fp32 constant already rounded (morph_adamw_hp).
 //
 // Layout and launch shape.  A launch covers up to kMaxTensors tensors.  Each
-// workgroup (256 lanes = 4 wave64) owns one contiguous chunk of kPerBlock
-// elements of one tensor; lane i of the group moves 4 consecutive elements per
-// access (one 128-bit load of each FP32 stream, one 64-bit load of a 16-bit
-// grad), and consecutive lanes cover consecutive 16-byte pieces, so every
-// wave-wide access is one contiguous 1 KiB (FP32) or 512 B (16-bit) segment.
-// kUnroll accesses per lane are issued before any arithmetic so each lane
-// keeps several 128-bit loads in flight.  Chunks map to workgroups in address
-// order; the dispatcher spreads consecutive workgroups round-robin over the 8
-// XCDs, which is what a pure stream with no reuse wants.
+// workgroup (kBlock lanes) owns one contiguous chunk of kPerBlock elements of
+// one tensor; lane i moves 4 consecutive elements per access (one 128-bit load
+// of each FP32 stream, one 64-bit load of a 16-bit grad), and consecutive
+// lanes cover consecutive 16-byte pieces, so every wave-wide access is one
+// contiguous 1 KiB (FP32) or 512 B (16-bit) segment.  All loads of a lane are
+// issued before any arithmetic.  Measured on MI355X (config 2 window), small
+// workgroups with one access per lane (128 x 1) stream best: many short-lived
+// workgroups keep every CU's memory pipeline full, while longer per-lane
+// chains (unroll 4/8) or 1024-lane groups lose 3-7%.  Chunks map to workgroups
+// in address order; the dispatcher spreads consecutive workgroups round-robin
+// over the 8 XCDs, which is what a pure stream with no reuse wants.
+//
+// Two launch forms share the kernel: host constants (morph_adamw_multi), and
+// device-resident control (morph_adamw_multi_dev) where the loss scale, the
+// skip decision and each tensor's step clock are read from HBM, so a training
+// loop can enqueue steps without waiting for the previous outcome.
 #include "common.h"
 
 #ifndef MORPH_ADAMW_UNROLL
-#define MORPH_ADAMW_UNROLL 4
+#define MORPH_ADAMW_UNROLL 1
+#endif
+#ifndef MORPH_ADAMW_BLOCK
+#define MORPH_ADAMW_BLOCK 128
 #endif
 #ifndef MORPH_ADAMW_NT
 #define MORPH_ADAMW_NT 1
@@ -30,7 +40,7 @@
 namespace morph {
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = MORPH_ADAMW_BLOCK;
 constexpr int kUnroll = MORPH_ADAMW_UNROLL;
 constexpr bool kNT = MORPH_ADAMW_NT != 0;
 constexpr int kPerBlock = kBlock * 4 * kUnroll;
@@ -50,14 +60,24 @@ struct TensorArg {
   int32_t hp;
   int32_t first_block;
   int32_t vector_ok;
-  int32_t pad;
+  int32_t clock;
 };
 
 struct LaunchArgs {
   TensorArg t[kMaxTensors];
   morph_adamw_hp hp[kMaxHp];
+  morph_adamw_sched sched[kMaxHp];  // device form only
+  const int64_t* clocks;            // device form only
+  const morph_step_state* state;    // device form only
   int32_t count;
 };
+
+// Power of two (normal double): zero fraction field, finite, positive.
+__device__ __forceinline__ bool pow2_double(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint32_t e = (uint32_t)(b >> 52) & 0x7FFu;
+  return (b >> 63) == 0 && e != 0 && e != 0x7FFu && (b & 0x000FFFFFFFFFFFFFull) == 0;
+}
 
 __device__ __forceinline__ void adamw_update(float g, float& p, float& m, float& v,
                                              const morph_adamw_hp& hp) {
@@ -176,16 +196,32 @@ __device__ __forceinline__ void chunk_scalar(const TensorArg& T, const morph_ada
   }
 }
 
-template <typename GT, typename OT>
+template <typename GT, typename OT, bool kDev>
 __global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const LaunchArgs a,
                                                              const uint32_t* __restrict__ skip) {
   // Conditional skip: a flagged (overflowed) step leaves every byte untouched.
-  if (skip != nullptr && *skip != 0u) return;
+  if constexpr (kDev) {
+    if ((a.state->found_inf | a.state->fatal) != 0u) return;
+  } else {
+    if (skip != nullptr && *skip != 0u) return;
+  }
   const int b = blockIdx.x;
   int ti = 0;
   while (ti + 1 < a.count && a.t[ti + 1].first_block <= b) ++ti;
   const TensorArg& T = a.t[ti];
-  const morph_adamw_hp& hp = a.hp[T.hp];
+  morph_adamw_hp hp = a.hp[T.hp];
+  if constexpr (kDev) {
+    // Step-dependent constants from device state, in the host's double arithmetic.
+    const morph_adamw_sched& S = a.sched[T.hp];
+    const int64_t t = a.clocks[T.clock] + 1;
+    if (t < 1 || t > S.table_len) return;  // host keeps clocks inside the tables
+    const double scale = a.state->scale;
+    hp.scale = (float)scale;
+    hp.inv_scale = (float)(1.0 / scale);
+    hp.flags = (hp.flags & ~MORPH_HP_DIVIDE_SCALE) | (pow2_double(scale) ? 0u : MORPH_HP_DIVIDE_SCALE);
+    hp.bias_correction2_sqrt = S.bias_correction2_sqrt[t - 1];
+    hp.neg_step_size = (float)(-(S.lr / S.bias_correction1[t - 1]));
+  }
   const int64_t base = (int64_t)(b - T.first_block) * kPerBlock;
   if (T.vector_ok && base + kPerBlock <= T.n)
     chunk_vector<GT, OT>(T, hp, base);
@@ -194,29 +230,34 @@ __global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const LaunchArgs a,
 }
 
 template <typename GT, typename OT>
-int launch(const LaunchArgs& a, int blocks, const uint32_t* skip, hipStream_t s) {
-  hipLaunchKernelGGL((adamw_multi_kernel<GT, OT>), dim3(blocks), dim3(kBlock), 0, s, a, skip);
+int launch(bool dev, const LaunchArgs& a, int blocks, const uint32_t* skip, hipStream_t s) {
+  if (dev)
+    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, true>), dim3(blocks), dim3(kBlock), 0, s, a,
+                       skip);
+  else
+    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, false>), dim3(blocks), dim3(kBlock), 0, s, a,
+                       skip);
   return launch_status();
 }
 
 template <typename GT>
-int launch_out(int out_dtype, const LaunchArgs& a, int blocks, const uint32_t* skip,
+int launch_out(bool dev, int out_dtype, const LaunchArgs& a, int blocks, const uint32_t* skip,
                hipStream_t s) {
   switch (out_dtype) {
-    case MORPH_DTYPE_NONE: return launch<GT, NoOut>(a, blocks, skip, s);
-    case MORPH_DTYPE_F32: return launch<GT, F32>(a, blocks, skip, s);
-    case MORPH_DTYPE_F16: return launch<GT, F16>(a, blocks, skip, s);
-    case MORPH_DTYPE_BF16: return launch<GT, BF16>(a, blocks, skip, s);
+    case MORPH_DTYPE_NONE: return launch<GT, NoOut>(dev, a, blocks, skip, s);
+    case MORPH_DTYPE_F32: return launch<GT, F32>(dev, a, blocks, skip, s);
+    case MORPH_DTYPE_F16: return launch<GT, F16>(dev, a, blocks, skip, s);
+    case MORPH_DTYPE_BF16: return launch<GT, BF16>(dev, a, blocks, skip, s);
     default: return MORPH_EDTYPE;
   }
 }
 
-int dispatch(int grad_dtype, int out_dtype, const LaunchArgs& a, int blocks,
+int dispatch(bool dev, int grad_dtype, int out_dtype, const LaunchArgs& a, int blocks,
              const uint32_t* skip, hipStream_t s) {
   switch (grad_dtype) {
-    case MORPH_DTYPE_F32: return launch_out<F32>(out_dtype, a, blocks, skip, s);
-    case MORPH_DTYPE_F16: return launch_out<F16>(out_dtype, a, blocks, skip, s);
-    case MORPH_DTYPE_BF16: return launch_out<BF16>(out_dtype, a, blocks, skip, s);
+    case MORPH_DTYPE_F32: return launch_out<F32>(dev, out_dtype, a, blocks, skip, s);
+    case MORPH_DTYPE_F16: return launch_out<F16>(dev, out_dtype, a, blocks, skip, s);
+    case MORPH_DTYPE_BF16: return launch_out<BF16>(dev, out_dtype, a, blocks, skip, s);
     default: return MORPH_EDTYPE;
   }
 }
@@ -232,37 +273,45 @@ int dtype_bytes(int dtype) {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-}  // namespace
-}  // namespace morph
-
-using namespace morph;
-
-extern "C" int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dtype,
-                                 int out_dtype, const morph_adamw_hp* hps, int n_hp,
-                                 const uint32_t* d_skip, void* stream) {
+// Validates everything, then splits the tensor list into launches of at most
+// kMaxTensors segments and kMaxHp constant sets.  `scheds`, `clocks` and
+// `state` are non-null exactly for the device-resident form.
+int enqueue(const morph_adamw_tensor* tensors, int count, int grad_dtype, int out_dtype,
+            const morph_adamw_hp* hps, const morph_adamw_sched* scheds, int n_hp,
+            const int64_t* clocks, const morph_step_state* state, const uint32_t* d_skip,
+            void* stream) {
+  const bool dev = state != nullptr;
   if (count < 0 || (count > 0 && (tensors == nullptr || hps == nullptr)) || n_hp < 0)
     return MORPH_EINVAL;
+  if (dev && (scheds == nullptr || clocks == nullptr)) return MORPH_EINVAL;
   const int gb = dtype_bytes(grad_dtype);
   if (gb == 0) return MORPH_EDTYPE;
   if (out_dtype != MORPH_DTYPE_NONE && dtype_bytes(out_dtype) == 0) return MORPH_EDTYPE;
   const int ob = out_dtype == MORPH_DTYPE_NONE ? 0 : dtype_bytes(out_dtype);
-  // Validate everything before the first launch so an error enqueues nothing.
   for (int i = 0; i < count; ++i) {
     const morph_adamw_tensor& t = tensors[i];
     if (t.numel < 0 || t.hp_index < 0 || t.hp_index >= n_hp) return MORPH_EINVAL;
     if (t.numel > 0 && (t.grad == nullptr || t.param == nullptr || t.exp_avg == nullptr ||
                         t.exp_avg_sq == nullptr))
       return MORPH_EINVAL;
+    if (dev && t.clock_index < 0) return MORPH_EINVAL;
   }
+  if (dev)
+    for (int k = 0; k < n_hp; ++k)
+      if (scheds[k].table_len < 1 || scheds[k].bias_correction1 == nullptr ||
+          scheds[k].bias_correction2_sqrt == nullptr)
+        return MORPH_EINVAL;
   hipStream_t s = as_stream(stream);
   LaunchArgs a;
+  a.clocks = clocks;
+  a.state = state;
   int hp_src[kMaxHp];
   int blocks = 0;
   a.count = 0;
   int n_local_hp = 0;
   auto flush = [&]() -> int {
     if (a.count == 0) return MORPH_OK;
-    const int rc = dispatch(grad_dtype, out_dtype, a, blocks, d_skip, s);
+    const int rc = dispatch(dev, grad_dtype, out_dtype, a, blocks, d_skip, s);
     a.count = 0;
     n_local_hp = 0;
     blocks = 0;
@@ -285,6 +334,7 @@ extern "C" int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, i
         local = n_local_hp++;
         hp_src[local] = t.hp_index;
         a.hp[local] = hps[t.hp_index];
+        if (dev) a.sched[local] = scheds[t.hp_index];
       }
       TensorArg& d = a.t[a.count++];
       d.grad = static_cast<const char*>(t.grad) + off * gb;
@@ -297,11 +347,33 @@ extern "C" int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, i
       d.first_block = blocks;
       d.vector_ok = aligned(d.p, 16) && aligned(d.m, 16) && aligned(d.v, 16) &&
                     aligned(d.grad, 4 * gb) && (d.out == nullptr || aligned(d.out, 4 * ob));
-      d.pad = 0;
+      d.clock = dev ? t.clock_index : 0;
       blocks += (int)((n + kPerBlock - 1) / kPerBlock);
     }
   }
   return flush();
+}
+
+}  // namespace
+}  // namespace morph
+
+using namespace morph;
+
+extern "C" int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dtype,
+                                 int out_dtype, const morph_adamw_hp* hps, int n_hp,
+                                 const uint32_t* d_skip, void* stream) {
+  return enqueue(tensors, count, grad_dtype, out_dtype, hps, nullptr, n_hp, nullptr, nullptr,
+                 d_skip, stream);
+}
+
+extern "C" int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad_dtype,
+                                     int out_dtype, const morph_adamw_hp* hps,
+                                     const morph_adamw_sched* scheds, int n_hp,
+                                     const int64_t* d_clocks, const morph_step_state* d_state,
+                                     void* stream) {
+  if (d_state == nullptr) return MORPH_EINVAL;
+  return enqueue(tensors, count, grad_dtype, out_dtype, hps, scheds, n_hp, d_clocks, d_state,
+                 nullptr, stream);
 }
 
 extern "C" int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp_avg,
@@ -316,6 +388,6 @@ extern "C" int morph_adamw_fused(const void* grad, int grad_dtype, float* param,
   t.out = out;
   t.numel = n;
   t.hp_index = 0;
-  t.reserved = 0;
+  t.clock_index = 0;
   return morph_adamw_multi(&t, 1, grad_dtype, out_dtype, hp, 1, d_skip, stream);
 }

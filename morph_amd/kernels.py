@@ -28,8 +28,15 @@ def flag_clear(flag, stream=None):
 
 
 def nonfinite_or(grads, flag, stream=None):
-    """OR into `flag` whether any element of any gradient is +-inf/NaN."""
-    require_device_tensor(flag, "flag")
+    """OR into `flag` whether any element of any gradient is +-inf/NaN.
+
+    flag: a device int32 tensor, or a raw device address (int) of a uint32.
+    """
+    if isinstance(flag, int):
+        flag_ptr = ctypes.c_void_p(flag)
+    else:
+        require_device_tensor(flag, "flag")
+        flag_ptr = _ptr(flag)
     by_dtype = {}
     for i, g in enumerate(grads):
         require_device_tensor(g, f"grads[{i}]")
@@ -38,7 +45,7 @@ def nonfinite_or(grads, flag, stream=None):
         ptrs = (ctypes.c_void_p * len(group))(*[g.data_ptr() for g in group])
         sizes = (ctypes.c_int64 * len(group))(*[g.numel() for g in group])
         check(lib().morph_nonfinite_or_multi(ptrs, sizes, len(group), dtype_code(dtype),
-                                             _ptr(flag), stream_handle(stream)))
+                                             flag_ptr, stream_handle(stream)))
 
 
 class AdamwBatch:
@@ -49,12 +56,14 @@ class AdamwBatch:
     keep one batch and only swap the constants.
     """
 
-    def __init__(self, params, exp_avgs, exp_avg_sqs, grads, outs=None, hp_index=None):
+    def __init__(self, params, exp_avgs, exp_avg_sqs, grads, outs=None, hp_index=None,
+                 clock_index=None):
         n = len(params)
         if not (len(exp_avgs) == len(exp_avg_sqs) == len(grads) == n):
             raise ValueError("params, exp_avgs, exp_avg_sqs and grads must have equal length")
         outs = list(outs) if outs is not None else [None] * n
         hp_index = list(hp_index) if hp_index is not None else [0] * n
+        clock_index = list(clock_index) if clock_index is not None else list(range(n))
         grad_dtypes = {g.dtype for g in grads}
         if len(grad_dtypes) > 1:
             raise ValueError(f"one launch takes one gradient dtype, got {grad_dtypes}")
@@ -88,6 +97,7 @@ class AdamwBatch:
             d.out = o.data_ptr() if o is not None else None
             d.numel = p.numel()
             d.hp_index = hp_index[i]
+            d.clock_index = clock_index[i]
             keep.append((p, m, v, g, o))
         self._keep = keep  # the tensors must outlive the descriptors
 
@@ -102,6 +112,38 @@ class AdamwBatch:
             require_device_tensor(skip_flag, "skip_flag")
         check(lib().morph_adamw_multi(self.array, self.count, self.grad_dtype, self.out_dtype,
                                       arr, len(hps), _ptr(skip_flag), stream_handle(stream)))
+
+
+    def launch_dev(self, hps, scheds, clocks, state, stream=None):
+        """Enqueue the device-resident form (morph_adamw_multi_dev).
+
+        scheds: AdamwSched per constant set; clocks: device int64 tensor;
+        state: device tensor holding a morph_step_state.
+        """
+        if self.count == 0:
+            return
+        if len(hps) < self.n_hp or len(scheds) != len(hps):
+            raise ValueError("need one constant set and one schedule per hp index")
+        require_device_tensor(clocks, "clocks")
+        require_device_tensor(state, "state")
+        if clocks.dtype != torch.int64 or state.numel() * state.element_size() < 64:
+            raise ValueError("clocks must be int64 and state must hold a morph_step_state")
+        harr = (_lib.AdamwHP * len(hps))(*hps)
+        sarr = (_lib.AdamwSched * len(scheds))(*scheds)
+        check(lib().morph_adamw_multi_dev(self.array, self.count, self.grad_dtype,
+                                          self.out_dtype, harr, sarr, len(hps), _ptr(clocks),
+                                          _ptr(state), stream_handle(stream)))
+
+
+def step_end(state, clocks, clock_list, stream=None):
+    """Enqueue morph_step_end (clock_list: device int32 tensor of distinct indices)."""
+    require_device_tensor(state, "state")
+    require_device_tensor(clocks, "clocks")
+    require_device_tensor(clock_list, "clock_list")
+    if clock_list.dtype != torch.int32 or clocks.dtype != torch.int64:
+        raise TypeError("clock_list must be int32 and clocks int64")
+    check(lib().morph_step_end(_ptr(state), _ptr(clocks), _ptr(clock_list), clock_list.numel(),
+                               stream_handle(stream)))
 
 
 def adamw_step(param, exp_avg, exp_avg_sq, grad, hp, out=None, skip_flag=None, stream=None):

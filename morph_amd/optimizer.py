@@ -9,12 +9,18 @@ streamtrain/disk.py:447 / sparse_disk.py:107, with the non-finite decision of
 optimizer.py:49-51 driving a conditional skip and DynamicLossScale
 (precision.py:6-17).  Parameters whose gradient is None are not touched and
 their step clock does not advance (sparse_disk.py:1-5, torch's own rule).
+
+A step is three kernels on the caller's stream -- detector, fused AdamW,
+step close -- driven by device-resident state (morph_amd.control), so no step
+waits for the host.  The host copies of the clocks and of the loss scale are
+refreshed by resolve(); with sync=True (or on_overflow="raise") every step
+resolves and reports its outcome like the reference does.
 """
 import torch
 
 from . import kernels
+from .control import BiasTables, StepControl
 from .hyper import adamw_constants
-from .precision import DynamicLossScale
 
 _OVERFLOW_POLICIES = ("skip", "raise")
 
@@ -38,17 +44,19 @@ class FusedAdamW:
     """torch.optim.AdamW(foreach=False)-exact AdamW with fused unscale, skip and export.
 
     params: FP32 CUDA tensors (or torch-style param-group dicts).
-    loss_scale: None (no scaling), a float, or a DynamicLossScale whose
-      overflow()/success() this optimizer calls after each step.
+    loss_scale: None (no scaling), a float (fixed scale), or a DynamicLossScale
+      whose state this optimizer advances (on the device) after every step.
     export_dtype: torch.float16 / torch.bfloat16 to keep an export copy of
       every master (self.exports), written in the same pass.
     on_overflow: "skip" -- a step with a non-finite gradient changes no
-      master/moment/clock and step() returns False; "raise" -- additionally
-      raise FloatingPointError like HybridMuonAdamW (optimizer.py:50-51).
+      master/moment/clock; "raise" -- additionally raise FloatingPointError
+      from step() like HybridMuonAdamW (optimizer.py:50-51); implies sync.
+    sync: resolve after every step; step() then returns True (applied) or
+      False (skipped).  Otherwise step() returns None and enqueues only.
     """
 
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2, *,
-                 loss_scale=None, export_dtype=None, on_overflow="skip"):
+                 loss_scale=None, export_dtype=None, on_overflow="skip", sync=False):
         if on_overflow not in _OVERFLOW_POLICIES:
             raise ValueError(f"on_overflow must be one of {_OVERFLOW_POLICIES}")
         if not 0.0 <= lr:
@@ -58,36 +66,42 @@ class FusedAdamW:
         self.defaults = dict(lr=lr, betas=tuple(betas), eps=eps, weight_decay=weight_decay)
         self.param_groups = _groups(params, self.defaults)
         self.on_overflow = on_overflow
-        self.loss_scale = loss_scale
+        self.sync = sync or on_overflow == "raise"
         self.export_dtype = export_dtype
         self.state = {}
         self.exports = []
+        flat = self._flat()
+        if len({id(p) for _, p in flat}) != len(flat):
+            raise ValueError("a parameter appears more than once")
         device = None
-        for group in self.param_groups:
-            for p in group["params"]:
-                kernels.require_device_tensor(p, "param")
-                if p.dtype != torch.float32:
-                    raise TypeError("FusedAdamW keeps FP32 masters; got " + str(p.dtype))
-                device = device or p.device
-                self.state[p] = {"step": 0, "exp_avg": torch.zeros_like(p),
-                                 "exp_avg_sq": torch.zeros_like(p)}
-                if export_dtype is not None:
-                    self.exports.append(p.detach().to(export_dtype))
-        self._flag = kernels.new_flag(device)
-        self._flag_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
-        self._batch_key = None
-        self._batch = None
+        for _, p in flat:
+            kernels.require_device_tensor(p, "param")
+            if p.dtype != torch.float32:
+                raise TypeError("FusedAdamW keeps FP32 masters; got " + str(p.dtype))
+            if device is not None and p.device != device:
+                raise ValueError("all parameters must be on one device")
+            device = p.device
+            self.state[p] = {"step": 0, "exp_avg": torch.zeros_like(p),
+                             "exp_avg_sq": torch.zeros_like(p)}
+            if export_dtype is not None:
+                self.exports.append(p.detach().to(export_dtype))
+        self.device = device
+        self._ctl = StepControl(device, len(flat), loss_scale)
+        self._tables = {}
+        self._bound = [0] * len(flat)  # upper bound of each device clock
+        self._cache_key = None
+        self._cache = None
+        self.kernel_timer = None  # optional list: (start, end) events around each AdamW launch
         self.skipped_steps = 0
+        self.applied_steps = 0
+
+    @property
+    def loss_scale(self):
+        return self._ctl.loss_scale
 
     # -- helpers -----------------------------------------------------------
     def _flat(self):
         return [(gi, p) for gi, group in enumerate(self.param_groups) for p in group["params"]]
-
-    def _scale(self):
-        s = self.loss_scale
-        if s is None:
-            return 1.0
-        return float(s.scale) if hasattr(s, "scale") else float(s)
 
     def zero_grad(self, set_to_none=True):
         for _, p in self._flat():
@@ -99,21 +113,61 @@ class FusedAdamW:
     def set_exports(self, outs):
         """Write the export copy into caller buffers (e.g. a slot's compute weights)."""
         outs = list(outs)
-        if len(outs) != len(self._flat()):
+        flat = self._flat()
+        if len(outs) != len(flat):
             raise ValueError("one export buffer per parameter")
-        for (_, p), o in zip(self._flat(), outs):
+        for (_, p), o in zip(flat, outs):
             kernels.require_device_tensor(o, "export")
             if o.numel() != p.numel() or o.dtype not in (torch.float16, torch.bfloat16):
                 raise ValueError("export buffers must match params and be fp16/bf16")
+        if len({o.dtype for o in outs}) != 1:
+            raise ValueError("export buffers must share one dtype")
         self.exports = outs
-        self._batch_key = None
+        self._cache_key = None
+
+    def _table(self, betas):
+        key = (float(betas[0]), float(betas[1]))
+        if key not in self._tables:
+            self._tables[key] = BiasTables(key[0], key[1], self.device)
+        return self._tables[key]
+
+    def _prepare(self, grads, present):
+        """Descriptor batch, per-group constants and clock list for this set of tensors."""
+        flat = self._flat()
+        groups = sorted({flat[i][0] for i in present})
+        hp_of = {gi: k for k, gi in enumerate(groups)}
+        key = (tuple(present), tuple(grads[i].data_ptr() for i in present),
+               tuple(e.data_ptr() for e in self.exports) if self.exports else None)
+        if key != self._cache_key:
+            ps = [flat[i][1] for i in present]
+            batch = kernels.AdamwBatch(
+                ps, [self.state[p]["exp_avg"] for p in ps],
+                [self.state[p]["exp_avg_sq"] for p in ps], [grads[i] for i in present],
+                [self.exports[i] for i in present] if self.exports else None,
+                hp_index=[hp_of[flat[i][0]] for i in present], clock_index=list(present))
+            clock_list = torch.tensor(present, dtype=torch.int32).to(self.device)
+            self._cache = (batch, clock_list)
+            self._cache_key = key
+        batch, clock_list = self._cache
+        hps, scheds = [], []
+        for gi in groups:
+            group = self.param_groups[gi]
+            beta1, beta2 = group["betas"]
+            hps.append(adamw_constants(lr=group["lr"], beta1=beta1, beta2=beta2, eps=group["eps"],
+                                       weight_decay=group["weight_decay"], step=1))
+            table = self._table(group["betas"])
+            need = max(self._bound[i] for i in present if flat[i][0] == gi) + 1
+            table.ensure(need)
+            scheds.append(table.sched(group["lr"]))
+        return batch, clock_list, hps, scheds
 
     # -- the step ----------------------------------------------------------
-    def enqueue(self, grads=None, stream=None):
-        """Enqueue detector + fused AdamW without waiting; returns the launch record.
+    @torch.no_grad()
+    def step(self, grads=None, stream=None):
+        """Enqueue one optimizer step (detector, fused AdamW, step close).
 
-        finish(record) must follow before the next enqueue (it reads the
-        device flag and advances clocks and the loss scale).
+        grads: one tensor (or None) per parameter in param-group order; by
+        default p.grad.  Returns None, or with sync the applied/skipped outcome.
         """
         flat = self._flat()
         if grads is None:
@@ -123,68 +177,57 @@ class FusedAdamW:
             raise ValueError(f"expected {len(flat)} gradients, got {len(grads)}")
         present = [i for i, g in enumerate(grads) if g is not None]
         if not present:
+            return True if self.sync else None
+        if self._ctl.scaler_changed():  # the caller edited the scaler: resync the device copy
+            self.resolve()
+            self._ctl.push_scale()
+        batch, clock_list, hps, scheds = self._prepare(grads, present)
+        ctl = self._ctl
+        kernels.nonfinite_or([grads[i] for i in present], ctl.found_inf_ptr, stream)
+        if self.kernel_timer is not None:
+            s = stream or torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, stream)
+            e1.record(s)
+            self.kernel_timer.append((e0, e1))
+        else:
+            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, stream)
+        kernels.step_end(ctl.state, ctl.clocks, clock_list, stream)
+        for i in present:
+            self._bound[i] += 1
+        if not self.sync:
             return None
-        scale = self._scale()
-        flag = self._flag
-        kernels.flag_clear(flag, stream)
-        kernels.nonfinite_or([grads[i] for i in present], flag, stream)
-        hps, hp_of = [], {}
-        hp_index = []
-        for i in present:
-            gi, p = flat[i]
-            group = self.param_groups[gi]
-            key = (gi, self.state[p]["step"] + 1)
-            if key not in hp_of:
-                beta1, beta2 = group["betas"]
-                hp_of[key] = len(hps)
-                hps.append(adamw_constants(lr=group["lr"], beta1=beta1, beta2=beta2,
-                                           eps=group["eps"], weight_decay=group["weight_decay"],
-                                           step=key[1], loss_scale=scale))
-            hp_index.append(hp_of[key])
-        outs = [self.exports[i] if self.exports else None for i in present]
-        key = (tuple(present), tuple(grads[i].data_ptr() for i in present), tuple(hp_index),
-               tuple(o.data_ptr() if o is not None else 0 for o in outs))
-        if key != self._batch_key:
-            ps = [flat[i][1] for i in present]
-            self._batch = kernels.AdamwBatch(
-                ps, [self.state[p]["exp_avg"] for p in ps],
-                [self.state[p]["exp_avg_sq"] for p in ps], [grads[i] for i in present],
-                outs if self.exports else None, hp_index)
-            self._batch_key = key
-        self._batch.launch(hps, skip_flag=flag, stream=stream)
-        self._flag_host.copy_(flag, non_blocking=True)
-        event = torch.cuda.Event()
-        event.record(stream)
-        return (present, event)
+        st = self.resolve()
+        if st.last_found_inf and self.on_overflow == "raise":
+            raise FloatingPointError("nonfinite gradient; optimizer not updated")
+        return not st.last_found_inf
 
-    def finish(self, record):
-        """Wait for an enqueued step; apply the skip decision on the host side."""
-        if record is None:
-            return True
-        present, event = record
-        event.synchronize()
-        overflowed = bool(self._flag_host.item())
-        flat = self._flat()
-        if overflowed:
-            self.skipped_steps += 1
-            if isinstance(self.loss_scale, DynamicLossScale) or hasattr(self.loss_scale, "overflow"):
-                self.loss_scale.overflow()
-            if self.on_overflow == "raise":
-                raise FloatingPointError("nonfinite gradient; optimizer not updated")
-            return False
-        for i in present:
-            self.state[flat[i][1]]["step"] += 1
-        if hasattr(self.loss_scale, "success"):
-            self.loss_scale.success()
-        return True
+    def resolve(self):
+        """Wait for enqueued steps; refresh clocks, counters and the host loss scale.
 
-    @torch.no_grad()
-    def step(self, grads=None, stream=None):
-        """One optimizer step; True if applied, False if skipped on overflow."""
-        return self.finish(self.enqueue(grads, stream))
+        Raises FloatingPointError if a step overflowed at loss scale <= 1 (the
+        reference raises there; on the device that step and every later one
+        changed nothing).
+        """
+        st = self._ctl.read()
+        clocks = self._ctl.clocks.cpu().tolist()
+        for i, (_, p) in enumerate(self._flat()):
+            self.state[p]["step"] = clocks[i]
+            self._bound[i] = clocks[i]
+        self.skipped_steps = int(st.skipped)
+        self.applied_steps = int(st.applied)
+        self._ctl.mirror(st)
+        err = self._ctl.fatal_error(st)
+        if err is not None:
+            raise err
+        return st
+
+    synchronize = resolve
 
     # -- persistence (torch.optim.Optimizer layout) ------------------------
     def state_dict(self):
+        self.resolve()
         index = {}
         groups = []
         for group in self.param_groups:
@@ -199,21 +242,26 @@ class FusedAdamW:
         return {"state": state, "param_groups": groups}
 
     def load_state_dict(self, state_dict):
+        self.resolve()
         flat = [p for _, p in self._flat()]
         if len(state_dict["param_groups"]) != len(self.param_groups):
             raise ValueError("loaded state dict has a different number of parameter groups")
         for group, saved in zip(self.param_groups, state_dict["param_groups"]):
             if len(saved["params"]) != len(group["params"]):
                 raise ValueError("loaded state dict contains a group of a different size")
+        for group, saved in zip(self.param_groups, state_dict["param_groups"]):
             for k, v in saved.items():
                 if k != "params":
                     group[k] = tuple(v) if k == "betas" else v
+        clocks = []
         for i, p in enumerate(flat):
-            saved = state_dict["state"].get(i)
-            if saved is None:
-                continue
             st = self.state[p]
-            st["step"] = int(float(saved["step"]))
-            st["exp_avg"].copy_(saved["exp_avg"])
-            st["exp_avg_sq"].copy_(saved["exp_avg_sq"])
-        self._batch_key = None
+            saved = state_dict["state"].get(i)
+            if saved is not None:
+                st["step"] = int(float(saved["step"]))
+                st["exp_avg"].copy_(saved["exp_avg"])
+                st["exp_avg_sq"].copy_(saved["exp_avg_sq"])
+            clocks.append(st["step"])
+            self._bound[i] = st["step"]
+        self._ctl.clocks.copy_(torch.tensor(clocks, dtype=torch.int64))
+        self._cache_key = None

@@ -60,7 +60,8 @@ def test_config1_bitexact_vs_oracle_and_torch_golden(golden_dir):
     dev = [m.to(DEV) for m in masters]
     groups = [dict(params=[p for p in dev if p.ndim == 2], weight_decay=CONFIG1["wd_2d"]),
               dict(params=[p for p in dev if p.ndim == 1], weight_decay=0.0)]
-    opt = FusedAdamW(groups, lr=CONFIG1["lr"], betas=CONFIG1["betas"], eps=CONFIG1["eps"])
+    opt = FusedAdamW(groups, lr=CONFIG1["lr"], betas=CONFIG1["betas"], eps=CONFIG1["eps"],
+                     sync=True)
     order = [p for g in opt.param_groups for p in g["params"]]
     index = [next(i for i, q in enumerate(dev) if q is p) for p in order]
     ora = OracleWindow([masters[i] for i in index])
@@ -92,7 +93,7 @@ def test_config1_vs_live_torch_adamw_on_gpu_box():
     dev = [m.to(DEV) for m in masters]
     groups = [dict(params=[p for p in dev if p.ndim == 2], weight_decay=.1),
               dict(params=[p for p in dev if p.ndim == 1], weight_decay=0.)]
-    opt = FusedAdamW(groups, lr=3e-4, betas=(.9, .95), eps=1e-8)
+    opt = FusedAdamW(groups, lr=3e-4, betas=(.9, .95), eps=1e-8)  # asynchronous steps
     for t in range(1, 11):
         gs = grads(t)
         for p, g in zip(ref, gs):
@@ -100,6 +101,7 @@ def test_config1_vs_live_torch_adamw_on_gpu_box():
         topt.step()
         by_id = {id(p): g for p, g in zip(dev, gs)}
         opt.step([by_id[id(p)].to(DEV) for grp in opt.param_groups for p in grp["params"]])
+    opt.resolve()
     for p, q in zip(ref, dev):
         st, qs = topt.state[p], opt.state[q]
         assert torch.equal(st["exp_avg"], qs["exp_avg"].cpu())
@@ -117,7 +119,7 @@ def _config2_run(shapes, steps, seed):
     shapes = [tuple(m.shape) for m in masters]
     scaler = DynamicLossScale(65536., 2000)
     opt = FusedAdamW([m.to(DEV) for m in masters], lr=3e-4, betas=(.9, .95), eps=1e-8,
-                     weight_decay=.1, loss_scale=scaler, export_dtype=torch.float16)
+                     weight_decay=.1, loss_scale=scaler, export_dtype=torch.float16, sync=True)
     ora = OracleWindow(masters)
     outs = None
     for t in range(1, steps + 1):
@@ -145,7 +147,7 @@ def test_config3_tied_embedding_full_size():
     from oracle import reference as R
     w0 = torch.randn(65536, 3072, generator=torch.Generator().manual_seed(4)) * .02
     opt = FusedAdamW([w0.to(DEV)], lr=3e-4, betas=(.9, .95), eps=1e-8, weight_decay=0.0,
-                     export_dtype=torch.bfloat16)
+                     export_dtype=torch.bfloat16, sync=True)
     ora = OracleWindow([w0])
     for t in (1, 2):
         g, active = bench.config3_embedding_grad(7000 + t)
@@ -179,7 +181,7 @@ def test_config4_overflow_skip_sequence(golden_dir, shapes):
     scaler = DynamicLossScale(cfg["initial"], cfg["growth_interval"])
     oscaler = R.LossScale(cfg["initial"], cfg["growth_interval"])
     opt = FusedAdamW([m.to(DEV) for m in masters], lr=3e-4, betas=(.9, .95), eps=1e-8,
-                     weight_decay=.1, loss_scale=scaler, export_dtype=torch.float16)
+                     weight_decay=.1, loss_scale=scaler, export_dtype=torch.float16, sync=True)
     ora = OracleWindow(masters)
     rng = np.random.RandomState(44)
     seen = []
@@ -219,7 +221,7 @@ def test_none_grad_leaves_param_and_clock():
     a = torch.randn(1000, generator=torch.Generator().manual_seed(1)).to(DEV)
     b = torch.randn(1000, generator=torch.Generator().manual_seed(2)).to(DEV)
     b0 = b.clone()
-    opt = FusedAdamW([a, b], lr=1e-3)
+    opt = FusedAdamW([a, b], lr=1e-3, sync=True)
     g = torch.randn(1000, device=DEV) * 1e-3
     assert opt.step([g, None])
     assert opt.step([g, None])
@@ -248,8 +250,101 @@ def test_state_dict_interchanges_with_torch_adamw():
         p.grad = g.clone()
         topt.step()
         opt.step([g.to(DEV)])
+    opt.resolve()
+    assert opt.state[q]["step"] == 4
     assert torch.equal(opt.state[q]["exp_avg"].cpu(), topt.state[p]["exp_avg"])
     assert torch.equal(opt.state[q]["exp_avg_sq"].cpu(), topt.state[p]["exp_avg_sq"])
     assert (q.cpu() - p.detach()).abs().max() <= 1e-6 * p.detach().abs().max()
     back = opt.state_dict()
     assert float(back["state"][0]["step"]) == 4.0
+
+
+def _config4_grads(shapes, rng, t, scale, overflow_steps):
+    grads = bench.config2_grads("cpu", 2000 + t, shapes, scale=scale)
+    if t in overflow_steps:
+        for _ in range(int(rng.randint(1, 9))):
+            k = int(rng.randint(len(grads)))
+            flat = grads[k].view(-1)
+            flat[int(rng.randint(flat.numel()))] = float(rng.choice([np.inf, -np.inf, np.nan]))
+    return grads
+
+
+def test_async_steps_equal_synchronous_steps(golden_dir):
+    """16 steps enqueued back to back (no host round trip) end in the same bytes, clocks
+    and loss scale as the step-by-step run, though the host learns the outcomes only at
+    the end.  Gradients are pre-scaled with the scale sequence the skips imply."""
+    cfg = json.loads((golden_dir / "loss_scale.json").read_text())["config4"]
+    shapes = [(512, 256), (256, 512), (1000,)]
+    masters = [torch.randn(s, generator=torch.Generator().manual_seed(60 + i)) * .02
+               for i, s in enumerate(shapes)]
+    runs = []
+    for sync in (True, False):
+        scaler = DynamicLossScale(cfg["initial"], cfg["growth_interval"])
+        opt = FusedAdamW([m.to(DEV) for m in masters], lr=3e-4, betas=(.9, .95),
+                         weight_decay=.1, loss_scale=scaler, export_dtype=torch.float16, sync=sync)
+        rng = np.random.RandomState(45)
+        for t in range(1, cfg["steps"] + 1):
+            grads = _config4_grads(shapes, rng, t, cfg["scale_before_step"][t - 1],
+                                   cfg["overflow_steps"])
+            opt.step([g.to(DEV) for g in grads])
+        opt.resolve()
+        runs.append((opt, scaler))
+    (a, sa), (b, sb) = runs
+    assert sa.state_dict() == sb.state_dict() and sa.scale == cfg["final_scale"]
+    assert a.skipped_steps == b.skipped_steps == 3 and a.applied_steps == b.applied_steps == 13
+    for p, q in zip(a.param_groups[0]["params"], b.param_groups[0]["params"]):
+        assert torch.equal(p, q)
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(a.state[p][k], b.state[q][k])
+        assert a.state[p]["step"] == b.state[q]["step"] == 13
+    for e, f in zip(a.exports, b.exports):
+        assert torch.equal(e, f)
+
+
+def test_overflow_at_minimum_scale_raises_and_freezes_state():
+    """precision.py:9-10: overflow at scale <= 1 raises with the state unchanged; on the
+    device every step after it is a no-op until the host sees the error."""
+    w = torch.randn(4096, generator=torch.Generator().manual_seed(3)).to(DEV)
+    scaler = DynamicLossScale(2., growth_interval=2000)
+    opt = FusedAdamW([w], lr=1e-3, loss_scale=scaler)
+    good = torch.randn(4096, device=DEV).half()
+    bad = good.clone()
+    bad[5] = float("inf")
+    opt.step([good])
+    opt.step([bad])   # scale 2 -> 1
+    opt.step([bad])   # at scale 1: the reference raises here
+    before = w.clone()
+    opt.step([good])  # enqueued before the host knows: must change nothing
+    with pytest.raises(FloatingPointError, match="minimum loss scale"):
+        opt.resolve()
+    assert torch.equal(w, before)
+    assert scaler.scale == 1.0 and opt.state[w]["step"] == 1
+
+
+def test_fixed_scale_and_raise_policy():
+    """A float loss scale never changes; on_overflow='raise' raises before any mutation."""
+    w = torch.randn(3000, generator=torch.Generator().manual_seed(4)).to(DEV)
+    opt = FusedAdamW([w], lr=1e-3, loss_scale=1024.0, on_overflow="raise")
+    g = (torch.randn(3000, device=DEV) * 1e-3 * 1024).half()
+    assert opt.step([g]) is True
+    before = w.clone()
+    g[0] = float("nan")
+    with pytest.raises(FloatingPointError, match="nonfinite gradient"):
+        opt.step([g])
+    assert torch.equal(w, before) and opt.state[w]["step"] == 1
+    g[0] = 0.0
+    assert opt.step([g]) is True and opt.state[w]["step"] == 2
+
+
+def test_loss_scale_growth_on_device_matches_host_rule():
+    """growth_interval 3: the scale doubles every 3 clean steps, capped at 65536."""
+    from oracle import reference as R
+    w = torch.randn(2048, generator=torch.Generator().manual_seed(5)).to(DEV)
+    scaler = DynamicLossScale(16384., growth_interval=3)
+    oscaler = R.LossScale(16384., 3)
+    opt = FusedAdamW([w], lr=1e-3, loss_scale=scaler)
+    for t in range(14):
+        opt.step([(torch.randn(2048, device=DEV) * 1e-4).half()])
+        oscaler.success()
+    opt.resolve()
+    assert scaler.state_dict() == oscaler.state_dict() and scaler.scale == 65536.
