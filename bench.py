@@ -18,12 +18,14 @@ library the reference's AdamW group runs -- on this host's cores.
 """
 import argparse
 import json
-import os
 import sys
 import time
+from pathlib import Path
 
 import torch
 
+ROOT = Path(__file__).resolve().parent
+TRAFFIC_PROFILE = ROOT / "profiles" / "adamw_config2_traffic.json"
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_PARAM = 28  # read g16 2 + w 4 + m 4 + v 4; write w 4 + m 4 + v 4 + export 2
 CONFIG2_SHAPES = [(6144, 3072), (6144, 3072), (3072, 6144)]  # W_gate, W_up, W_down (nn.Linear storage)
@@ -124,13 +126,31 @@ def cpu_baseline(seconds=10.0):
                        f"torch.optim.AdamW(foreach=False) after FP16 unscale; CPU: {cpu}")
 
 
+def measured_traffic():
+    """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
+    try:
+        return json.loads(TRAFFIC_PROFILE.read_text())["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
+                    help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration << 18, device="cuda")  # MiB of float32
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_each_way": src.numel() * 4}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this "
               "build (the optimizer step shards by contiguous ranges across GPUs, see the "
@@ -164,7 +184,7 @@ def main():
         "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(),
                      "kernel": "adamw_multi_kernel<F16,F16,dev>",
                      "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
                      "bytes_per_launch": BYTES_PER_PARAM * n},

@@ -8,7 +8,7 @@
 // which is non-finite exactly when some element is.
 //
 // Each lane loads 16 bytes per access (8 fp16/bf16 or 4 fp32), kUnroll
-// accesses before testing; a wave reduces its lanes with a ballot and one lane
+// accesses before testing, with temporal loads (see MORPH_NONFINITE_NT); a wave reduces its lanes with a ballot and one lane
 // writes 1 to the flag with a plain vector store (every writer writes the
 // same value, so the race is benign).  Nothing is ever written on a clean
 // pass, so detector calls over several tensors OR into one flag.
@@ -16,6 +16,12 @@
 
 #ifndef MORPH_NONFINITE_UNROLL
 #define MORPH_NONFINITE_UNROLL 4
+#endif
+// Temporal loads on purpose: the fused AdamW pass re-reads these gradients
+// right after, and leaving them in the Infinity Cache (MALL) takes that
+// re-read off HBM, so detector + AdamW move 28 bytes/parameter of HBM traffic.
+#ifndef MORPH_NONFINITE_NT
+#define MORPH_NONFINITE_NT 0
 #endif
 
 namespace morph {
@@ -70,7 +76,8 @@ __global__ __launch_bounds__(kBlock) void nonfinite_kernel(const LaunchArgs a,
                                                     base * kElemBytes);
     u32x4 w[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) w[u] = load_stream<true>(p + u * kBlock + threadIdx.x);
+    for (int u = 0; u < kUnroll; ++u)
+      w[u] = load_stream<MORPH_NONFINITE_NT != 0>(p + u * kBlock + threadIdx.x);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
       bad |= word_nonfinite<GT>(w[u].x) | word_nonfinite<GT>(w[u].y) |
