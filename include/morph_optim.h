@@ -217,6 +217,79 @@ int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad
 int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* d_clock_list,
                    int n, void* stream);
 
+/* ---- Hybrid Muon: Newton-Schulz orthogonalisation on bf16 MFMA ---------- */
+
+/* Tile of morph_gemm_nt_bf16: M and N must be multiples of 128, K of 64. */
+#define MORPH_GEMM_TILE_M 128
+#define MORPH_GEMM_TILE_N 128
+#define MORPH_GEMM_TILE_K 64
+
+/*
+ * Batched bf16 GEMM, "NT" layout, fp32 accumulation:
+ *   C[b] = alpha * P[b] . Q[b]^T + beta * D[b];   Ct[b] = C[b]^T if Ct != NULL
+ * P [M, K], Q [N, K], D/C [M, N], Ct [N, M], all row-major bf16 (uint16 bits)
+ * with leading dimensions ld* and batch strides stride_* in elements; b < batch.
+ * D may be NULL (beta ignored) and may alias C.  Each output element is
+ * rounded once (RNE) from fp32.  The three products of one Newton-Schulz
+ * iteration of optimizer.py:19-21 are all of this form (see gemm.hip).
+ * MORPH_ERANGE when a dimension is not a tile multiple.
+ */
+int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D, uint16_t* C,
+                       uint16_t* Ct, int64_t M, int64_t N, int64_t K, int64_t batch,
+                       int64_t ldp, int64_t ldq, int64_t ldd, int64_t ldc, int64_t ldct,
+                       int64_t stride_p, int64_t stride_q, int64_t stride_d, int64_t stride_c,
+                       int64_t stride_ct, float alpha, float beta, void* stream);
+
+/* One Muon matrix: FP32 [rows, cols] row-major device buffers. */
+typedef struct morph_muon_matrix {
+  const float* grad;
+  float* momentum; /* updated in place (unused by morph_muon_orthogonalize) */
+  float* param;    /* FP32 master, updated in place (the output of morph_muon_orthogonalize) */
+} morph_muon_matrix;
+
+/*
+ * Constants of one Muon step (streamtrain/optimizer.py:52-61), fp32 values of
+ * the reference's Python scalars: momentum_weight = .05 (lerp_(g, .05)),
+ * nesterov_weight = .95 (g.lerp(m, .95)), a/b/c = 3.4445, -4.775, 2.0315,
+ * update_scale = sqrt(max(1, rows/cols)), decay = 1 - lr * weight_decay,
+ * neg_lr = -lr; ns_steps = 5.
+ */
+typedef struct morph_muon_hp {
+  float momentum_weight;
+  float nesterov_weight;
+  float a, b, c;
+  float update_scale;
+  float decay;
+  float neg_lr;
+  int32_t ns_steps;
+  int32_t reserved;
+} morph_muon_hp;
+
+/* Workspace bytes morph_muon_step needs for `count` matrices of [rows, cols]. */
+size_t morph_muon_workspace_bytes(int64_t rows, int64_t cols, int count);
+
+/*
+ * One Muon step for `count` (<= 64) matrices of the same shape, batched:
+ * momentum and Nesterov blend (fp32, torch's rounding), Frobenius
+ * normalisation, ns_steps Newton-Schulz iterations in bf16 on MFMA (A = X X^T,
+ * B = b A + c A A, X = a X + B X, fp32 accumulation), and the fp32 master update
+ * p = p * decay + (U * update_scale) * neg_lr with U in p's layout (transposed
+ * back when rows > cols, optimizer.py:15-17, 22).  The workspace must be
+ * 256-byte aligned and zero-filled once before first use (its zero padding is
+ * kept by every call).  Replaces optimizer.py:13-22 and 52-61.
+ */
+int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+                    const morph_muon_hp* hp, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/*
+ * orthogonalize(grad) alone (optimizer.py:13-22): param <- NS(grad / (|grad| + 1e-7))
+ * as fp32 values of the bf16 result; momentum, update_scale, decay and neg_lr unused.
+ */
+int morph_muon_orthogonalize(const morph_muon_matrix* mats, int count, int64_t rows,
+                             int64_t cols, const morph_muon_hp* hp, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,8 +22,10 @@ HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
 EXPORTS = (
     "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
-    "morph_adamw_multi_dev", "morph_step_end",
+    "morph_adamw_multi_dev", "morph_step_end", "morph_gemm_nt_bf16",
+    "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
 )
+GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 128, 128, 64
 FATAL_MIN_SCALE = 1
 
 
@@ -62,6 +64,19 @@ class AdamwSched(ctypes.Structure):
                 ("bias_correction2_sqrt", ctypes.c_void_p), ("table_len", ctypes.c_int64)]
 
 
+class MuonMatrix(ctypes.Structure):
+    """morph_muon_matrix."""
+    _fields_ = [("grad", ctypes.c_void_p), ("momentum", ctypes.c_void_p),
+                ("param", ctypes.c_void_p)]
+
+
+class MuonHP(ctypes.Structure):
+    """morph_muon_hp."""
+    _fields_ = [(name, ctypes.c_float) for name in (
+        "momentum_weight", "nesterov_weight", "a", "b", "c", "update_scale", "decay",
+        "neg_lr")] + [("ns_steps", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
 _lib = None
 
 
@@ -89,6 +104,13 @@ def lib():
                                        ctypes.POINTER(AdamwHP), ctypes.POINTER(AdamwSched), i32,
                                        vp, vp, vp], i32),
             "morph_step_end": ([vp, vp, vp, i32, vp], i32),
+            "morph_gemm_nt_bf16": ([vp, vp, vp, vp, vp] + [i64] * 14 +
+                                   [ctypes.c_float, ctypes.c_float, vp], i32),
+            "morph_muon_workspace_bytes": ([i64, i64, i32], ctypes.c_size_t),
+            "morph_muon_step": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                                 ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
+            "morph_muon_orthogonalize": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                                          ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(handle, name)

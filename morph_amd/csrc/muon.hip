@@ -1,0 +1,297 @@
+// Hybrid Muon step for gfx950: momentum, Nesterov blend, Frobenius
+// normalisation, Newton-Schulz quintic on bf16 MFMA, FP32 master update.
+// Follows streamtrain/optimizer.py:13-22 (orthogonalize) and 52-61 (the Muon
+// loop) for a batch of matrices that share one shape:
+//
+//   momentum.lerp_(g, mom_w)                    fma(mom_w, g - m, m)           (58)
+//   u = g.lerp(momentum, nesterov_w)            fma(nesterov_w - 1, m - g, m)  (59)
+//   X = u (or u^T when rows > cols) / (|u|_F + 1e-7)                      (15-18)
+//   5x: A = X X^T; X = a X + (b A + c A A) X    bf16 operands, fp32 accum   (19-21)
+//   p = p * decay + (U * scale) * neg_lr        U = X in p's layout           (60-61)
+//
+// The reference computes orthogonalize in FP32; here X, A and B are bf16 (the
+// BASELINE's Newton-Schulz precision) with fp32 accumulation and one rounding
+// per product, so parity with the reference is a tolerance, not bit equality.
+// The elementwise steps round exactly like torch (explicit fmaf where its CPU
+// kernels fuse, plain multiplies elsewhere).
+//
+// Workspace (caller-allocated, zero-filled once; morph_muon_workspace_bytes):
+// u fp32 [count][rows*cols]; per-block partial sums f64; denominators f32;
+// X [count][Mp][Np], Xt0/Xt1 [count][Np][Mp], A and B [count][Mp][Mp], bf16,
+// with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.  The
+// zero padding is exact for Newton-Schulz: padded rows of X give zero rows and
+// columns of A and B, which keep the padding of X zero in every iteration.
+#include "common.h"
+
+namespace morph {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kMaxMats = 64;
+constexpr int kElemsPerBlock = kBlock * 16;  // 16 elements per lane, lane-strided (coalesced)
+constexpr int kTile = 64;                       // transpose tile
+
+struct MatPtrs {
+  const float* grad[kMaxMats];
+  float* mom[kMaxMats];
+  float* param[kMaxMats];
+};
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+struct Layout {
+  int64_t rows, cols, m, n, mp, np, count, numel, blocks;
+  size_t off_u, off_part, off_den, off_x, off_xt0, off_xt1, off_a, off_b, total;
+};
+
+Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
+  Layout L;
+  L.rows = rows;
+  L.cols = cols;
+  L.count = count;
+  L.m = rows < cols ? rows : cols;
+  L.n = rows < cols ? cols : rows;
+  L.mp = round_up(L.m, MORPH_GEMM_TILE_M);
+  L.np = round_up(L.n, MORPH_GEMM_TILE_N);  // also a multiple of the K tile (64)
+  L.numel = rows * cols;
+  L.blocks = (L.numel + kElemsPerBlock - 1) / kElemsPerBlock;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = (off + bytes + 255) / 256 * 256;
+    return at;
+  };
+  L.off_u = take((size_t)count * L.numel * 4);
+  L.off_part = take((size_t)count * L.blocks * 8);
+  L.off_den = take((size_t)count * 4);
+  L.off_x = take((size_t)count * L.mp * L.np * 2);
+  L.off_xt0 = take((size_t)count * L.np * L.mp * 2);
+  L.off_xt1 = take((size_t)count * L.np * L.mp * 2);
+  L.off_a = take((size_t)count * L.mp * L.mp * 2);
+  L.off_b = take((size_t)count * L.mp * L.mp * 2);
+  L.total = off;
+  return L;
+}
+
+__device__ __forceinline__ double block_sum(double x, double* lds) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds[wave] = x;
+  __syncthreads();
+  double s = 0.0;
+  if (threadIdx.x == 0)
+    for (int w = 0; w < kBlock / 64; ++w) s += lds[w];
+  return s;  // valid in thread 0
+}
+
+// momentum + Nesterov blend + partial sums of u^2 (one partial per block).
+// kMomentum = false: u = grad (orthogonalize alone).
+template <bool kMomentum>
+__global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u_all,
+                                                          double* part_all, int64_t numel,
+                                                          int64_t blocks, float mom_w,
+                                                          float nest_w) {
+  __shared__ double lds[kBlock / 64];
+  const int mat = blockIdx.y;
+  const float* g = mats.grad[mat];
+  float* mom = mats.mom[mat];
+  float* u = u_all + (int64_t)mat * numel;
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
+  const bool large_m = mom_w >= 0.5f, large_n = nest_w >= 0.5f;
+  double ss = 0.0;
+  for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
+    const float gi = g[i];
+    float ui = gi;
+    if constexpr (kMomentum) {
+      float m = mom[i];
+      m = large_m ? __fmaf_rn(mom_w - 1.0f, gi - m, gi) : __fmaf_rn(mom_w, gi - m, m);
+      ui = large_n ? __fmaf_rn(nest_w - 1.0f, m - gi, m) : __fmaf_rn(nest_w, m - gi, gi);
+      mom[i] = m;
+    }
+    u[i] = ui;
+    ss += (double)ui * (double)ui;
+  }
+  const double s = block_sum(ss, lds);
+  if (threadIdx.x == 0) part_all[(int64_t)mat * blocks + blockIdx.x] = s;
+}
+
+// den = fp32(sqrt(sum)) + fp32(1e-7): x / (x.norm() + 1e-7) of optimizer.py:18.
+__global__ __launch_bounds__(kBlock) void norm_kernel(const double* part_all, float* den,
+                                                      int64_t blocks) {
+  __shared__ double lds[kBlock / 64];
+  const int mat = blockIdx.x;
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < blocks; i += kBlock) s += part_all[(int64_t)mat * blocks + i];
+  const double t = block_sum(s, lds);
+  if (threadIdx.x == 0) den[mat] = (float)sqrt(t) + 1e-7f;
+}
+
+// X / Xt (bf16, padded) from u / den.  The param layout is [rows, cols]; X is
+// [m, n] with m = min: when rows <= cols X has the param layout and Xt is the
+// transpose, otherwise the other way round.  One 64 x 64 tile of u per block,
+// transposed through LDS so both writes are coalesced.
+__global__ __launch_bounds__(kBlock) void scale_kernel(const float* u_all, const float* den,
+                                                       uint16_t* x_all, uint16_t* xt_all,
+                                                       int64_t rows, int64_t cols, int64_t mp,
+                                                       int64_t np, int64_t numel) {
+  __shared__ uint16_t tile[kTile][kTile + 2];
+  const int mat = blockIdx.z;
+  const float d = den[mat];
+  const float* u = u_all + (int64_t)mat * numel;
+  const bool same_is_x = rows <= cols;  // X has the param layout
+  uint16_t* same = same_is_x ? x_all + (int64_t)mat * mp * np : xt_all + (int64_t)mat * np * mp;
+  uint16_t* trans = same_is_x ? xt_all + (int64_t)mat * np * mp : x_all + (int64_t)mat * mp * np;
+  const int64_t ld_same = same_is_x ? np : mp;   // row length of the param-layout copy
+  const int64_t ld_trans = same_is_x ? mp : np;  // row length of the transposed copy
+  const int64_t r0 = (int64_t)blockIdx.y * kTile, c0 = (int64_t)blockIdx.x * kTile;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int rr = ty; rr < kTile; rr += kBlock / 64) {
+    const int64_t r = r0 + rr, c = c0 + tx;
+    uint16_t h = 0;
+    if (r < rows && c < cols) {
+      h = (uint16_t)float_to_bf16_bits(u[r * cols + c] / d);
+      same[r * ld_same + c] = h;
+    }
+    tile[rr][tx] = h;
+  }
+  __syncthreads();
+  for (int cc = ty; cc < kTile; cc += kBlock / 64) {
+    const int64_t c = c0 + cc, r = r0 + tx;
+    if (r < rows && c < cols) trans[c * ld_trans + r] = tile[tx][cc];
+  }
+}
+
+// p = p * decay + (U * scale) * neg_lr, U read from the bf16 copy in p's layout.
+// kExtract: p = U instead (orthogonalize alone returns the fp32 value of U).
+template <bool kExtract>
+__global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint16_t* x_all,
+                                                       const uint16_t* xt_all, int64_t rows,
+                                                       int64_t cols, int64_t mp, int64_t np,
+                                                       float scale, float decay, float neg_lr) {
+  const int mat = blockIdx.y;
+  float* p = mats.param[mat];
+  const bool same_is_x = rows <= cols;
+  const uint16_t* U = same_is_x ? x_all + (int64_t)mat * mp * np : xt_all + (int64_t)mat * np * mp;
+  const int64_t ld = same_is_x ? np : mp;
+  const int64_t numel = rows * cols;
+  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
+  for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
+    const int64_t r = i / cols, c = i - r * cols;
+    if constexpr (kExtract) {
+      p[i] = bf16_bits_to_float(U[r * ld + c]);
+    } else {
+      const float upd = bf16_bits_to_float(U[r * ld + c]) * scale;
+      p[i] = __fmaf_rn(upd, neg_lr, p[i] * decay);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace morph
+
+using namespace morph;
+
+extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D,
+                                  uint16_t* C, uint16_t* Ct, int64_t M, int64_t N, int64_t K,
+                                  int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
+                                  int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
+                                  int64_t stride_d, int64_t stride_c, int64_t stride_ct,
+                                  float alpha, float beta, void* stream);
+
+extern "C" size_t morph_muon_workspace_bytes(int64_t rows, int64_t cols, int count) {
+  if (rows <= 0 || cols <= 0 || count <= 0) return 0;
+  return make_layout(rows, cols, count).total;
+}
+
+namespace {
+
+// The whole sequence for one batch of same-shape matrices.  orth_only: u = grad,
+// and the result U (fp32) is written into mats[i].param.
+int run_muon(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+             const morph_muon_hp* hp, void* workspace, size_t workspace_bytes, bool orth_only,
+             void* stream) {
+  if (mats == nullptr || hp == nullptr || count < 0 || rows <= 0 || cols <= 0 ||
+      hp->ns_steps < 0)
+    return MORPH_EINVAL;
+  if (count == 0) return MORPH_OK;
+  if (count > kMaxMats) return MORPH_ERANGE;
+  for (int i = 0; i < count; ++i)
+    if (mats[i].grad == nullptr || mats[i].param == nullptr ||
+        (!orth_only && mats[i].momentum == nullptr))
+      return MORPH_EINVAL;
+  const Layout L = make_layout(rows, cols, count);
+  if (workspace == nullptr || workspace_bytes < L.total) return MORPH_EWORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return MORPH_EINVAL;
+  if ((rows + kTile - 1) / kTile > 65535) return MORPH_ERANGE;  // grid y of scale_kernel
+  char* ws = static_cast<char*>(workspace);
+  float* u = reinterpret_cast<float*>(ws + L.off_u);
+  double* part = reinterpret_cast<double*>(ws + L.off_part);
+  float* den = reinterpret_cast<float*>(ws + L.off_den);
+  uint16_t* X = reinterpret_cast<uint16_t*>(ws + L.off_x);
+  uint16_t* Xt[2] = {reinterpret_cast<uint16_t*>(ws + L.off_xt0),
+                     reinterpret_cast<uint16_t*>(ws + L.off_xt1)};
+  uint16_t* A = reinterpret_cast<uint16_t*>(ws + L.off_a);
+  uint16_t* B = reinterpret_cast<uint16_t*>(ws + L.off_b);
+  hipStream_t s = as_stream(stream);
+  MatPtrs mp_;
+  for (int i = 0; i < count; ++i) {
+    mp_.grad[i] = mats[i].grad;
+    mp_.mom[i] = mats[i].momentum;
+    mp_.param[i] = mats[i].param;
+  }
+  const dim3 ew((unsigned)L.blocks, count);
+  if (orth_only)
+    hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kBlock), 0, s, mp_, u, part, L.numel,
+                       L.blocks, hp->momentum_weight, hp->nesterov_weight);
+  else
+    hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kBlock), 0, s, mp_, u, part, L.numel,
+                       L.blocks, hp->momentum_weight, hp->nesterov_weight);
+  int rc = launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, part, den, L.blocks);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(scale_kernel,
+                     dim3((unsigned)((cols + kTile - 1) / kTile),
+                          (unsigned)((rows + kTile - 1) / kTile), count),
+                     dim3(kBlock), 0, s, u, den, X, Xt[0], rows, cols, L.mp, L.np, L.numel);
+  if ((rc = launch_status())) return rc;
+  const int64_t sx = L.mp * L.np, ss = L.mp * L.mp;
+  int cur = 0;
+  for (int it = 0; it < hp->ns_steps; ++it) {
+    // A = X X^T
+    rc = morph_gemm_nt_bf16(X, X, nullptr, A, nullptr, L.mp, L.mp, L.np, count, L.np, L.np, 0,
+                            L.mp, 0, sx, sx, 0, ss, 0, 1.0f, 0.0f, stream);
+    if (rc) return rc;
+    // B = c (A A^T) + b A
+    rc = morph_gemm_nt_bf16(A, A, A, B, nullptr, L.mp, L.mp, L.mp, count, L.mp, L.mp, L.mp,
+                            L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b, stream);
+    if (rc) return rc;
+    // X' = (B Xt^T) + a X, written in place over X and transposed into the other Xt
+    rc = morph_gemm_nt_bf16(B, Xt[cur], X, X, Xt[cur ^ 1], L.mp, L.np, L.mp, count, L.mp, L.mp,
+                            L.np, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a, stream);
+    if (rc) return rc;
+    cur ^= 1;
+  }
+  if (orth_only)
+    hipLaunchKernelGGL(apply_kernel<true>, ew, dim3(kBlock), 0, s, mp_, X, Xt[cur], rows, cols,
+                       L.mp, L.np, hp->update_scale, hp->decay, hp->neg_lr);
+  else
+    hipLaunchKernelGGL(apply_kernel<false>, ew, dim3(kBlock), 0, s, mp_, X, Xt[cur], rows, cols,
+                       L.mp, L.np, hp->update_scale, hp->decay, hp->neg_lr);
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t rows,
+                               int64_t cols, const morph_muon_hp* hp, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  return run_muon(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
+}
+
+extern "C" int morph_muon_orthogonalize(const morph_muon_matrix* mats, int count, int64_t rows,
+                                        int64_t cols, const morph_muon_hp* hp, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return run_muon(mats, count, rows, cols, hp, workspace, workspace_bytes, true, stream);
+}

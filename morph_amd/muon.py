@@ -1,0 +1,218 @@
+"""Hybrid Muon on the gfx950 kernels (streamtrain/optimizer.py:13-70).
+
+orthogonalize() and muon_step() drive morph_muon_* (momentum, Nesterov blend,
+Frobenius normalisation, bf16 MFMA Newton-Schulz, fp32 master update);
+gemm_nt() exposes the batched bf16 GEMM the iteration is built from.
+HybridMuonAdamW keeps the reference class's constructor, partition rule,
+step/zero_grad/state_dict/load_state_dict, with the AdamW group on FusedAdamW.
+"""
+import ctypes
+
+import torch
+from torch import nn
+
+from . import _lib, kernels
+from ._lib import MuonHP, MuonMatrix, check, lib, require_device_tensor, stream_handle
+from .hyper import to_f32
+from .optimizer import FusedAdamW
+
+NS_COEFFS = (3.4445, -4.775, 2.0315)  # optimizer.py:21
+NS_STEPS = 5  # optimizer.py:13
+
+
+def _bf16_ptr(t):
+    if t is None:
+        return None
+    if t.dtype != torch.bfloat16:
+        raise TypeError("bf16 tensor expected")
+    require_device_tensor(t, "gemm operand")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, stream=None):
+    """out = alpha * P @ Q^T + beta * D (bf16, fp32 accumulation); out_t = out^T if given.
+
+    P [.., M, K], Q [.., N, K], D/out [.., M, N], out_t [.., N, M]; a leading batch
+    dimension is optional.  M, N multiples of 128 and K of 64.
+    """
+    batched = P.dim() == 3
+    if not batched:
+        P, Q = P.unsqueeze(0), Q.unsqueeze(0)
+        D = D.unsqueeze(0) if D is not None else None
+    b, M, K = P.shape
+    N = Q.shape[1]
+    if Q.shape != (b, N, K) or (D is not None and D.shape != (b, M, N)):
+        raise ValueError("gemm_nt: shapes do not match P [b,M,K], Q [b,N,K], D [b,M,N]")
+    if out is None:
+        out = torch.empty((b, M, N), dtype=torch.bfloat16, device=P.device)
+    elif not batched:
+        out = out.unsqueeze(0)
+    if out_t is not None and not batched:
+        out_t = out_t.unsqueeze(0)
+    if out.shape != (b, M, N) or (out_t is not None and out_t.shape != (b, N, M)):
+        raise ValueError("gemm_nt: output shapes do not match")
+    check(lib().morph_gemm_nt_bf16(
+        _bf16_ptr(P), _bf16_ptr(Q), _bf16_ptr(D), _bf16_ptr(out), _bf16_ptr(out_t),
+        M, N, K, b, K, K, N, N, M, M * K, N * K, M * N, M * N, N * M,
+        float(alpha), float(beta), stream_handle(stream)))
+    return out if batched else out[0]
+
+
+class _Workspaces:
+    """Zero-filled device workspaces, one per (shape, count, device), kept for reuse."""
+
+    def __init__(self):
+        self._ws = {}
+
+    def get(self, rows, cols, count, device):
+        key = (rows, cols, count, device)
+        if key not in self._ws:
+            nbytes = lib().morph_muon_workspace_bytes(rows, cols, count)
+            if nbytes == 0:
+                raise ValueError(f"bad Muon shape {rows}x{cols} x{count}")
+            self._ws[key] = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        return self._ws[key]
+
+
+_WORKSPACES = _Workspaces()
+
+
+def _hp(momentum_weight=.05, nesterov_weight=.95, update_scale=1.0, decay=1.0, neg_lr=0.0,
+        steps=NS_STEPS, coeffs=NS_COEFFS):
+    a, b, c = coeffs
+    return MuonHP(to_f32(momentum_weight), to_f32(nesterov_weight), to_f32(a), to_f32(b),
+                  to_f32(c), to_f32(update_scale), to_f32(decay), to_f32(neg_lr), steps, 0)
+
+
+def _by_shape(items):
+    groups = {}
+    for item in items:
+        groups.setdefault(tuple(item[0].shape), []).append(item)
+    return groups
+
+
+def _run(entry, mats, rows, cols, hp, stream, workspaces):
+    for start in range(0, len(mats), 64):
+        chunk = mats[start:start + 64]
+        ws = workspaces.get(rows, cols, len(chunk), chunk[0][0].device)
+        arr = (MuonMatrix * len(chunk))()
+        for i, (p, g, m) in enumerate(chunk):
+            arr[i].grad, arr[i].param = g.data_ptr(), p.data_ptr()
+            arr[i].momentum = m.data_ptr() if m is not None else None
+        check(entry(arr, len(chunk), rows, cols, ctypes.byref(hp),
+                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream_handle(stream)))
+
+
+def _check_matrix(t, name):
+    require_device_tensor(t, name)
+    if t.dim() != 2 or t.dtype != torch.float32:
+        raise ValueError(f"{name} must be a 2-D float32 tensor")
+
+
+def orthogonalize(gradients, steps=NS_STEPS, stream=None, workspaces=_WORKSPACES):
+    """optimizer.py:13-22 on the GPU: NS(g / (|g|_F + 1e-7)), bf16 MFMA, returned as fp32.
+
+    gradients: one 2-D tensor or a list; same-shape matrices run as one batch.
+    """
+    single = torch.is_tensor(gradients)
+    gs = [gradients] if single else list(gradients)
+    outs = []
+    for g in gs:
+        _check_matrix(g, "gradient")
+        outs.append(torch.empty_like(g))
+    items = [(o, g, None) for o, g in zip(outs, gs)]
+    for (rows, cols), group in _by_shape(items).items():
+        _run(lib().morph_muon_orthogonalize, group, rows, cols, _hp(steps=steps), stream,
+             workspaces)
+    return outs[0] if single else outs
+
+
+def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=None,
+              workspaces=_WORKSPACES):
+    """The Muon loop body of optimizer.py:55-61 for every (param, grad, momentum) triple.
+
+    In place on params and momenta.  Scalars follow the reference: decay
+    1 - lr * weight_decay, update scale sqrt(max(1, rows / cols)), alpha -lr.
+    """
+    items = []
+    for p, g, m in zip(params, grads, momenta):
+        for t, name in ((p, "param"), (g, "grad"), (m, "momentum")):
+            _check_matrix(t, name)
+        if not (p.shape == g.shape == m.shape):
+            raise ValueError("param, grad and momentum shapes differ")
+        items.append((p, g, m))
+    for (rows, cols), group in _by_shape(items).items():
+        hp = _hp(update_scale=max(1, rows / cols) ** .5, decay=1 - lr * weight_decay,
+                 neg_lr=-lr, steps=steps)
+        _run(lib().morph_muon_step, group, rows, cols, hp, stream, workspaces)
+
+
+def partition(model):
+    """optimizer.py:25-31: hidden nn.Linear weights (not lm_head) -> Muon; the rest -> AdamW."""
+    hidden = {id(module.weight) for name, module in model.named_modules()
+              if isinstance(module, nn.Linear) and name != 'lm_head'}
+    muon, adam = [], []
+    for param in model.parameters():
+        (muon if id(param) in hidden else adam).append(param)
+    return muon, adam
+
+
+class HybridMuonAdamW:
+    """streamtrain/optimizer.py:34-70 on the GPU.
+
+    Same constructor and methods.  step() raises FloatingPointError before any
+    mutation when a gradient is non-finite (optimizer.py:49-51), then runs the
+    Muon update for the hidden matrices (batched by shape) and the AdamW group
+    (betas .9/.95, FusedAdamW).  The Newton-Schulz iteration is bf16 on MFMA
+    where the reference uses FP32 (optimizer.py:3-6).
+    """
+
+    def __init__(self, model, lr=1e-3, muon_lr=None, weight_decay=.01):
+        self.muon, adam = partition(model)
+        self.lr = lr if muon_lr is None else muon_lr
+        self.weight_decay = weight_decay
+        self.momentum = {}
+        self.adam = FusedAdamW(adam, lr=lr, weight_decay=weight_decay, betas=(.9, .95),
+                               sync=True) if adam else None
+        self._flag = None
+
+    def zero_grad(self, set_to_none=True):
+        for p in self.muon:
+            p.grad = None if set_to_none else torch.zeros_like(p)
+        if self.adam is not None:
+            self.adam.zero_grad(set_to_none=set_to_none)
+
+    def _all_params(self):
+        adam = [p for g in self.adam.param_groups for p in g["params"]] if self.adam else []
+        return self.muon + adam
+
+    @torch.no_grad()
+    def step(self):
+        grads = [p.grad for p in self._all_params() if p.grad is not None]
+        if grads:
+            if self._flag is None:
+                self._flag = kernels.new_flag(grads[0].device)
+            kernels.flag_clear(self._flag)
+            kernels.nonfinite_or(grads, self._flag)
+            if self._flag.item():
+                raise FloatingPointError('nonfinite gradient; optimizer not updated')
+        live = [(i, p) for i, p in enumerate(self.muon) if p.grad is not None]
+        for i, p in live:
+            if i not in self.momentum:
+                self.momentum[i] = torch.zeros_like(p)
+        if live:
+            muon_step([p for _, p in live], [p.grad for _, p in live],
+                      [self.momentum[i] for i, _ in live], self.lr, self.weight_decay)
+        if self.adam is not None:
+            self.adam.step()
+
+    def state_dict(self):
+        return dict(momentum=self.momentum,
+                    adam=self.adam.state_dict() if self.adam else None,
+                    lr=self.lr, weight_decay=self.weight_decay)
+
+    def load_state_dict(self, state):
+        self.momentum = {i: value.to(self.muon[i].device) for i, value in state['momentum'].items()}
+        if self.adam is not None:
+            self.adam.load_state_dict(state['adam'])
+        self.lr, self.weight_decay = state['lr'], state['weight_decay']
