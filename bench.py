@@ -31,6 +31,9 @@ BYTES_PER_PARAM = 28  # read g16 2 + w 4 + m 4 + v 4; write w 4 + m 4 + v 4 + ex
 CONFIG2_SHAPES = [(6144, 3072), (6144, 3072), (3072, 6144)]  # W_gate, W_up, W_down (nn.Linear storage)
 LOSS_SCALE = 65536.0
 HYPER = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+CONFIG5_LAYERS = 14        # 5B preset: 14 SwiGLU blocks -> 42 hidden matrices
+CONFIG5_ADAM_VECTORS = 326  # x 3072 = 1,001,472 norm/bias parameters
 
 
 # ------------------------------------------------------------ workloads --
@@ -57,6 +60,29 @@ def config3_embedding_grad(step_seed, rows=65536, cols=3072, tokens=4 * 1024, s=
     g = torch.zeros(rows, cols, dtype=torch.bfloat16)
     g[active] = (torch.randn(active.numel(), cols, generator=gen) * 1e-3).to(torch.bfloat16)
     return g.to(device), active
+
+
+class Config5(torch.nn.Module):
+    """42 hidden Linear weights (Muon) + ~1M norm/bias params (AdamW).
+
+    Per SwiGLU block W_gate, W_up [6144, 3072] and W_down [3072, 6144] in nn.Linear
+    storage, so after optimizer.py:15-17's transpose rule every Newton-Schulz
+    operand is [3072, 6144].  Weights N(0, .02); norms/biases ones.
+    """
+
+    def __init__(self, device):
+        super().__init__()
+        mk = lambda o, i: torch.nn.Linear(i, o, bias=False, device=device)
+        self.blocks = torch.nn.ModuleList(
+            torch.nn.ModuleDict(dict(gate=mk(6144, 3072), up=mk(6144, 3072), down=mk(3072, 6144)))
+            for _ in range(CONFIG5_LAYERS))
+        self.vectors = torch.nn.ParameterList(
+            torch.nn.Parameter(torch.ones(3072, device=device)) for _ in range(CONFIG5_ADAM_VECTORS))
+        gen = torch.Generator(device=device).manual_seed(5)
+        with torch.no_grad():
+            for block in self.blocks:
+                for lin in block.values():
+                    lin.weight.copy_(torch.randn(lin.weight.shape, generator=gen, device=device) * .02)
 
 
 # --------------------------------------------------------------- timing --
@@ -126,6 +152,74 @@ def cpu_baseline(seconds=10.0):
                        f"torch.optim.AdamW(foreach=False) after FP16 unscale; CPU: {cpu}")
 
 
+def time_muon(steps, warmup):
+    """Config 5 through HybridMuonAdamW: gate, batched Muon (bf16 MFMA NS), AdamW group."""
+    from morph_amd.muon import HybridMuonAdamW, ns_flops
+    device = torch.device("cuda", 0)
+    model = Config5(device)
+    gen = torch.Generator(device=device).manual_seed(6)
+    for p in model.parameters():
+        p.grad = torch.randn(p.shape, generator=gen, device=device) * 1e-3
+    opt = HybridMuonAdamW(model, lr=3e-4, muon_lr=0.02)
+    for _ in range(warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    opt.ns_timer = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ns_s = sum(a.elapsed_time(b) for a, b, _ in opt.ns_timer) / 1e3 / steps
+    flops = sum(f for _, _, f in opt.ns_timer) / steps
+    n_muon = sum(p.numel() for p in opt.muon)
+    n_adam = sum(p.numel() for g in opt.adam.param_groups for p in g["params"])
+    return dict(elapsed=elapsed, ns_s=ns_s, flops=flops, n_muon=n_muon, n_adam=n_adam,
+                expected_flops=ns_flops(3072, 6144, 42))
+
+
+def cpu_baseline_muon():
+    """The reference's FP32 Muon update (optimizer.py:55-61, torch CPU) on one [6144, 3072]
+    matrix of the 42, scaled by 42 to a whole step (the 1M AdamW group is negligible)."""
+    from oracle import reference as R
+    threads = min(16, R.cpu_threads())
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(7)
+    p = torch.randn(6144, 3072, generator=gen) * .02
+    g = torch.randn(6144, 3072, generator=gen) * 1e-3
+    m = torch.zeros_like(p)
+    R.muon_reference_step(p, g, m, .02, .01)  # warm-up
+    t0 = time.perf_counter()
+    R.muon_reference_step(p, g, m, .02, .01)
+    one = time.perf_counter() - t0
+    return dict(value=round(42 * one * 1e3, 1), unit="ms/step", cores=threads, kind="port",
+                sample=f"one [6144, 3072] Muon matrix (FP32 NS, torch CPU) = {one * 1e3:.1f} ms, "
+                       "x42 for the step")
+
+
+def muon_main(args):
+    r = time_muon(args.steps, args.warmup)
+    ms = r["elapsed"] / args.steps * 1e3
+    achieved = r["flops"] / r["ns_s"] / 1e12
+    line = {
+        "metric": "Hybrid Muon step, 42 x [3072, 6144] NS bf16 + 1M AdamW, 1 MI355X",
+        "value": round(ms, 3), "unit": "ms/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "config 5: 14 x (W_gate, W_up [6144,3072], W_down [3072,6144]) "
+                               "Muon (5 NS iterations, bf16 MFMA, lr .02, momentum .95) + "
+                               f"{r['n_adam']} AdamW params", "muon_params": r["n_muon"]},
+        "ns_ms_per_step": round(r["ns_s"] * 1e3, 3),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel": "gemm_nt_kernel (15 launches per shape group)",
+                     "flops_per_step": r["flops"]},
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_muon(),
+    }
+    assert r["flops"] == r["expected_flops"]
+    print(json.dumps(line), flush=True)
+
+
 def measured_traffic():
     """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
     try:
@@ -140,6 +234,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("adamw", "muon"), default="adamw",
+                    help="adamw: the headline config-2 step (default); muon: config 5")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()
@@ -159,6 +255,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "muon":
+        return muon_main(args)
     r = time_gpu(args.steps, args.warmup)
     n = r["n"]
     ms_per_step = r["elapsed"] / args.steps * 1e3

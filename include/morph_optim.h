@@ -290,6 +290,23 @@ int morph_muon_orthogonalize(const morph_muon_matrix* mats, int count, int64_t r
                              int64_t cols, const morph_muon_hp* hp, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/*
+ * The three phases morph_muon_step / morph_muon_orthogonalize run, for callers
+ * that interleave other work or time the Newton-Schulz GEMM chain on its own:
+ * prepare (momentum + Nesterov, or u = grad when orthogonalize_only; norm;
+ * bf16 X and X^T into the workspace), newton_schulz (hp->ns_steps iterations,
+ * 3 GEMMs each, on the workspace only), finish (master update, or U into
+ * param when orthogonalize_only).  Same arguments and workspace throughout.
+ */
+int morph_muon_prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+                       const morph_muon_hp* hp, int orthogonalize_only, void* workspace,
+                       size_t workspace_bytes, void* stream);
+int morph_muon_newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp,
+                             void* workspace, size_t workspace_bytes, void* stream);
+int morph_muon_finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+                      const morph_muon_hp* hp, int orthogonalize_only, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,7 @@ EXPORTS = (
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
     "morph_adamw_multi_dev", "morph_step_end", "morph_gemm_nt_bf16",
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
+    "morph_muon_prepare", "morph_muon_newton_schulz", "morph_muon_finish",
 )
 GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 128, 128, 64
 FATAL_MIN_SCALE = 1
@@ -111,6 +112,12 @@ def lib():
                                  ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
             "morph_muon_orthogonalize": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
                                           ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
+            "morph_muon_prepare": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                                    ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp], i32),
+            "morph_muon_newton_schulz": ([i32, i64, i64, ctypes.POINTER(MuonHP), vp,
+                                          ctypes.c_size_t, vp], i32),
+            "morph_muon_finish": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                                   ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(handle, name)

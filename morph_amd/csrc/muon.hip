@@ -206,92 +206,167 @@ extern "C" size_t morph_muon_workspace_bytes(int64_t rows, int64_t cols, int cou
 
 namespace {
 
-// The whole sequence for one batch of same-shape matrices.  orth_only: u = grad,
-// and the result U (fp32) is written into mats[i].param.
-int run_muon(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
-             const morph_muon_hp* hp, void* workspace, size_t workspace_bytes, bool orth_only,
-             void* stream) {
-  if (mats == nullptr || hp == nullptr || count < 0 || rows <= 0 || cols <= 0 ||
-      hp->ns_steps < 0)
+struct Bufs {
+  Layout L;
+  float* u;
+  double* part;
+  float* den;
+  uint16_t* X;
+  uint16_t* Xt[2];
+  uint16_t* A;
+  uint16_t* B;
+};
+
+// Validates the call and carves the workspace.  need_mats: mats must be given.
+int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+          const morph_muon_hp* hp, void* workspace, size_t workspace_bytes, bool need_mats,
+          bool need_momentum, Bufs* out) {
+  if (hp == nullptr || count < 0 || rows <= 0 || cols <= 0 || hp->ns_steps < 0)
     return MORPH_EINVAL;
-  if (count == 0) return MORPH_OK;
   if (count > kMaxMats) return MORPH_ERANGE;
-  for (int i = 0; i < count; ++i)
-    if (mats[i].grad == nullptr || mats[i].param == nullptr ||
-        (!orth_only && mats[i].momentum == nullptr))
-      return MORPH_EINVAL;
-  const Layout L = make_layout(rows, cols, count);
+  if (need_mats) {
+    if (count > 0 && mats == nullptr) return MORPH_EINVAL;
+    for (int i = 0; i < count; ++i)
+      if (mats[i].grad == nullptr || mats[i].param == nullptr ||
+          (need_momentum && mats[i].momentum == nullptr))
+        return MORPH_EINVAL;
+  }
+  const Layout L = make_layout(rows, cols, count > 0 ? count : 1);
   if (workspace == nullptr || workspace_bytes < L.total) return MORPH_EWORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return MORPH_EINVAL;
   if ((rows + kTile - 1) / kTile > 65535) return MORPH_ERANGE;  // grid y of scale_kernel
   char* ws = static_cast<char*>(workspace);
-  float* u = reinterpret_cast<float*>(ws + L.off_u);
-  double* part = reinterpret_cast<double*>(ws + L.off_part);
-  float* den = reinterpret_cast<float*>(ws + L.off_den);
-  uint16_t* X = reinterpret_cast<uint16_t*>(ws + L.off_x);
-  uint16_t* Xt[2] = {reinterpret_cast<uint16_t*>(ws + L.off_xt0),
-                     reinterpret_cast<uint16_t*>(ws + L.off_xt1)};
-  uint16_t* A = reinterpret_cast<uint16_t*>(ws + L.off_a);
-  uint16_t* B = reinterpret_cast<uint16_t*>(ws + L.off_b);
-  hipStream_t s = as_stream(stream);
-  MatPtrs mp_;
+  out->L = L;
+  out->u = reinterpret_cast<float*>(ws + L.off_u);
+  out->part = reinterpret_cast<double*>(ws + L.off_part);
+  out->den = reinterpret_cast<float*>(ws + L.off_den);
+  out->X = reinterpret_cast<uint16_t*>(ws + L.off_x);
+  out->Xt[0] = reinterpret_cast<uint16_t*>(ws + L.off_xt0);
+  out->Xt[1] = reinterpret_cast<uint16_t*>(ws + L.off_xt1);
+  out->A = reinterpret_cast<uint16_t*>(ws + L.off_a);
+  out->B = reinterpret_cast<uint16_t*>(ws + L.off_b);
+  return MORPH_OK;
+}
+
+MatPtrs pointers(const morph_muon_matrix* mats, int count) {
+  MatPtrs m;
   for (int i = 0; i < count; ++i) {
-    mp_.grad[i] = mats[i].grad;
-    mp_.mom[i] = mats[i].momentum;
-    mp_.param[i] = mats[i].param;
+    m.grad[i] = mats[i].grad;
+    m.mom[i] = mats[i].momentum;
+    m.param[i] = mats[i].param;
   }
+  return m;
+}
+
+int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+            const morph_muon_hp* hp, void* workspace, size_t workspace_bytes, bool orth_only,
+            void* stream) {
+  Bufs W;
+  int rc = setup(mats, count, rows, cols, hp, workspace, workspace_bytes, true, !orth_only, &W);
+  if (rc || count == 0) return rc;
+  const Layout& L = W.L;
+  hipStream_t s = as_stream(stream);
+  const MatPtrs mp_ = pointers(mats, count);
   const dim3 ew((unsigned)L.blocks, count);
   if (orth_only)
-    hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kBlock), 0, s, mp_, u, part, L.numel,
+    hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.u, W.part, L.numel,
                        L.blocks, hp->momentum_weight, hp->nesterov_weight);
   else
-    hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kBlock), 0, s, mp_, u, part, L.numel,
+    hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.u, W.part, L.numel,
                        L.blocks, hp->momentum_weight, hp->nesterov_weight);
-  int rc = launch_status();
-  if (rc) return rc;
-  hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, part, den, L.blocks);
+  if ((rc = launch_status())) return rc;
+  hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, W.part, W.den, L.blocks);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(scale_kernel,
                      dim3((unsigned)((cols + kTile - 1) / kTile),
                           (unsigned)((rows + kTile - 1) / kTile), count),
-                     dim3(kBlock), 0, s, u, den, X, Xt[0], rows, cols, L.mp, L.np, L.numel);
-  if ((rc = launch_status())) return rc;
+                     dim3(kBlock), 0, s, W.u, W.den, W.X, W.Xt[0], rows, cols, L.mp, L.np,
+                     L.numel);
+  return launch_status();
+}
+
+int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  Bufs W;
+  int rc = setup(nullptr, count, rows, cols, hp, workspace, workspace_bytes, false, false, &W);
+  if (rc || count == 0) return rc;
+  const Layout& L = W.L;
   const int64_t sx = L.mp * L.np, ss = L.mp * L.mp;
   int cur = 0;
   for (int it = 0; it < hp->ns_steps; ++it) {
     // A = X X^T
-    rc = morph_gemm_nt_bf16(X, X, nullptr, A, nullptr, L.mp, L.mp, L.np, count, L.np, L.np, 0,
-                            L.mp, 0, sx, sx, 0, ss, 0, 1.0f, 0.0f, stream);
+    rc = morph_gemm_nt_bf16(W.X, W.X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, L.np, L.np,
+                            0, L.mp, 0, sx, sx, 0, ss, 0, 1.0f, 0.0f, stream);
     if (rc) return rc;
     // B = c (A A^T) + b A
-    rc = morph_gemm_nt_bf16(A, A, A, B, nullptr, L.mp, L.mp, L.mp, count, L.mp, L.mp, L.mp,
-                            L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b, stream);
+    rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, L.mp, L.mp,
+                            L.mp, L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b, stream);
     if (rc) return rc;
     // X' = (B Xt^T) + a X, written in place over X and transposed into the other Xt
-    rc = morph_gemm_nt_bf16(B, Xt[cur], X, X, Xt[cur ^ 1], L.mp, L.np, L.mp, count, L.mp, L.mp,
-                            L.np, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a, stream);
+    rc = morph_gemm_nt_bf16(W.B, W.Xt[cur], W.X, W.X, W.Xt[cur ^ 1], L.mp, L.np, L.mp, count,
+                            L.mp, L.mp, L.np, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a, stream);
     if (rc) return rc;
     cur ^= 1;
   }
+  return MORPH_OK;
+}
+
+int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+           const morph_muon_hp* hp, void* workspace, size_t workspace_bytes, bool orth_only,
+           void* stream) {
+  Bufs W;
+  int rc = setup(mats, count, rows, cols, hp, workspace, workspace_bytes, true, false, &W);
+  if (rc || count == 0) return rc;
+  const Layout& L = W.L;
+  const MatPtrs mp_ = pointers(mats, count);
+  const dim3 ew((unsigned)L.blocks, count);
+  uint16_t* xt = W.Xt[hp->ns_steps & 1];  // the copy the last iteration wrote
+  hipStream_t s = as_stream(stream);
   if (orth_only)
-    hipLaunchKernelGGL(apply_kernel<true>, ew, dim3(kBlock), 0, s, mp_, X, Xt[cur], rows, cols,
+    hipLaunchKernelGGL(apply_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
                        L.mp, L.np, hp->update_scale, hp->decay, hp->neg_lr);
   else
-    hipLaunchKernelGGL(apply_kernel<false>, ew, dim3(kBlock), 0, s, mp_, X, Xt[cur], rows, cols,
+    hipLaunchKernelGGL(apply_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
                        L.mp, L.np, hp->update_scale, hp->decay, hp->neg_lr);
   return launch_status();
 }
 
 }  // namespace
 
+extern "C" int morph_muon_prepare(const morph_muon_matrix* mats, int count, int64_t rows,
+                                  int64_t cols, const morph_muon_hp* hp, int orthogonalize_only,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  return prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, orthogonalize_only != 0,
+                 stream);
+}
+
+extern "C" int morph_muon_newton_schulz(int count, int64_t rows, int64_t cols,
+                                        const morph_muon_hp* hp, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream);
+}
+
+extern "C" int morph_muon_finish(const morph_muon_matrix* mats, int count, int64_t rows,
+                                 int64_t cols, const morph_muon_hp* hp, int orthogonalize_only,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  return finish(mats, count, rows, cols, hp, workspace, workspace_bytes, orthogonalize_only != 0,
+                stream);
+}
+
 extern "C" int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t rows,
                                int64_t cols, const morph_muon_hp* hp, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  return run_muon(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
+  int rc = prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
+  if (!rc) rc = newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream);
+  if (!rc) rc = finish(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
+  return rc;
 }
 
 extern "C" int morph_muon_orthogonalize(const morph_muon_matrix* mats, int count, int64_t rows,
                                         int64_t cols, const morph_muon_hp* hp, void* workspace,
                                         size_t workspace_bytes, void* stream) {
-  return run_muon(mats, count, rows, cols, hp, workspace, workspace_bytes, true, stream);
+  int rc = prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, true, stream);
+  if (!rc) rc = newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream);
+  if (!rc) rc = finish(mats, count, rows, cols, hp, workspace, workspace_bytes, true, stream);
+  return rc;
 }

@@ -91,7 +91,18 @@ def _by_shape(items):
     return groups
 
 
-def _run(entry, mats, rows, cols, hp, stream, workspaces):
+def ns_flops(rows, cols, count, steps=NS_STEPS):
+    """Dense FLOPs of the Newton-Schulz chain: (4 m^2 n + 2 m^3) per matrix and iteration."""
+    m, n = min(rows, cols), max(rows, cols)
+    return count * steps * (4 * m * m * n + 2 * m ** 3)
+
+
+def _run(mats, rows, cols, hp, orth_only, stream, workspaces, timer=None):
+    """prepare -> Newton-Schulz -> finish for up to 64 same-shape matrices per batch.
+
+    timer: optional list; (start_event, end_event, flops) around each NS chain.
+    """
+    L = lib()
     for start in range(0, len(mats), 64):
         chunk = mats[start:start + 64]
         ws = workspaces.get(rows, cols, len(chunk), chunk[0][0].device)
@@ -99,8 +110,18 @@ def _run(entry, mats, rows, cols, hp, stream, workspaces):
         for i, (p, g, m) in enumerate(chunk):
             arr[i].grad, arr[i].param = g.data_ptr(), p.data_ptr()
             arr[i].momentum = m.data_ptr() if m is not None else None
-        check(entry(arr, len(chunk), rows, cols, ctypes.byref(hp),
-                    ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream_handle(stream)))
+        args = (ctypes.byref(hp),)
+        wsp, wsn, sh = ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream_handle(stream)
+        check(L.morph_muon_prepare(arr, len(chunk), rows, cols, *args, int(orth_only), wsp, wsn, sh))
+        if timer is not None:
+            s = stream or torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+        check(L.morph_muon_newton_schulz(len(chunk), rows, cols, *args, wsp, wsn, sh))
+        if timer is not None:
+            e1.record(s)
+            timer.append((e0, e1, ns_flops(rows, cols, len(chunk), hp.ns_steps)))
+        check(L.morph_muon_finish(arr, len(chunk), rows, cols, *args, int(orth_only), wsp, wsn, sh))
 
 
 def _check_matrix(t, name):
@@ -122,13 +143,12 @@ def orthogonalize(gradients, steps=NS_STEPS, stream=None, workspaces=_WORKSPACES
         outs.append(torch.empty_like(g))
     items = [(o, g, None) for o, g in zip(outs, gs)]
     for (rows, cols), group in _by_shape(items).items():
-        _run(lib().morph_muon_orthogonalize, group, rows, cols, _hp(steps=steps), stream,
-             workspaces)
+        _run(group, rows, cols, _hp(steps=steps), True, stream, workspaces)
     return outs[0] if single else outs
 
 
 def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=None,
-              workspaces=_WORKSPACES):
+              workspaces=_WORKSPACES, timer=None):
     """The Muon loop body of optimizer.py:55-61 for every (param, grad, momentum) triple.
 
     In place on params and momenta.  Scalars follow the reference: decay
@@ -144,7 +164,7 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
     for (rows, cols), group in _by_shape(items).items():
         hp = _hp(update_scale=max(1, rows / cols) ** .5, decay=1 - lr * weight_decay,
                  neg_lr=-lr, steps=steps)
-        _run(lib().morph_muon_step, group, rows, cols, hp, stream, workspaces)
+        _run(group, rows, cols, hp, False, stream, workspaces, timer)
 
 
 def partition(model):
@@ -169,6 +189,7 @@ class HybridMuonAdamW:
 
     def __init__(self, model, lr=1e-3, muon_lr=None, weight_decay=.01):
         self.muon, adam = partition(model)
+        self.ns_timer = None  # optional list: HIP events around each Newton-Schulz chain
         self.lr = lr if muon_lr is None else muon_lr
         self.weight_decay = weight_decay
         self.momentum = {}
@@ -202,7 +223,8 @@ class HybridMuonAdamW:
                 self.momentum[i] = torch.zeros_like(p)
         if live:
             muon_step([p for _, p in live], [p.grad for _, p in live],
-                      [self.momentum[i] for i, _ in live], self.lr, self.weight_decay)
+                      [self.momentum[i] for i, _ in live], self.lr, self.weight_decay,
+                      timer=self.ns_timer)
         if self.adam is not None:
             self.adam.step()
 

@@ -213,3 +213,23 @@ def test_hybrid_state_dict_roundtrip():
     ob.step()
     for (n, p), (_, q) in zip(a.named_parameters(), b.named_parameters()):
         assert torch.equal(p, q), n
+
+
+def test_one_call_c_entry_equals_phased_path():
+    """morph_muon_step (C convenience) == prepare/newton_schulz/finish as the Python layer runs them."""
+    import ctypes
+    from morph_amd import _lib
+    gen = torch.Generator().manual_seed(9)
+    shape = (192, 320)
+    p0, m0, g = (torch.randn(shape, generator=gen) * s for s in (.02, 1e-3, 1e-3))
+    pa, ma = p0.to(DEV), m0.to(DEV)
+    muon.muon_step([pa], [g.to(DEV)], [ma], .02, .01)
+    pb, mb, gb = p0.to(DEV), m0.to(DEV), g.to(DEV)
+    ws = torch.zeros(_lib.lib().morph_muon_workspace_bytes(*shape, 1), dtype=torch.uint8, device=DEV)
+    arr = (_lib.MuonMatrix * 1)()
+    arr[0].grad, arr[0].momentum, arr[0].param = gb.data_ptr(), mb.data_ptr(), pb.data_ptr()
+    hp = muon._hp(update_scale=1.0, decay=1 - .02 * .01, neg_lr=-.02)
+    _lib.check(_lib.lib().morph_muon_step(arr, 1, *shape, ctypes.byref(hp),
+                                          ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                          _lib.stream_handle()))
+    assert torch.equal(pa, pb) and torch.equal(ma, mb)
