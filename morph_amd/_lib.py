@@ -26,7 +26,7 @@ EXPORTS = (
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
     "morph_muon_prepare", "morph_muon_newton_schulz", "morph_muon_finish",
 )
-GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 128, 128, 64
+GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 256, 256, 64
 FATAL_MIN_SCALE = 1
 
 
@@ -106,7 +106,7 @@ def lib():
                                        vp, vp, vp], i32),
             "morph_step_end": ([vp, vp, vp, i32, vp], i32),
             "morph_gemm_nt_bf16": ([vp, vp, vp, vp, vp] + [i64] * 14 +
-                                   [ctypes.c_float, ctypes.c_float, vp], i32),
+                                   [ctypes.c_float, ctypes.c_float, i32, vp], i32),
             "morph_muon_workspace_bytes": ([i64, i64, i32], ctypes.c_size_t),
             "morph_muon_step": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
                                  ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),

@@ -9,19 +9,44 @@
 // such products: A = X X^T; B = b A + c A A^T (A is symmetric); X' = a X + B Xt^T
 // (B is symmetric, Xt = X^T), which is why only this one layout is needed.
 //
-// Tiling.  A workgroup (256 lanes, 4 wave64) owns a 128 x 128 tile of C; wave w
-// owns the 64 x 64 quarter (w / 2, w % 2) as 2 x 2 tiles of
-// v_mfma_f32_32x32x16_bf16.  K advances 64 per iteration: the P and Q tiles
-// (128 x 64 bf16 each) are staged global -> registers -> LDS, the next
-// iteration's global loads are issued before this iteration's MFMAs so their
-// latency hides behind the math.  LDS rows are padded to 72 bf16 (144 bytes)
-// so the 128-bit fragment reads of 16 consecutive rows hit distinct banks.
+// Tiling.  A workgroup (256 lanes, 4 wave64) owns a 256 x 256 tile of C; wave w
+// owns the 128 x 128 quarter (w / 2, w % 2) as 4 x 4 tiles of
+// v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane).  Per 32x32x16
+// step a wave reads 8 fragments (8 KiB) from LDS for 16 MFMAs.
+//
+// Operand pipeline.  K advances 32 per stage through a ring of kStages LDS
+// buffers (32 KiB each: P and Q sub-tiles of 256 x 32 bf16).  Operands go
+// global -> LDS directly (global_load_lds_dwordx4: lane l's 16 bytes land at
+// the instruction's LDS base + 16 l), so no registers are spent on staging and
+// kStages - 1 stages are in flight while one is consumed -- about 3000 MFMA
+// cycles to cover the L2 / fabric latency.  One barrier per stage: after it,
+// the stage just consumed is refilled with the one kStages - 1 ahead.
+// Because the DMA writes LDS linearly, rows cannot be padded; instead the four
+// 16-byte chunks of each 64-byte row are stored XOR-swizzled (slot = chunk ^
+// ((row >> 2) & 3)), chosen on the load side by which global chunk each lane
+// fetches, so the 128-bit fragment reads of 16 consecutive rows hit distinct
+// banks.
+//
+// Workgroup order.  The dispatcher hands workgroup i to XCD i % 8; each XCD
+// has its own L2.  Tiles are therefore numbered so that the workgroups one
+// XCD runs at a time form a compact block (groups of kGroupM tile rows walked
+// column by column), and each XCD gets a contiguous range of that numbering:
+// the concurrently running tiles of an XCD share operand panels in its L2.
+//
+// Symmetric mode (A = X X^T and B = b A + c A A^T are symmetric): only tiles
+// with tile_row <= tile_col run, and each off-diagonal tile is also written
+// transposed into the mirror position, halving the work of those products.
+//
+// Epilogue.  After the K loop the LDS holds the output tile: D is loaded into
+// it with coalesced 16-byte reads, each lane combines alpha * acc + beta * D in
+// fp32, rounds once to bf16 and writes back; then C (and Ct / the mirror tile)
+// leave with coalesced 16-byte stores.
 //
 // MFMA 32x32x16 lane layout (checked on the device): lane l holds
 // A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32] for i < 8; output
 // register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
 //
-// Dimensions must be multiples of the tile (M, N of 128, K of 64): callers pad
+// Dimensions must be multiples of the tile (M, N of 256, K of 64): callers pad
 // with zeros, which is exact for Newton-Schulz (zero rows stay zero).
 #include "common.h"
 
@@ -33,10 +58,18 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = MORPH_GEMM_TILE_M;
 constexpr int BN = MORPH_GEMM_TILE_N;
-constexpr int BK = MORPH_GEMM_TILE_K;
-constexpr int LDK = BK + 8;  // padded LDS row (bf16 elements)
+constexpr int BKS = 32;              // K per pipeline stage
+constexpr int kStages = 4;
+constexpr int LDE = BN + 8;          // padded LDS row of the output tile (bf16)
 constexpr int kThreads = 256;
-constexpr int kChunks = BM * BK / 8 / kThreads;  // 16-byte chunks per lane per tile (4)
+constexpr int kSubTile = BM * BKS;                   // bf16 per operand sub-tile (256 x 32)
+constexpr int kStageElems = 2 * kSubTile;            // P and Q
+constexpr int kLoadsPerOperand = kSubTile * 2 / 1024 / (kThreads / 64);  // 1 KiB DMA per wave-instr (4)
+constexpr int kSmemElems = (kStages * kStageElems > BM * LDE) ? kStages * kStageElems : BM * LDE;
+constexpr int kGroupM = 4;
+static_assert(BM == BN && BM == 256 && MORPH_GEMM_TILE_K % BKS == 0, "256 x 256 tiles, K % 32");
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 struct GemmArgs {
   const uint16_t* P;
@@ -44,108 +77,196 @@ struct GemmArgs {
   const uint16_t* D;
   uint16_t* C;
   uint16_t* Ct;
-  int64_t M, N, K;
+  int64_t K;
   int64_t ldp, ldq, ldd, ldc, ldct;
   int64_t sp, sq, sd, sc, sct;
   float alpha, beta;
+  int32_t tiles_m, tiles_n;
+  int32_t tiles_per_matrix;  // tiles_m * tiles_n, or the upper triangle when symmetric
+  int32_t symmetric;
+  int64_t total_tiles;       // batch * tiles_per_matrix
 };
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return float_to_bf16_bits(lo) | (float_to_bf16_bits(hi) << 16);
+// Tile (row, col) of the t-th tile of one matrix.
+__device__ __forceinline__ void tile_of(const GemmArgs& g, int t, int& tr, int& tc) {
+  if (g.symmetric) {  // upper triangle, row by row
+    int r = 0;
+    while (t >= g.tiles_n - r) {
+      t -= g.tiles_n - r;
+      ++r;
+    }
+    tr = r;
+    tc = r + t;
+    return;
+  }
+  const int per_group = kGroupM * g.tiles_n;
+  const int group = t / per_group;
+  const int within = t - group * per_group;
+  const int first = group * kGroupM;
+  const int rows = min(kGroupM, g.tiles_m - first);
+  tc = within / rows;
+  tr = first + within % rows;
 }
 
-__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t sP[BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[BN * LDK];
+__global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[kSmemElems];
+
+  // XCD-aware numbering: the grid is a multiple of 8; XCD x = id % 8 runs the
+  // contiguous logical range [x * per_xcd, (x + 1) * per_xcd).
+  const int64_t per_xcd = (int64_t)gridDim.x / 8;
+  const int64_t logical = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (logical >= g.total_tiles) return;
+  const int64_t b = logical / g.tiles_per_matrix;
+  int tr, tc;
+  tile_of(g, (int)(logical - b * g.tiles_per_matrix), tr, tc);
+  const int64_t row0 = (int64_t)tr * BM, col0 = (int64_t)tc * BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t b = blockIdx.z;
-  const int64_t row0 = (int64_t)blockIdx.y * BM;
-  const int64_t col0 = (int64_t)blockIdx.x * BN;
   const uint16_t* P = g.P + b * g.sp + row0 * g.ldp;
   const uint16_t* Q = g.Q + b * g.sq + col0 * g.ldq;
 
-  // Global -> register staging: chunk c of a tile is row c / 8, 16-byte column c % 8.
-  u32x4 rp[kChunks], rq[kChunks];
-  auto load_tiles = [&](int64_t k0) {
+  // DMA assignment: wave w, load j covers rows (w * 4 + j) * 16 .. +16 of a sub-tile;
+  // lane l -> row base + l / 4, LDS slot l % 4 holding global chunk slot ^ swz(row).
+  const int lrow = lane >> 2, lslot = lane & 3;
+  auto issue_stage = [&](int buf, int64_t k0) {
+    uint16_t* sP = smem + buf * kStageElems;
+    uint16_t* sQ = sP + kSubTile;
 #pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = tid + i * kThreads;
-      const int r = c >> 3, kc = (c & 7) * 8;
-      rp[i] = *reinterpret_cast<const u32x4*>(P + r * g.ldp + k0 + kc);
-      rq[i] = *reinterpret_cast<const u32x4*>(Q + r * g.ldq + k0 + kc);
-    }
-  };
-  auto store_tiles = [&]() {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = tid + i * kThreads;
-      const int r = c >> 3, kc = (c & 7) * 8;
-      *reinterpret_cast<u32x4*>(sP + r * LDK + kc) = rp[i];
-      *reinterpret_cast<u32x4*>(sQ + r * LDK + kc) = rq[i];
+    for (int j = 0; j < kLoadsPerOperand; ++j) {
+      const int r = (wave * kLoadsPerOperand + j) * 16 + lrow;
+      const int c = lslot ^ ((r >> 2) & 3);
+      const int lds_off = (wave * kLoadsPerOperand + j) * 16 * BKS;  // 1 KiB per instruction
+      __builtin_amdgcn_global_load_lds(P + r * g.ldp + k0 + c * 8, (lds_void*)(sP + lds_off), 16,
+                                       0, 0);
+      __builtin_amdgcn_global_load_lds(Q + r * g.ldq + k0 + c * 8, (lds_void*)(sQ + lds_off), 16,
+                                       0, 0);
     }
   };
 
-  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
-  const int fr = lane & 31, fk = (lane >> 5) * 8;
-  f32x16 acc[2][2];
+  const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
+  const int fr = lane & 31, fh = lane >> 5;  // fragment row in a 32-row tile, k half
+  f32x16 acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  const int64_t KT = g.K / BK;
-  load_tiles(0);
+  // Fragment of row R, 16-byte chunk c (c = 2 kk16 + k half): swizzled slot.
+  auto frag = [&](const uint16_t* sub, int R, int c) {
+    return *reinterpret_cast<const bf16x8*>(sub + R * BKS + ((c ^ ((R >> 2) & 3)) * 8));
+  };
+
+  const int64_t KT = g.K / BKS;
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < KT) issue_stage(s, (int64_t)s * BKS);
   for (int64_t kt = 0; kt < KT; ++kt) {
-    __syncthreads();  // every wave finished reading the previous tile
-    store_tiles();
-    __syncthreads();
-    if (kt + 1 < KT) load_tiles((kt + 1) * BK);  // in flight during the MFMAs below
+    // this wave's DMA for stage kt is complete once at most the later stages'
+    // 2 * kLoadsPerOperand loads each are outstanding
+    const int64_t later = (KT - 1 - kt) < (kStages - 2) ? (KT - 1 - kt) : (kStages - 2);
+    if (later >= 2)
+      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
+    else if (later == 1)
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();  // every wave's DMA for stage kt landed; stage kt - 1 is consumed
+    if (kt + kStages - 1 < KT)
+      issue_stage((int)((kt + kStages - 1) % kStages), (kt + kStages - 1) * BKS);
+    const uint16_t* sP = smem + (int)(kt % kStages) * kStageElems;
+    const uint16_t* sQ = sP + kSubTile;
+    // Fragment reads of both k halves are issued before the first MFMA (the
+    // second half's reads then overlap the first half's MFMAs), so LDS latency
+    // is paid about once per stage instead of once per fragment.
+    bf16x8 a[BKS / 16][4], q[BKS / 16][4];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      bf16x8 a[2], q[2];
+    for (int kk = 0; kk < BKS / 16; ++kk) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[i] = *reinterpret_cast<const bf16x8*>(sP + (wr + i * 32 + fr) * LDK + kk + fk);
-        q[i] = *reinterpret_cast<const bf16x8*>(sQ + (wc + i * 32 + fr) * LDK + kk + fk);
+      for (int i = 0; i < 4; ++i) {
+        a[kk][i] = frag(sP, wr + i * 32 + fr, kk * 2 + fh);
+        q[kk][i] = frag(sQ, wc + i * 32 + fr, kk * 2 + fh);
       }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int kk = 0; kk < BKS / 16; ++kk) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], q[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk][i], q[kk][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  __syncthreads();  // all fragment reads done before the epilogue reuses the LDS
 
-  // Epilogue: out = alpha * acc + beta * D, rounded once to bf16.
-  const uint16_t* D = g.D ? g.D + b * g.sd : nullptr;
-  uint16_t* C = g.C + b * g.sc;
-  uint16_t* Ct = g.Ct ? g.Ct + b * g.sct : nullptr;
+  // ---- epilogue through LDS --------------------------------------------------
+  uint16_t* E = smem;  // [BM][LDE] bf16 output tile
+  const uint16_t* D = g.D ? g.D + b * g.sd + row0 * g.ldd + col0 : nullptr;
+  if (D) {
+    // All 32 loads of a lane are in flight before the first LDS write (a
+    // load-then-write loop would pay the memory latency 32 times per tile).
+    constexpr int kDChunks = BM * (BN / 8) / kThreads;
+    u32x4 dv[kDChunks];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kDChunks; ++i) {
+      const int c = tid + i * kThreads;
+      const int r = c / (BN / 8), cc = (c % (BN / 8)) * 8;
+      dv[i] = *reinterpret_cast<const u32x4*>(D + r * g.ldd + cc);
+    }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = col0 + wc + j * 32 + fr;
+    for (int i = 0; i < kDChunks; ++i) {
+      const int c = tid + i * kThreads;
+      const int r = c / (BN / 8), cc = (c % (BN / 8)) * 8;
+      *reinterpret_cast<u32x4*>(E + r * LDE + cc) = dv[i];
+    }
+    __syncthreads();
+  }
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int64_t rbase = row0 + wr + i * 32 + q4 * 8 + (lane >> 5) * 4;
-        float v[4];
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float x = g.alpha * acc[i][j][q4 * 4 + r];
-          if (D) x = __fmaf_rn(g.beta, bf16_bits_to_float(D[(rbase + r) * g.ldd + col]), x);
-          v[r] = x;
-          C[(rbase + r) * g.ldc + col] = (uint16_t)float_to_bf16_bits(x);
-        }
-        if (Ct) {
-          u32x2 t;
-          t.x = pack_bf16x2(v[0], v[1]);
-          t.y = pack_bf16x2(v[2], v[3]);
-          *reinterpret_cast<u32x2*>(Ct + col * g.ldct + rbase) = t;
-        }
+    for (int j = 0; j < 4; ++j) {
+      const int col = wc + j * 32 + fr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wr + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        float x = g.alpha * acc[i][j][r];
+        if (D) x = __fmaf_rn(g.beta, bf16_bits_to_float(E[row * LDE + col]), x);
+        E[row * LDE + col] = (uint16_t)float_to_bf16_bits(x);
       }
+    }
+  }
+  __syncthreads();
+  uint16_t* C = g.C + b * g.sc + row0 * g.ldc + col0;
+  for (int c = tid; c < BM * (BN / 8); c += kThreads) {
+    const int r = c / (BN / 8), cc = (c % (BN / 8)) * 8;
+    *reinterpret_cast<u32x4*>(C + r * g.ldc + cc) = *reinterpret_cast<const u32x4*>(E + r * LDE + cc);
+  }
+  // Transposed copy: Ct, or the mirror tile of a symmetric product.
+  uint16_t* T = nullptr;
+  int64_t ldt = 0;
+  if (g.symmetric) {
+    if (tr != tc) {
+      T = g.C + b * g.sc + col0 * g.ldc + row0;
+      ldt = g.ldc;
+    }
+  } else if (g.Ct) {
+    T = g.Ct + b * g.sct + col0 * g.ldct + row0;
+    ldt = g.ldct;
+  }
+  if (T) {
+    // lane -> (column, 8-row group): a wave reads 64 consecutive columns of one
+    // row group from LDS and writes 64 rows of the transposed tile, 16 B each.
+    for (int c = tid; c < BN * (BM / 8); c += kThreads) {
+      const int col = c % BN, rr = (c / BN) * 8;
+      u32x4 v;
+      v.x = E[(rr + 0) * LDE + col] | ((uint32_t)E[(rr + 1) * LDE + col] << 16);
+      v.y = E[(rr + 2) * LDE + col] | ((uint32_t)E[(rr + 3) * LDE + col] << 16);
+      v.z = E[(rr + 4) * LDE + col] | ((uint32_t)E[(rr + 5) * LDE + col] << 16);
+      v.w = E[(rr + 6) * LDE + col] | ((uint32_t)E[(rr + 7) * LDE + col] << 16);
+      *reinterpret_cast<u32x4*>(T + col * ldt + rr) = v;
     }
   }
 }
@@ -160,24 +281,32 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
                                   int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
                                   int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
                                   int64_t stride_d, int64_t stride_c, int64_t stride_ct,
-                                  float alpha, float beta, void* stream) {
+                                  float alpha, float beta, int symmetric, void* stream) {
   if (P == nullptr || Q == nullptr || C == nullptr || M < 0 || N < 0 || K <= 0 || batch < 0)
     return MORPH_EINVAL;
   auto misaligned = [](const void* p, uintptr_t a) {
     return p != nullptr && (reinterpret_cast<uintptr_t>(p) % a) != 0;
   };
-  if (misaligned(P, 16) || misaligned(Q, 16) || misaligned(Ct, 8) || misaligned(C, 2) ||
-      misaligned(D, 2))
+  if (misaligned(P, 16) || misaligned(Q, 16) || misaligned(C, 16) || misaligned(D, 16) ||
+      misaligned(Ct, 16))
     return MORPH_EINVAL;
-  if (M % BM || N % BN || K % BK) return MORPH_ERANGE;
+  if (M % BM || N % BN || K % MORPH_GEMM_TILE_K) return MORPH_ERANGE;
   if (ldp < K || ldq < K || ldc < N || (D && ldd < N) || (Ct && ldct < M)) return MORPH_EINVAL;
-  if (ldp % 8 || ldq % 8 || stride_p % 8 || stride_q % 8 || (Ct && (ldct % 4 || stride_ct % 4)))
-    return MORPH_EINVAL;  // 16-byte operand loads, 8-byte transposed stores
+  // 16-byte loads and stores of rows: every leading dimension and batch stride a multiple of 8
+  if ((ldp | ldq | ldc | stride_p | stride_q | stride_c) % 8 ||
+      (D && (ldd | stride_d) % 8) || (Ct && (ldct | stride_ct) % 8))
+    return MORPH_EINVAL;
+  if (symmetric && (M != N || Ct != nullptr)) return MORPH_EINVAL;
   if (M == 0 || N == 0 || batch == 0) return MORPH_OK;
-  if (M / BM > 65535 || batch > 65535 || N / BN > (1 << 30)) return MORPH_ERANGE;
-  GemmArgs g{P, Q, D, C, Ct, M, N, K, ldp, ldq, ldd, ldc, ldct,
-             stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta};
-  hipLaunchKernelGGL(gemm_nt_kernel, dim3((unsigned)(N / BN), (unsigned)(M / BM), (unsigned)batch),
-                     dim3(kThreads), 0, as_stream(stream), g);
+  const int64_t tm = M / BM, tn = N / BN;
+  const int64_t per = symmetric ? tm * (tm + 1) / 2 : tm * tn;
+  const int64_t total = batch * per;
+  const int64_t grid = (total + 7) / 8 * 8;
+  if (per > (int64_t(1) << 31) - 1 || grid > (int64_t(1) << 31) - 1) return MORPH_ERANGE;
+  GemmArgs g{P, Q, D, C, Ct, K, ldp, ldq, ldd, ldc, ldct,
+             stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta,
+             (int32_t)tm, (int32_t)tn, (int32_t)per, symmetric ? 1 : 0, total};
+  hipLaunchKernelGGL(gemm_nt_kernel, dim3((unsigned)grid), dim3(kThreads), 0, as_stream(stream),
+                     g);
   return launch_status();
 }

@@ -192,12 +192,6 @@ __global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint1
 
 using namespace morph;
 
-extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D,
-                                  uint16_t* C, uint16_t* Ct, int64_t M, int64_t N, int64_t K,
-                                  int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
-                                  int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
-                                  int64_t stride_d, int64_t stride_c, int64_t stride_ct,
-                                  float alpha, float beta, void* stream);
 
 extern "C" size_t morph_muon_workspace_bytes(int64_t rows, int64_t cols, int count) {
   if (rows <= 0 || cols <= 0 || count <= 0) return 0;
@@ -294,17 +288,18 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
   const int64_t sx = L.mp * L.np, ss = L.mp * L.mp;
   int cur = 0;
   for (int it = 0; it < hp->ns_steps; ++it) {
-    // A = X X^T
+    // A = X X^T (symmetric: upper triangle of tiles, mirrored)
     rc = morph_gemm_nt_bf16(W.X, W.X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, L.np, L.np,
-                            0, L.mp, 0, sx, sx, 0, ss, 0, 1.0f, 0.0f, stream);
+                            0, L.mp, 0, sx, sx, 0, ss, 0, 1.0f, 0.0f, 1, stream);
     if (rc) return rc;
-    // B = c (A A^T) + b A
+    // B = c (A A^T) + b A (symmetric)
     rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, L.mp, L.mp,
-                            L.mp, L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b, stream);
+                            L.mp, L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b, 1, stream);
     if (rc) return rc;
     // X' = (B Xt^T) + a X, written in place over X and transposed into the other Xt
     rc = morph_gemm_nt_bf16(W.B, W.Xt[cur], W.X, W.X, W.Xt[cur ^ 1], L.mp, L.np, L.mp, count,
-                            L.mp, L.mp, L.np, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a, stream);
+                            L.mp, L.mp, L.np, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a, 0,
+                            stream);
     if (rc) return rc;
     cur ^= 1;
   }

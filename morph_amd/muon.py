@@ -29,11 +29,14 @@ def _bf16_ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, stream=None):
+def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, symmetric=False,
+            stream=None):
     """out = alpha * P @ Q^T + beta * D (bf16, fp32 accumulation); out_t = out^T if given.
 
     P [.., M, K], Q [.., N, K], D/out [.., M, N], out_t [.., N, M]; a leading batch
-    dimension is optional.  M, N multiples of 128 and K of 64.
+    dimension is optional.  M, N multiples of 256 and K of 64.  symmetric=True:
+    the result is known to be symmetric (M == N, D symmetric): only the upper
+    triangle of tiles is computed and mirrored.
     """
     batched = P.dim() == 3
     if not batched:
@@ -54,7 +57,7 @@ def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, stream=None
     check(lib().morph_gemm_nt_bf16(
         _bf16_ptr(P), _bf16_ptr(Q), _bf16_ptr(D), _bf16_ptr(out), _bf16_ptr(out_t),
         M, N, K, b, K, K, N, N, M, M * K, N * K, M * N, M * N, N * M,
-        float(alpha), float(beta), stream_handle(stream)))
+        float(alpha), float(beta), int(bool(symmetric)), stream_handle(stream)))
     return out if batched else out[0]
 
 

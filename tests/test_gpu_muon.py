@@ -31,7 +31,7 @@ def rand_bf16(shape, seed, scale=1.0):
     return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
 
 
-@pytest.mark.parametrize("b,M,N,K", [(1, 128, 128, 64), (3, 256, 384, 192), (2, 384, 128, 512)])
+@pytest.mark.parametrize("b,M,N,K", [(1, 256, 256, 64), (3, 512, 768, 192), (2, 768, 256, 512)])
 def test_gemm_nt_against_exact_product(b, M, N, K):
     P, Q, D = rand_bf16((b, M, K), 1), rand_bf16((b, N, K), 2), rand_bf16((b, M, N), 3)
     alpha, beta = 2.0315, -4.775
@@ -48,11 +48,32 @@ def test_gemm_nt_against_exact_product(b, M, N, K):
 
 def test_gemm_nt_in_place_output_over_D():
     """D may alias C (the X' = a X + B X step writes over X)."""
-    P, Q = rand_bf16((128, 128), 4).to(DEV), rand_bf16((256, 128), 5).to(DEV)
-    X = rand_bf16((128, 256), 6).to(DEV)
+    P, Q = rand_bf16((256, 256), 4).to(DEV), rand_bf16((512, 256), 5).to(DEV)
+    X = rand_bf16((256, 512), 6).to(DEV)
     expect = muon.gemm_nt(P, Q, X.clone(), 1.0, 3.4445)
     muon.gemm_nt(P, Q, X, 1.0, 3.4445, out=X)
     assert torch.equal(X, expect)
+
+
+@pytest.mark.parametrize("b,M,K", [(1, 256, 64), (2, 1024, 320), (3, 768, 768)])
+def test_gemm_nt_symmetric_mode(b, M, K):
+    """Upper-triangle tiles + mirror: exactly symmetric, equal to the full product's bound,
+    and the upper triangle equals the full computation bit for bit."""
+    X = rand_bf16((b, M, K), 7).to(DEV)
+    full = muon.gemm_nt(X, X)
+    sym = muon.gemm_nt(X, X, symmetric=True)
+    assert torch.equal(sym, sym.transpose(1, 2))
+    upper = torch.triu(torch.ones(M // 256, M // 256, dtype=torch.bool)).repeat_interleave(
+        256, 0).repeat_interleave(256, 1).to(DEV)
+    assert torch.equal(sym[:, upper], full[:, upper])
+    # with a symmetric D and alpha/beta, as in B = c A A^T + b A
+    A = sym
+    B = muon.gemm_nt(A, A, A, 2.0315, -4.775, symmetric=True)
+    Ad = A.double().cpu()
+    exact = 2.0315 * Ad @ Ad.transpose(1, 2) - 4.775 * Ad
+    mag = 2.0315 * Ad.abs() @ Ad.abs().transpose(1, 2) + 4.775 * Ad.abs()
+    assert ((B.double().cpu() - exact).abs() <= 2 ** -8 * exact.abs() + 1e-6 * M * mag).all()
+    assert torch.equal(B, B.transpose(1, 2))
 
 
 def test_orthogonalize_diagonal_closed_form():
