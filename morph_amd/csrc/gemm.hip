@@ -130,19 +130,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
   // DMA assignment: wave w, load j covers rows (w * 4 + j) * 16 .. +16 of a sub-tile;
   // lane l -> row base + l / 4, LDS slot l % 4 holding global chunk slot ^ swz(row).
   const int lrow = lane >> 2, lslot = lane & 3;
+  // DMA load j (0..7) of a stage: operand j & 1 (P, Q), 16-row block j >> 1 of this wave.
+  auto issue_load = [&](int buf, int64_t k0, int j) {
+    const int blk = wave * kLoadsPerOperand + (j >> 1);
+    const int r = blk * 16 + lrow;
+    const int c = lslot ^ ((r >> 2) & 3);
+    uint16_t* dst = smem + buf * kStageElems + (j & 1) * kSubTile + blk * 16 * BKS;
+    const uint16_t* src = (j & 1) ? Q + r * g.ldq : P + r * g.ldp;
+    __builtin_amdgcn_global_load_lds(src + k0 + c * 8, (lds_void*)dst, 16, 0, 0);
+  };
   auto issue_stage = [&](int buf, int64_t k0) {
-    uint16_t* sP = smem + buf * kStageElems;
-    uint16_t* sQ = sP + kSubTile;
 #pragma unroll
-    for (int j = 0; j < kLoadsPerOperand; ++j) {
-      const int r = (wave * kLoadsPerOperand + j) * 16 + lrow;
-      const int c = lslot ^ ((r >> 2) & 3);
-      const int lds_off = (wave * kLoadsPerOperand + j) * 16 * BKS;  // 1 KiB per instruction
-      __builtin_amdgcn_global_load_lds(P + r * g.ldp + k0 + c * 8, (lds_void*)(sP + lds_off), 16,
-                                       0, 0);
-      __builtin_amdgcn_global_load_lds(Q + r * g.ldq + k0 + c * 8, (lds_void*)(sQ + lds_off), 16,
-                                       0, 0);
-    }
+    for (int j = 0; j < 2 * kLoadsPerOperand; ++j) issue_load(buf, k0, j);
   };
 
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
@@ -158,49 +157,89 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     return *reinterpret_cast<const bf16x8*>(sub + R * BKS + ((c ^ ((R >> 2) & 3)) * 8));
   };
 
-  const int64_t KT = g.K / BKS;
-  for (int s = 0; s < kStages - 1; ++s)
-    if (s < KT) issue_stage(s, (int64_t)s * BKS);
-  for (int64_t kt = 0; kt < KT; ++kt) {
-    // this wave's DMA for stage kt is complete once at most the later stages'
-    // 2 * kLoadsPerOperand loads each are outstanding
-    const int64_t later = (KT - 1 - kt) < (kStages - 2) ? (KT - 1 - kt) : (kStages - 2);
-    if (later >= 2)
-      __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
-    else if (later == 1)
-      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
-    else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();  // every wave's DMA for stage kt landed; stage kt - 1 is consumed
-    if (kt + kStages - 1 < KT)
-      issue_stage((int)((kt + kStages - 1) % kStages), (kt + kStages - 1) * BKS);
-    const uint16_t* sP = smem + (int)(kt % kStages) * kStageElems;
+  // Workgroup barrier for LDS only: the memory clobber keeps the compiler from
+  // moving LDS accesses across it and no vmcnt wait is attached, so younger
+  // stages stay in flight (__syncthreads would drain every outstanding load).
+  auto lds_barrier = []() { asm volatile("s_barrier" ::: "memory"); };
+  auto read_frags = [&](int stage, bf16x8 (&a)[BKS / 16][4], bf16x8 (&q)[BKS / 16][4]) {
+    const uint16_t* sP = smem + stage * kStageElems;
     const uint16_t* sQ = sP + kSubTile;
-    // Fragment reads of both k halves are issued before the first MFMA (the
-    // second half's reads then overlap the first half's MFMAs), so LDS latency
-    // is paid about once per stage instead of once per fragment.
-    bf16x8 a[BKS / 16][4], q[BKS / 16][4];
 #pragma unroll
-    for (int kk = 0; kk < BKS / 16; ++kk) {
+    for (int kk = 0; kk < BKS / 16; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         a[kk][i] = frag(sP, wr + i * 32 + fr, kk * 2 + fh);
         q[kk][i] = frag(sQ, wc + i * 32 + fr, kk * 2 + fh);
       }
+  };
+  auto mfma = [&](int n, const bf16x8 (&ca)[BKS / 16][4], const bf16x8 (&cq)[BKS / 16][4]) {
+    const int kk = n >> 4, i = (n >> 2) & 3, j = n & 3;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[kk][i], cq[kk][j], acc[i][j], 0, 0, 0);
+  };
+
+  // Pipeline: kStages LDS buffers plus one register stage.  At step kt the
+  // registers hold stage kt, buffer (kt + 1) % kStages holds stage kt + 1 and
+  // the two after it are in flight.  After the barrier the buffer of stage kt
+  // is refilled with stage kt + kStages (past the end: the last stage again, so
+  // every step keeps the same number of loads in flight and has no branch),
+  // and the LDS reads of stage kt + 1 run under the 32 MFMAs of stage kt.
+  // The scheduling barriers pin that order: without them the compiler is free
+  // to hoist the final LDS wait above the MFMAs.
+  const int64_t KT = g.K / BKS;  // even, >= 2
+  auto issue = [&](int buf, int64_t stage) {
+    issue_stage(buf, (stage < KT ? stage : KT - 1) * BKS);
+  };
+  for (int s = 0; s < kStages; ++s) issue(s, s);
+  __builtin_amdgcn_s_waitcnt(0x4F78);  // vmcnt(24): stage 0 landed
+  lds_barrier();
+  bf16x8 a0[BKS / 16][4], q0[BKS / 16][4], a1[BKS / 16][4], q1[BKS / 16][4];
+  read_frags(0, a0, q0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+
+  auto step = [&](int64_t kt, const bf16x8 (&ca)[BKS / 16][4], const bf16x8 (&cq)[BKS / 16][4],
+                  bf16x8 (&na)[BKS / 16][4], bf16x8 (&nq)[BKS / 16][4]) {
+    // Two MFMAs of the registered stage go first so the unit is busy across
+    // the barrier; then one LDS fragment read or one DMA issue per MFMA.
+    mfma(0, ca, cq);
+    mfma(1, ca, cq);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): stage kt + 1 landed for this wave
+    lds_barrier();
+    const uint16_t* sP = smem + (int)((kt + 1) % kStages) * kStageElems;
+    const uint16_t* sQ = sP + kSubTile;
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+      mfma(n + 2, ca, cq);
+      __builtin_amdgcn_sched_barrier(0);
+      const int kk = n >> 3, i = (n >> 1) & 3;
+      if (n & 1)
+        nq[kk][i] = frag(sQ, wc + i * 32 + fr, kk * 2 + fh);
+      else
+        na[kk][i] = frag(sP, wr + i * 32 + fr, kk * 2 + fh);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int64_t next = kt + kStages;
+    const int64_t k0 = (next < KT ? next : KT - 1) * BKS;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      mfma(j + 18, ca, cq);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_load((int)(kt % kStages), k0, j);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int kk = 0; kk < BKS / 16; ++kk) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk][i], q[kk][j], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+    for (int n = 26; n < 32; ++n) mfma(n, ca, cq);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage kt + 1 is in registers
+  };
+  for (int64_t kt = 0; kt + 2 < KT; kt += 2) {
+    step(kt, a0, q0, a1, q1);
+    step(kt + 1, a1, q1, a0, q0);
   }
-  __syncthreads();  // all fragment reads done before the epilogue reuses the LDS
+  step(KT - 2, a0, q0, a1, q1);
+#pragma unroll
+  for (int n = 0; n < 32; ++n) mfma(n, a1, q1);
+  __syncthreads();  // all fragment reads and trailing loads done before the epilogue reuses the LDS
 
   // ---- epilogue through LDS --------------------------------------------------
   uint16_t* E = smem;  // [BM][LDE] bf16 output tile
