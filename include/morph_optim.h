@@ -224,6 +224,10 @@ int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* 
 #define MORPH_GEMM_TILE_N 256
 #define MORPH_GEMM_TILE_K 64
 
+/* Flags of morph_gemm_nt_bf16. */
+#define MORPH_GEMM_SYMMETRIC 1    /* C symmetric: compute the upper triangle of tiles, mirror */
+#define MORPH_GEMM_D_TRANSPOSED 2 /* D is passed as D^T: [N, M] row-major, leading dim ldd */
+
 /*
  * Batched bf16 GEMM, "NT" layout, fp32 accumulation:
  *   C[b] = alpha * P[b] . Q[b]^T + beta * D[b];   Ct[b] = C[b]^T if Ct != NULL
@@ -232,17 +236,18 @@ int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* 
  * D may be NULL (beta ignored) and may alias C.  Each output element is
  * rounded once (RNE) from fp32.  The three products of one Newton-Schulz
  * iteration of optimizer.py:19-21 are all of this form (see gemm.hip).
- * symmetric != 0 (requires M == N, Ct == NULL, and D symmetric if given): C
- * is known to be symmetric, so only the upper triangle of tiles is computed
- * and each off-diagonal tile is mirrored.  Pointers 16-byte aligned, leading
- * dimensions and strides multiples of 8; MORPH_ERANGE when a dimension is not
- * a tile multiple.
+ * flags: MORPH_GEMM_SYMMETRIC (requires M == N, Ct == NULL, and D symmetric
+ * if given): C is known to be symmetric, so only the upper triangle of tiles
+ * is computed and each off-diagonal tile is mirrored.  MORPH_GEMM_D_TRANSPOSED:
+ * D points at D^T ([N, M], ldd >= M), the layout the kernel reads fastest.
+ * Pointers 16-byte aligned, leading dimensions and strides multiples of 8;
+ * MORPH_ERANGE when a dimension is not a tile multiple.
  */
 int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D, uint16_t* C,
                        uint16_t* Ct, int64_t M, int64_t N, int64_t K, int64_t batch,
                        int64_t ldp, int64_t ldq, int64_t ldd, int64_t ldc, int64_t ldct,
                        int64_t stride_p, int64_t stride_q, int64_t stride_d, int64_t stride_c,
-                       int64_t stride_ct, float alpha, float beta, int symmetric, void* stream);
+                       int64_t stride_ct, float alpha, float beta, int flags, void* stream);
 
 /* One Muon matrix: FP32 [rows, cols] row-major device buffers. */
 typedef struct morph_muon_matrix {

@@ -15,12 +15,13 @@
 // step a wave reads 8 fragments (8 KiB) from LDS for 16 MFMAs.
 //
 // Operand pipeline.  K advances 32 per stage through a ring of kStages LDS
-// buffers (32 KiB each: P and Q sub-tiles of 256 x 32 bf16).  Operands go
-// global -> LDS directly (global_load_lds_dwordx4: lane l's 16 bytes land at
-// the instruction's LDS base + 16 l), so no registers are spent on staging and
-// kStages - 1 stages are in flight while one is consumed -- about 3000 MFMA
-// cycles to cover the L2 / fabric latency.  One barrier per stage: after it,
-// the stage just consumed is refilled with the one kStages - 1 ahead.
+// buffers (32 KiB each: P and Q sub-tiles of 256 x 32 bf16) plus one stage of
+// fragments in registers.  Operands go global -> LDS directly
+// (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS
+// base + 16 l), so no registers are spent on staging; a stage is issued three
+// steps before it is read (about 3000 MFMA cycles of cover).  One LDS-only
+// barrier per stage; the fragment reads of the next stage and the DMA issue of
+// a later one are interleaved one per MFMA with the current stage's MFMAs.
 // Because the DMA writes LDS linearly, rows cannot be padded; instead the four
 // 16-byte chunks of each 64-byte row are stored XOR-swizzled (slot = chunk ^
 // ((row >> 2) & 3)), chosen on the load side by which global chunk each lane
@@ -37,10 +38,14 @@
 // with tile_row <= tile_col run, and each off-diagonal tile is also written
 // transposed into the mirror position, halving the work of those products.
 //
-// Epilogue.  After the K loop the LDS holds the output tile: D is loaded into
-// it with coalesced 16-byte reads, each lane combines alpha * acc + beta * D in
-// fp32, rounds once to bf16 and writes back; then C (and Ct / the mirror tile)
-// leave with coalesced 16-byte stores.
+// Epilogue.  Each lane combines alpha * acc + beta * D in fp32 and rounds once
+// to bf16.  In the MFMA output layout four consecutive registers of a lane are
+// four consecutive rows of one column, i.e. 8 contiguous bytes of a row of the
+// transposed tile: Ct, the mirror tile of a symmetric product and a D given
+// transposed (MORPH_GEMM_D_TRANSPOSED) move straight between registers and
+// memory.  The row-major C (and a D given row-major) pass through an LDS copy
+// of the tile for coalesced 16-byte rows.  Loads are issued in batches ahead of
+// their use so the epilogue pays memory latency a few times, not per element.
 //
 // MFMA 32x32x16 lane layout (checked on the device): lane l holds
 // A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32] for i < 8; output
@@ -83,13 +88,13 @@ struct GemmArgs {
   float alpha, beta;
   int32_t tiles_m, tiles_n;
   int32_t tiles_per_matrix;  // tiles_m * tiles_n, or the upper triangle when symmetric
-  int32_t symmetric;
+  int32_t flags;             // MORPH_GEMM_SYMMETRIC | MORPH_GEMM_D_TRANSPOSED
   int64_t total_tiles;       // batch * tiles_per_matrix
 };
 
 // Tile (row, col) of the t-th tile of one matrix.
 __device__ __forceinline__ void tile_of(const GemmArgs& g, int t, int& tr, int& tc) {
-  if (g.symmetric) {  // upper triangle, row by row
+  if (g.flags & MORPH_GEMM_SYMMETRIC) {  // upper triangle, row by row
     int r = 0;
     while (t >= g.tiles_n - r) {
       t -= g.tiles_n - r;
@@ -106,6 +111,110 @@ __device__ __forceinline__ void tile_of(const GemmArgs& g, int t, int& tr, int& 
   const int rows = min(kGroupM, g.tiles_m - first);
   tc = within / rows;
   tr = first + within % rows;
+}
+
+enum DMode { kNoD, kDRowMajor, kDTransposed };
+
+// Epilogue of one tile.  acc[i][j][r] of lane (fh, fr) of wave (wr, wc) is tile
+// element (wr + 32 i + 8 (r / 4) + 4 fh + r % 4, wc + 32 j + fr).  The D mode
+// is a template parameter so that each variant is straight-line code (the
+// 128 registers of a transposed D must not be live across branches).
+template <int kDMode>
+__device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4],
+                                         uint16_t* smem, const uint16_t* D, uint16_t* C,
+                                         uint16_t* T, int64_t ldt) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
+  const int fr = lane & 31, fh = lane >> 5;
+  uint16_t* E = smem;  // [BM][LDE] bf16 copy of the output tile
+  const uint32_t ldd = (uint32_t)g.ldd, lt = (uint32_t)ldt;
+
+  // Transposed D: every value this lane needs, 4 rows per 8-byte load, all
+  // issued before the first store (a store to C or T may alias D).
+  u32x2 dt[4][4][4];
+  if (kDMode == kDTransposed) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          dt[i][j][q] = *reinterpret_cast<const u32x2*>(
+              D + ((uint32_t)(wc + j * 32 + fr) * ldd + (uint32_t)(wr + i * 32 + q * 8 + fh * 4)));
+  }
+  if (kDMode == kDRowMajor) {
+    // Row-major D into the LDS tile, all 32 loads of a lane in flight at once.
+    constexpr int kDChunks = BM * (BN / 8) / kThreads;
+    u32x4 dv[kDChunks];
+#pragma unroll
+    for (int i = 0; i < kDChunks; ++i) {
+      const int c = tid + i * kThreads;
+      dv[i] = *reinterpret_cast<const u32x4*>(D + (uint32_t)(c / (BN / 8)) * ldd + (c % (BN / 8)) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < kDChunks; ++i) {
+      const int c = tid + i * kThreads;
+      *reinterpret_cast<u32x4*>(E + (c / (BN / 8)) * LDE + (c % (BN / 8)) * 8) = dv[i];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = wc + j * 32 + fr;
+      const int rbase = wr + i * 32 + fh * 4;
+      float dval[16];
+      if (kDMode == kDTransposed) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          dval[4 * q + 0] = bf16_bits_to_float(dt[i][j][q].x & 0xFFFFu);
+          dval[4 * q + 1] = bf16_bits_to_float(dt[i][j][q].x >> 16);
+          dval[4 * q + 2] = bf16_bits_to_float(dt[i][j][q].y & 0xFFFFu);
+          dval[4 * q + 3] = bf16_bits_to_float(dt[i][j][q].y >> 16);
+        }
+      } else if (kDMode == kDRowMajor) {
+        // all 16 reads of the block before its writes: one LDS round trip
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          dval[r] = bf16_bits_to_float(E[(rbase + (r >> 2) * 8 + (r & 3)) * LDE + col]);
+      }
+      uint32_t bits[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = g.alpha * acc[i][j][r];
+        if (kDMode != kNoD) x = __fmaf_rn(g.beta, dval[r], x);
+        bits[r] = float_to_bf16_bits(x);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        E[(rbase + (r >> 2) * 8 + (r & 3)) * LDE + col] = (uint16_t)bits[r];
+      if (T) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x2 v;
+          v.x = bits[4 * q] | (bits[4 * q + 1] << 16);
+          v.y = bits[4 * q + 2] | (bits[4 * q + 3] << 16);
+          *reinterpret_cast<u32x2*>(T + ((uint32_t)col * lt + (uint32_t)(rbase + q * 8))) = v;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // C rows from the LDS tile: all 32 reads of a lane, then the 32 stores.
+  constexpr int kCChunks = BM * (BN / 8) / kThreads;
+  const uint32_t ldc = (uint32_t)g.ldc;
+  u32x4 cv[kCChunks];
+#pragma unroll
+  for (int i = 0; i < kCChunks; ++i) {
+    const int c = tid + i * kThreads;
+    cv[i] = *reinterpret_cast<const u32x4*>(E + (c / (BN / 8)) * LDE + (c % (BN / 8)) * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < kCChunks; ++i) {
+    const int c = tid + i * kThreads;
+    *reinterpret_cast<u32x4*>(C + ((uint32_t)(c / (BN / 8)) * ldc + (c % (BN / 8)) * 8)) = cv[i];
+  }
 }
 
 __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) {
@@ -241,52 +350,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
   for (int n = 0; n < 32; ++n) mfma(n, a1, q1);
   __syncthreads();  // all fragment reads and trailing loads done before the epilogue reuses the LDS
 
-  // ---- epilogue through LDS --------------------------------------------------
-  uint16_t* E = smem;  // [BM][LDE] bf16 output tile
-  const uint16_t* D = g.D ? g.D + b * g.sd + row0 * g.ldd + col0 : nullptr;
-  if (D) {
-    // All 32 loads of a lane are in flight before the first LDS write (a
-    // load-then-write loop would pay the memory latency 32 times per tile).
-    constexpr int kDChunks = BM * (BN / 8) / kThreads;
-    u32x4 dv[kDChunks];
-#pragma unroll
-    for (int i = 0; i < kDChunks; ++i) {
-      const int c = tid + i * kThreads;
-      const int r = c / (BN / 8), cc = (c % (BN / 8)) * 8;
-      dv[i] = *reinterpret_cast<const u32x4*>(D + r * g.ldd + cc);
-    }
-#pragma unroll
-    for (int i = 0; i < kDChunks; ++i) {
-      const int c = tid + i * kThreads;
-      const int r = c / (BN / 8), cc = (c % (BN / 8)) * 8;
-      *reinterpret_cast<u32x4*>(E + r * LDE + cc) = dv[i];
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = wc + j * 32 + fr;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = wr + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-        float x = g.alpha * acc[i][j][r];
-        if (D) x = __fmaf_rn(g.beta, bf16_bits_to_float(E[row * LDE + col]), x);
-        E[row * LDE + col] = (uint16_t)float_to_bf16_bits(x);
-      }
-    }
-  }
-  __syncthreads();
-  uint16_t* C = g.C + b * g.sc + row0 * g.ldc + col0;
-  for (int c = tid; c < BM * (BN / 8); c += kThreads) {
-    const int r = c / (BN / 8), cc = (c % (BN / 8)) * 8;
-    *reinterpret_cast<u32x4*>(C + r * g.ldc + cc) = *reinterpret_cast<const u32x4*>(E + r * LDE + cc);
-  }
-  // Transposed copy: Ct, or the mirror tile of a symmetric product.
-  uint16_t* T = nullptr;
+  // ---- epilogue ------------------------------------------------------------
+  const uint16_t* D = nullptr;
+  const bool d_t = (g.flags & MORPH_GEMM_D_TRANSPOSED) != 0;
+  if (g.D) D = g.D + b * g.sd + (d_t ? col0 * g.ldd + row0 : row0 * g.ldd + col0);
+  uint16_t* T = nullptr;  // transposed destination: Ct, or the mirror tile
   int64_t ldt = 0;
-  if (g.symmetric) {
+  if (g.flags & MORPH_GEMM_SYMMETRIC) {
     if (tr != tc) {
       T = g.C + b * g.sc + col0 * g.ldc + row0;
       ldt = g.ldc;
@@ -295,19 +365,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     T = g.Ct + b * g.sct + col0 * g.ldct + row0;
     ldt = g.ldct;
   }
-  if (T) {
-    // lane -> (column, 8-row group): a wave reads 64 consecutive columns of one
-    // row group from LDS and writes 64 rows of the transposed tile, 16 B each.
-    for (int c = tid; c < BN * (BM / 8); c += kThreads) {
-      const int col = c % BN, rr = (c / BN) * 8;
-      u32x4 v;
-      v.x = E[(rr + 0) * LDE + col] | ((uint32_t)E[(rr + 1) * LDE + col] << 16);
-      v.y = E[(rr + 2) * LDE + col] | ((uint32_t)E[(rr + 3) * LDE + col] << 16);
-      v.z = E[(rr + 4) * LDE + col] | ((uint32_t)E[(rr + 5) * LDE + col] << 16);
-      v.w = E[(rr + 6) * LDE + col] | ((uint32_t)E[(rr + 7) * LDE + col] << 16);
-      *reinterpret_cast<u32x4*>(T + col * ldt + rr) = v;
-    }
-  }
+  uint16_t* C = g.C + b * g.sc + row0 * g.ldc + col0;
+  if (D == nullptr)
+    epilogue<kNoD>(g, acc, smem, nullptr, C, T, ldt);
+  else if (d_t)
+    epilogue<kDTransposed>(g, acc, smem, D, C, T, ldt);
+  else
+    epilogue<kDRowMajor>(g, acc, smem, D, C, T, ldt);
 }
 
 }  // namespace
@@ -320,7 +384,7 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
                                   int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
                                   int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
                                   int64_t stride_d, int64_t stride_c, int64_t stride_ct,
-                                  float alpha, float beta, int symmetric, void* stream) {
+                                  float alpha, float beta, int flags, void* stream) {
   if (P == nullptr || Q == nullptr || C == nullptr || M < 0 || N < 0 || K <= 0 || batch < 0)
     return MORPH_EINVAL;
   auto misaligned = [](const void* p, uintptr_t a) {
@@ -330,12 +394,18 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
       misaligned(Ct, 16))
     return MORPH_EINVAL;
   if (M % BM || N % BN || K % MORPH_GEMM_TILE_K) return MORPH_ERANGE;
-  if (ldp < K || ldq < K || ldc < N || (D && ldd < N) || (Ct && ldct < M)) return MORPH_EINVAL;
+  if (flags & ~(MORPH_GEMM_SYMMETRIC | MORPH_GEMM_D_TRANSPOSED)) return MORPH_EINVAL;
+  const bool symmetric = (flags & MORPH_GEMM_SYMMETRIC) != 0;
+  const int64_t d_cols = (flags & MORPH_GEMM_D_TRANSPOSED) ? M : N;  // D stored [M, N] or [N, M]
+  if (ldp < K || ldq < K || ldc < N || (D && ldd < d_cols) || (Ct && ldct < M)) return MORPH_EINVAL;
   // 16-byte loads and stores of rows: every leading dimension and batch stride a multiple of 8
   if ((ldp | ldq | ldc | stride_p | stride_q | stride_c) % 8 ||
       (D && (ldd | stride_d) % 8) || (Ct && (ldct | stride_ct) % 8))
     return MORPH_EINVAL;
   if (symmetric && (M != N || Ct != nullptr)) return MORPH_EINVAL;
+  // epilogue offsets inside a tile are 32-bit: 255 rows of the widest leading dimension
+  constexpr int64_t kMaxLd = int64_t(1) << 23;
+  if (ldc > kMaxLd || (D && ldd > kMaxLd) || (Ct && ldct > kMaxLd)) return MORPH_ERANGE;
   if (M == 0 || N == 0 || batch == 0) return MORPH_OK;
   const int64_t tm = M / BM, tn = N / BN;
   const int64_t per = symmetric ? tm * (tm + 1) / 2 : tm * tn;
@@ -344,7 +414,7 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
   if (per > (int64_t(1) << 31) - 1 || grid > (int64_t(1) << 31) - 1) return MORPH_ERANGE;
   GemmArgs g{P, Q, D, C, Ct, K, ldp, ldq, ldd, ldc, ldct,
              stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta,
-             (int32_t)tm, (int32_t)tn, (int32_t)per, symmetric ? 1 : 0, total};
+             (int32_t)tm, (int32_t)tn, (int32_t)per, flags, total};
   hipLaunchKernelGGL(gemm_nt_kernel, dim3((unsigned)grid), dim3(kThreads), 0, as_stream(stream),
                      g);
   return launch_status();

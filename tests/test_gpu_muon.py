@@ -46,6 +46,23 @@ def test_gemm_nt_against_exact_product(b, M, N, K):
     assert torch.equal(out_t.cpu(), C.transpose(1, 2))
 
 
+@pytest.mark.parametrize("b,M,N,K", [(1, 256, 256, 64), (2, 512, 768, 192), (1, 768, 512, 256)])
+def test_gemm_nt_transposed_D_equals_row_major_D(b, M, N, K):
+    """MORPH_GEMM_D_TRANSPOSED reads D^T; the result is bit-identical to passing D,
+    with and without the transposed output."""
+    P, Q, D = rand_bf16((b, M, K), 11).to(DEV), rand_bf16((b, N, K), 12).to(DEV), \
+        rand_bf16((b, M, N), 13).to(DEV)
+    Dt = D.transpose(1, 2).contiguous()
+    for with_t in (False, True):
+        t0 = torch.empty((b, N, M), dtype=torch.bfloat16, device=DEV) if with_t else None
+        t1 = torch.empty((b, N, M), dtype=torch.bfloat16, device=DEV) if with_t else None
+        ref = muon.gemm_nt(P, Q, D, 1.0, 3.4445, out_t=t0)
+        got = muon.gemm_nt(P, Q, Dt, 1.0, 3.4445, out_t=t1, d_transposed=True)
+        assert torch.equal(got, ref)
+        if with_t:
+            assert torch.equal(t1, t0) and torch.equal(t1, got.transpose(1, 2))
+
+
 def test_gemm_nt_in_place_output_over_D():
     """D may alias C (the X' = a X + B X step writes over X)."""
     P, Q = rand_bf16((256, 256), 4).to(DEV), rand_bf16((512, 256), 5).to(DEV)
