@@ -225,8 +225,7 @@ int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* 
 #define MORPH_GEMM_TILE_K 64
 
 /* Flags of morph_gemm_nt_bf16. */
-#define MORPH_GEMM_SYMMETRIC 1    /* C symmetric: compute the upper triangle of tiles, mirror */
-#define MORPH_GEMM_D_TRANSPOSED 2 /* D is passed as D^T: [N, M] row-major, leading dim ldd */
+#define MORPH_GEMM_SYMMETRIC 1 /* C symmetric: compute the upper triangle of tiles, mirror */
 
 /*
  * Batched bf16 GEMM, "NT" layout, fp32 accumulation:
@@ -238,9 +237,7 @@ int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* 
  * iteration of optimizer.py:19-21 are all of this form (see gemm.hip).
  * flags: MORPH_GEMM_SYMMETRIC (requires M == N, Ct == NULL, and D symmetric
  * if given): C is known to be symmetric, so only the upper triangle of tiles
- * is computed and each off-diagonal tile is mirrored.  MORPH_GEMM_D_TRANSPOSED:
- * D points at D^T ([N, M], ldd >= M), the layout the kernel reads fastest.
- * Pointers 16-byte aligned, leading dimensions and strides multiples of 8;
+ * is computed and each off-diagonal tile is mirrored.  Pointers 16-byte aligned, leading dimensions and strides multiples of 8;
  * MORPH_ERANGE when a dimension is not a tile multiple.
  */
 int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D, uint16_t* C,

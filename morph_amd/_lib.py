@@ -27,7 +27,7 @@ EXPORTS = (
     "morph_muon_prepare", "morph_muon_newton_schulz", "morph_muon_finish",
 )
 GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 256, 256, 64
-GEMM_SYMMETRIC, GEMM_D_TRANSPOSED = 1, 2
+GEMM_SYMMETRIC = 1
 FATAL_MIN_SCALE = 1
 
 

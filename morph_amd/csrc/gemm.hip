@@ -39,13 +39,13 @@
 // transposed into the mirror position, halving the work of those products.
 //
 // Epilogue.  Each lane combines alpha * acc + beta * D in fp32 and rounds once
-// to bf16.  In the MFMA output layout four consecutive registers of a lane are
-// four consecutive rows of one column, i.e. 8 contiguous bytes of a row of the
-// transposed tile: Ct, the mirror tile of a symmetric product and a D given
-// transposed (MORPH_GEMM_D_TRANSPOSED) move straight between registers and
-// memory.  The row-major C (and a D given row-major) pass through an LDS copy
-// of the tile for coalesced 16-byte rows.  Loads are issued in batches ahead of
-// their use so the epilogue pays memory latency a few times, not per element.
+// to bf16 (packed converter, round to nearest even).  In the MFMA output layout
+// four consecutive registers of a lane are four consecutive rows of one
+// column, i.e. 8 contiguous bytes of a row of the transposed tile: Ct and the
+// mirror tile of a symmetric product are stored straight from registers.  The
+// row-major C and D pass through an LDS copy of the tile for coalesced 16-byte
+// rows.  Loads are issued in batches ahead of their use so the epilogue pays
+// memory latency a few times, not per element.
 //
 // MFMA 32x32x16 lane layout (checked on the device): lane l holds
 // A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32] for i < 8; output
@@ -75,6 +75,15 @@ constexpr int kGroupM = 4;
 static_assert(BM == BN && BM == 256 && MORPH_GEMM_TILE_K % BKS == 0, "256 x 256 tiles, K % 32");
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> packed bf16 (a in the low half), one v_cvt_pk_bf16_f32:
+// round to nearest even, the same bits as float_to_bf16_bits for every
+// non-NaN input (NaN payloads may differ; both stay NaN).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
 
 struct GemmArgs {
   const uint16_t* P;
@@ -88,7 +97,7 @@ struct GemmArgs {
   float alpha, beta;
   int32_t tiles_m, tiles_n;
   int32_t tiles_per_matrix;  // tiles_m * tiles_n, or the upper triangle when symmetric
-  int32_t flags;             // MORPH_GEMM_SYMMETRIC | MORPH_GEMM_D_TRANSPOSED
+  int32_t flags;             // MORPH_GEMM_SYMMETRIC
   int64_t total_tiles;       // batch * tiles_per_matrix
 };
 
@@ -113,13 +122,13 @@ __device__ __forceinline__ void tile_of(const GemmArgs& g, int t, int& tr, int& 
   tr = first + within % rows;
 }
 
-enum DMode { kNoD, kDRowMajor, kDTransposed };
+enum DMode { kNoD, kDRowMajor };
 
 // Epilogue of one tile.  acc[i][j][r] of lane (fh, fr) of wave (wr, wc) is tile
 // element (wr + 32 i + 8 (r / 4) + 4 fh + r % 4, wc + 32 j + fr).  The D mode
-// is a template parameter so that each variant is straight-line code (the
-// 128 registers of a transposed D must not be live across branches).
-template <int kDMode>
+// and the alpha multiply are template parameters so that each variant is
+// straight-line code.
+template <int kDMode, bool kScaled>
 __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4],
                                          uint16_t* smem, const uint16_t* D, uint16_t* C,
                                          uint16_t* T, int64_t ldt) {
@@ -129,19 +138,6 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
   uint16_t* E = smem;  // [BM][LDE] bf16 copy of the output tile
   const uint32_t ldd = (uint32_t)g.ldd, lt = (uint32_t)ldt;
 
-  // Transposed D: every value this lane needs, 4 rows per 8-byte load, all
-  // issued before the first store (a store to C or T may alias D).
-  u32x2 dt[4][4][4];
-  if (kDMode == kDTransposed) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          dt[i][j][q] = *reinterpret_cast<const u32x2*>(
-              D + ((uint32_t)(wc + j * 32 + fr) * ldd + (uint32_t)(wr + i * 32 + q * 8 + fh * 4)));
-  }
   if (kDMode == kDRowMajor) {
     // Row-major D into the LDS tile, all 32 loads of a lane in flight at once.
     constexpr int kDChunks = BM * (BN / 8) / kThreads;
@@ -158,6 +154,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
     }
     __syncthreads();
   }
+  // Per element: (alpha *) acc, fma with beta * D, one RNE rounding to bf16 by
+  // the packed converter (two rows per instruction; the packed pairs are the
+  // transposed tile's 4-byte halves as they are).
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -165,36 +164,33 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
       const int col = wc + j * 32 + fr;
       const int rbase = wr + i * 32 + fh * 4;
       float dval[16];
-      if (kDMode == kDTransposed) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          dval[4 * q + 0] = bf16_bits_to_float(dt[i][j][q].x & 0xFFFFu);
-          dval[4 * q + 1] = bf16_bits_to_float(dt[i][j][q].x >> 16);
-          dval[4 * q + 2] = bf16_bits_to_float(dt[i][j][q].y & 0xFFFFu);
-          dval[4 * q + 3] = bf16_bits_to_float(dt[i][j][q].y >> 16);
-        }
-      } else if (kDMode == kDRowMajor) {
+      if (kDMode == kDRowMajor) {
         // all 16 reads of the block before its writes: one LDS round trip
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           dval[r] = bf16_bits_to_float(E[(rbase + (r >> 2) * 8 + (r & 3)) * LDE + col]);
       }
-      uint32_t bits[16];
+      float x[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float x = g.alpha * acc[i][j][r];
-        if (kDMode != kNoD) x = __fmaf_rn(g.beta, dval[r], x);
-        bits[r] = float_to_bf16_bits(x);
+        x[r] = kScaled ? g.alpha * acc[i][j][r] : acc[i][j][r];
+        if (kDMode != kNoD) x[r] = __fmaf_rn(g.beta, dval[r], x[r]);
       }
+      uint32_t w[8];  // w[k]: rows rbase + 8 (k / 2) + 2 (k % 2) + {0, 1} of column col
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        E[(rbase + (r >> 2) * 8 + (r & 3)) * LDE + col] = (uint16_t)bits[r];
+      for (int k = 0; k < 8; ++k) w[k] = pack_bf16x2(x[2 * k], x[2 * k + 1]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int row = rbase + (k >> 1) * 8 + (k & 1) * 2;
+        E[row * LDE + col] = (uint16_t)w[k];
+        E[(row + 1) * LDE + col] = (uint16_t)(w[k] >> 16);
+      }
       if (T) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           u32x2 v;
-          v.x = bits[4 * q] | (bits[4 * q + 1] << 16);
-          v.y = bits[4 * q + 2] | (bits[4 * q + 3] << 16);
+          v.x = w[2 * q];
+          v.y = w[2 * q + 1];
           *reinterpret_cast<u32x2*>(T + ((uint32_t)col * lt + (uint32_t)(rbase + q * 8))) = v;
         }
       }
@@ -352,8 +348,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
 
   // ---- epilogue ------------------------------------------------------------
   const uint16_t* D = nullptr;
-  const bool d_t = (g.flags & MORPH_GEMM_D_TRANSPOSED) != 0;
-  if (g.D) D = g.D + b * g.sd + (d_t ? col0 * g.ldd + row0 : row0 * g.ldd + col0);
+  if (g.D) D = g.D + b * g.sd + row0 * g.ldd + col0;
   uint16_t* T = nullptr;  // transposed destination: Ct, or the mirror tile
   int64_t ldt = 0;
   if (g.flags & MORPH_GEMM_SYMMETRIC) {
@@ -366,12 +361,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     ldt = g.ldct;
   }
   uint16_t* C = g.C + b * g.sc + row0 * g.ldc + col0;
-  if (D == nullptr)
-    epilogue<kNoD>(g, acc, smem, nullptr, C, T, ldt);
-  else if (d_t)
-    epilogue<kDTransposed>(g, acc, smem, D, C, T, ldt);
-  else
-    epilogue<kDRowMajor>(g, acc, smem, D, C, T, ldt);
+  // alpha == 1 (A = X X^T, X' = a X + B X) skips the multiply, which is exact then
+  if (g.alpha == 1.0f) {
+    if (D == nullptr)
+      epilogue<kNoD, false>(g, acc, smem, nullptr, C, T, ldt);
+    else
+      epilogue<kDRowMajor, false>(g, acc, smem, D, C, T, ldt);
+  } else {
+    if (D == nullptr)
+      epilogue<kNoD, true>(g, acc, smem, nullptr, C, T, ldt);
+    else
+      epilogue<kDRowMajor, true>(g, acc, smem, D, C, T, ldt);
+  }
 }
 
 }  // namespace
@@ -394,10 +395,9 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
       misaligned(Ct, 16))
     return MORPH_EINVAL;
   if (M % BM || N % BN || K % MORPH_GEMM_TILE_K) return MORPH_ERANGE;
-  if (flags & ~(MORPH_GEMM_SYMMETRIC | MORPH_GEMM_D_TRANSPOSED)) return MORPH_EINVAL;
+  if (flags & ~MORPH_GEMM_SYMMETRIC) return MORPH_EINVAL;
   const bool symmetric = (flags & MORPH_GEMM_SYMMETRIC) != 0;
-  const int64_t d_cols = (flags & MORPH_GEMM_D_TRANSPOSED) ? M : N;  // D stored [M, N] or [N, M]
-  if (ldp < K || ldq < K || ldc < N || (D && ldd < d_cols) || (Ct && ldct < M)) return MORPH_EINVAL;
+  if (ldp < K || ldq < K || ldc < N || (D && ldd < N) || (Ct && ldct < M)) return MORPH_EINVAL;
   // 16-byte loads and stores of rows: every leading dimension and batch stride a multiple of 8
   if ((ldp | ldq | ldc | stride_p | stride_q | stride_c) % 8 ||
       (D && (ldd | stride_d) % 8) || (Ct && (ldct | stride_ct) % 8))

@@ -292,16 +292,14 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
     rc = morph_gemm_nt_bf16(W.X, W.X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, L.np, L.np,
                             0, L.mp, 0, sx, sx, 0, ss, 0, 1.0f, 0.0f, MORPH_GEMM_SYMMETRIC, stream);
     if (rc) return rc;
-    // B = c (A A^T) + b A (symmetric; A = A^T, so D is read in the transposed layout)
+    // B = c (A A^T) + b A (symmetric)
     rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, L.mp, L.mp,
-                            L.mp, L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b,
-                            MORPH_GEMM_SYMMETRIC | MORPH_GEMM_D_TRANSPOSED, stream);
+                            L.mp, L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b, MORPH_GEMM_SYMMETRIC,
+                            stream);
     if (rc) return rc;
-    // X' = (B Xt^T) + a X, written in place over X and transposed into the other
-    // Xt; D = X is read as Xt (the same bf16 values, transposed)
-    rc = morph_gemm_nt_bf16(W.B, W.Xt[cur], W.Xt[cur], W.X, W.Xt[cur ^ 1], L.mp, L.np, L.mp, count,
-                            L.mp, L.mp, L.mp, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a,
-                            MORPH_GEMM_D_TRANSPOSED, stream);
+    // X' = (B Xt^T) + a X, written in place over X and transposed into the other Xt
+    rc = morph_gemm_nt_bf16(W.B, W.Xt[cur], W.X, W.X, W.Xt[cur ^ 1], L.mp, L.np, L.mp, count,
+                            L.mp, L.mp, L.np, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a, 0, stream);
     if (rc) return rc;
     cur ^= 1;
   }

@@ -46,21 +46,22 @@ def test_gemm_nt_against_exact_product(b, M, N, K):
     assert torch.equal(out_t.cpu(), C.transpose(1, 2))
 
 
-@pytest.mark.parametrize("b,M,N,K", [(1, 256, 256, 64), (2, 512, 768, 192), (1, 768, 512, 256)])
-def test_gemm_nt_transposed_D_equals_row_major_D(b, M, N, K):
-    """MORPH_GEMM_D_TRANSPOSED reads D^T; the result is bit-identical to passing D,
-    with and without the transposed output."""
-    P, Q, D = rand_bf16((b, M, K), 11).to(DEV), rand_bf16((b, N, K), 12).to(DEV), \
-        rand_bf16((b, M, N), 13).to(DEV)
-    Dt = D.transpose(1, 2).contiguous()
-    for with_t in (False, True):
-        t0 = torch.empty((b, N, M), dtype=torch.bfloat16, device=DEV) if with_t else None
-        t1 = torch.empty((b, N, M), dtype=torch.bfloat16, device=DEV) if with_t else None
-        ref = muon.gemm_nt(P, Q, D, 1.0, 3.4445, out_t=t0)
-        got = muon.gemm_nt(P, Q, Dt, 1.0, 3.4445, out_t=t1, d_transposed=True)
-        assert torch.equal(got, ref)
-        if with_t:
-            assert torch.equal(t1, t0) and torch.equal(t1, got.transpose(1, 2))
+@pytest.mark.parametrize("alpha", [1 + 2 ** -8, 1 + 3 * 2 ** -8, 1 / 3, -0.7, 2.0 ** -140, 7.5e37])
+def test_gemm_output_rounding_is_round_to_nearest_even(alpha):
+    """C = alpha * I Q^T is one fp32 product alpha * q rounded once to bf16.  With q a
+    power of two, 1 + 2^-8 and 1 + 3 * 2^-8 land exactly on ties (to even: down and
+    up); 2^-140 gives fp32 denormals, 7.5e37 overflows bf16.  Bits must equal torch's
+    CPU conversion (round to nearest even) of the same fp32 product, in C and in Ct."""
+    g = torch.Generator().manual_seed(21)
+    Q = torch.randn(256, 256, generator=g)
+    Q[:64] = torch.sign(Q[:64]) * 2.0 ** torch.randint(-20, 20, (64, 256), generator=g).float()
+    Q = Q.to(torch.bfloat16)
+    P = torch.eye(256, dtype=torch.bfloat16)
+    out_t = torch.empty((256, 256), dtype=torch.bfloat16, device=DEV)
+    C = muon.gemm_nt(P.to(DEV), Q.to(DEV), None, alpha, out_t=out_t).cpu()
+    expect = (torch.tensor(alpha, dtype=torch.float32) * Q.float().T).to(torch.bfloat16)
+    assert torch.equal(C.view(torch.int16), expect.view(torch.int16))
+    assert torch.equal(out_t.cpu().view(torch.int16), expect.T.contiguous().view(torch.int16))
 
 
 def test_gemm_nt_in_place_output_over_D():
