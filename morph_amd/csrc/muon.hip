@@ -21,6 +21,9 @@
 // with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.  The
 // zero padding is exact for Newton-Schulz: padded rows of X give zero rows and
 // columns of A and B, which keep the padding of X zero in every iteration.
+// Rows are stored kRowPad elements longer than Mp / Np (never read): with
+// rows a multiple of 4 KiB apart, the 256 rows of a GEMM operand tile fall
+// on few L2 channels; the pad spreads them (about 6% on the K = Mp products).
 #include "common.h"
 
 namespace morph {
@@ -30,6 +33,7 @@ constexpr int kBlock = 256;
 constexpr int kMaxMats = 64;
 constexpr int kElemsPerBlock = kBlock * 16;  // 16 elements per lane, lane-strided (coalesced)
 constexpr int kTile = 64;                       // transpose tile
+constexpr int64_t kRowPad = 64;                 // bf16 elements appended to every X/Xt/A/B row
 
 struct MatPtrs {
   const float* grad[kMaxMats];
@@ -41,6 +45,7 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct Layout {
   int64_t rows, cols, m, n, mp, np, count, numel, blocks;
+  int64_t ldn, ldm;  // row lengths of X ([Mp][ldn]) and of Xt, A, B ([*][ldm])
   size_t off_u, off_part, off_den, off_x, off_xt0, off_xt1, off_a, off_b, total;
 };
 
@@ -53,6 +58,8 @@ Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
   L.n = rows < cols ? cols : rows;
   L.mp = round_up(L.m, MORPH_GEMM_TILE_M);
   L.np = round_up(L.n, MORPH_GEMM_TILE_N);  // also a multiple of the K tile (64)
+  L.ldn = L.np + kRowPad;
+  L.ldm = L.mp + kRowPad;
   L.numel = rows * cols;
   L.blocks = (L.numel + kElemsPerBlock - 1) / kElemsPerBlock;
   size_t off = 0;
@@ -64,11 +71,11 @@ Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
   L.off_u = take((size_t)count * L.numel * 4);
   L.off_part = take((size_t)count * L.blocks * 8);
   L.off_den = take((size_t)count * 4);
-  L.off_x = take((size_t)count * L.mp * L.np * 2);
-  L.off_xt0 = take((size_t)count * L.np * L.mp * 2);
-  L.off_xt1 = take((size_t)count * L.np * L.mp * 2);
-  L.off_a = take((size_t)count * L.mp * L.mp * 2);
-  L.off_b = take((size_t)count * L.mp * L.mp * 2);
+  L.off_x = take((size_t)count * L.mp * L.ldn * 2);
+  L.off_xt0 = take((size_t)count * L.np * L.ldm * 2);
+  L.off_xt1 = take((size_t)count * L.np * L.ldm * 2);
+  L.off_a = take((size_t)count * L.mp * L.ldm * 2);
+  L.off_b = take((size_t)count * L.mp * L.ldm * 2);
   L.total = off;
   return L;
 }
@@ -134,16 +141,19 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const double* part_all, fl
 __global__ __launch_bounds__(kBlock) void scale_kernel(const float* u_all, const float* den,
                                                        uint16_t* x_all, uint16_t* xt_all,
                                                        int64_t rows, int64_t cols, int64_t mp,
-                                                       int64_t np, int64_t numel) {
+                                                       int64_t np, int64_t ldm, int64_t ldn,
+                                                       int64_t numel) {
   __shared__ uint16_t tile[kTile][kTile + 2];
   const int mat = blockIdx.z;
   const float d = den[mat];
   const float* u = u_all + (int64_t)mat * numel;
   const bool same_is_x = rows <= cols;  // X has the param layout
-  uint16_t* same = same_is_x ? x_all + (int64_t)mat * mp * np : xt_all + (int64_t)mat * np * mp;
-  uint16_t* trans = same_is_x ? xt_all + (int64_t)mat * np * mp : x_all + (int64_t)mat * mp * np;
-  const int64_t ld_same = same_is_x ? np : mp;   // row length of the param-layout copy
-  const int64_t ld_trans = same_is_x ? mp : np;  // row length of the transposed copy
+  uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
+  uint16_t* xtm = xt_all + (int64_t)mat * np * ldm;
+  uint16_t* same = same_is_x ? xm : xtm;
+  uint16_t* trans = same_is_x ? xtm : xm;
+  const int64_t ld_same = same_is_x ? ldn : ldm;   // row length of the param-layout copy
+  const int64_t ld_trans = same_is_x ? ldm : ldn;  // row length of the transposed copy
   const int64_t r0 = (int64_t)blockIdx.y * kTile, c0 = (int64_t)blockIdx.x * kTile;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int rr = ty; rr < kTile; rr += kBlock / 64) {
@@ -168,12 +178,13 @@ template <bool kExtract>
 __global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint16_t* x_all,
                                                        const uint16_t* xt_all, int64_t rows,
                                                        int64_t cols, int64_t mp, int64_t np,
-                                                       float scale, float decay, float neg_lr) {
+                                                       int64_t ldm, int64_t ldn, float scale,
+                                                       float decay, float neg_lr) {
   const int mat = blockIdx.y;
   float* p = mats.param[mat];
   const bool same_is_x = rows <= cols;
-  const uint16_t* U = same_is_x ? x_all + (int64_t)mat * mp * np : xt_all + (int64_t)mat * np * mp;
-  const int64_t ld = same_is_x ? np : mp;
+  const uint16_t* U = same_is_x ? x_all + (int64_t)mat * mp * ldn : xt_all + (int64_t)mat * np * ldm;
+  const int64_t ld = same_is_x ? ldn : ldm;
   const int64_t numel = rows * cols;
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
   for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
@@ -275,7 +286,7 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
                      dim3((unsigned)((cols + kTile - 1) / kTile),
                           (unsigned)((rows + kTile - 1) / kTile), count),
                      dim3(kBlock), 0, s, W.u, W.den, W.X, W.Xt[0], rows, cols, L.mp, L.np,
-                     L.numel);
+                     L.ldm, L.ldn, L.numel);
   return launch_status();
 }
 
@@ -285,21 +296,21 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
   int rc = setup(nullptr, count, rows, cols, hp, workspace, workspace_bytes, false, false, &W);
   if (rc || count == 0) return rc;
   const Layout& L = W.L;
-  const int64_t sx = L.mp * L.np, ss = L.mp * L.mp;
+  const int64_t sx = L.mp * L.ldn, st = L.np * L.ldm, ss = L.mp * L.ldm;
+  const int64_t n = L.ldn, m = L.ldm;  // leading dimensions
   int cur = 0;
   for (int it = 0; it < hp->ns_steps; ++it) {
     // A = X X^T (symmetric: upper triangle of tiles, mirrored)
-    rc = morph_gemm_nt_bf16(W.X, W.X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, L.np, L.np,
-                            0, L.mp, 0, sx, sx, 0, ss, 0, 1.0f, 0.0f, MORPH_GEMM_SYMMETRIC, stream);
+    rc = morph_gemm_nt_bf16(W.X, W.X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, n, n, 0, m, 0,
+                            sx, sx, 0, ss, 0, 1.0f, 0.0f, MORPH_GEMM_SYMMETRIC, stream);
     if (rc) return rc;
     // B = c (A A^T) + b A (symmetric)
-    rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, L.mp, L.mp,
-                            L.mp, L.mp, 0, ss, ss, ss, ss, 0, hp->c, hp->b, MORPH_GEMM_SYMMETRIC,
-                            stream);
+    rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, m, m, m, m, 0,
+                            ss, ss, ss, ss, 0, hp->c, hp->b, MORPH_GEMM_SYMMETRIC, stream);
     if (rc) return rc;
     // X' = (B Xt^T) + a X, written in place over X and transposed into the other Xt
-    rc = morph_gemm_nt_bf16(W.B, W.Xt[cur], W.X, W.X, W.Xt[cur ^ 1], L.mp, L.np, L.mp, count,
-                            L.mp, L.mp, L.np, L.np, L.mp, ss, sx, sx, sx, sx, 1.0f, hp->a, 0, stream);
+    rc = morph_gemm_nt_bf16(W.B, W.Xt[cur], W.X, W.X, W.Xt[cur ^ 1], L.mp, L.np, L.mp, count, m, m,
+                            n, n, m, ss, st, sx, sx, st, 1.0f, hp->a, 0, stream);
     if (rc) return rc;
     cur ^= 1;
   }
@@ -319,10 +330,10 @@ int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   hipStream_t s = as_stream(stream);
   if (orth_only)
     hipLaunchKernelGGL(apply_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
-                       L.mp, L.np, hp->update_scale, hp->decay, hp->neg_lr);
+                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->decay, hp->neg_lr);
   else
     hipLaunchKernelGGL(apply_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
-                       L.mp, L.np, hp->update_scale, hp->decay, hp->neg_lr);
+                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->decay, hp->neg_lr);
   return launch_status();
 }
 
