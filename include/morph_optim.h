@@ -217,6 +217,44 @@ int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad
 int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* d_clock_list,
                    int n, void* stream);
 
+/* ---- Stage-gradient accumulation ------------------------------------------
+ * Replaces the reference's per-micro-batch
+ *   destination.add_(g.detach().float() / loss_scale)
+ * into the zeroed FP32 stage window (streamtrain/sparse_disk.py:82-87,
+ * 104-108; disk.py:446-448) and its norm pass
+ *   norm_squared += piece.double().square().sum().item()
+ * (disk.py:466-468; sparse_disk.py:136), whose finiteness is the skip / retry
+ * decision (disk.py:485) and whose value sets the clip (disk.py:489).
+ */
+#define MORPH_ACCUM_ELEMS_PER_BLOCK 2048 /* elements per workgroup = per FP64 partial */
+#define MORPH_ACCUM_OVERWRITE 1 /* first micro-batch: dst = 0 + x (zero_() then add_()) */
+#define MORPH_ACCUM_FINAL 2     /* also OR the non-finite flag of dst and write FP64 partials */
+
+typedef struct morph_accum_tensor {
+  const void* grad; /* this micro-batch's gradient (grad_dtype), contiguous; NULL = none */
+  float* dst;       /* FP32 accumulation window for the same parameter */
+  int64_t numel;
+} morph_accum_tensor;
+
+/* Number of FP64 partials a MORPH_ACCUM_FINAL call over these tensors writes
+ * (one per MORPH_ACCUM_ELEMS_PER_BLOCK elements of each tensor). */
+int64_t morph_grad_partials(const morph_accum_tensor* tensors, int count);
+
+/* dst = (OVERWRITE ? 0 : dst) + fp32(grad) / loss_scale, elementwise, for
+ * every tensor (a NULL grad adds nothing).  The division is a multiply by
+ * 2^-k when loss_scale = 2^k (the same bits) and an IEEE division otherwise.
+ * With MORPH_ACCUM_FINAL the same pass ORs 1 into *d_found_inf when any
+ * resulting dst element is inf or NaN, and writes sum((double)dst^2) per
+ * workgroup into d_partials[0 .. morph_grad_partials()) for morph_sumsq_total. */
+int morph_grad_accumulate(const morph_accum_tensor* tensors, int count, int grad_dtype,
+                          double loss_scale, int flags, uint32_t* d_found_inf, double* d_partials,
+                          int64_t partials_len, void* stream);
+
+/* *d_out = (accumulate ? *d_out : 0) + sum of d_partials[0 .. n), in a fixed
+ * order (deterministic for a given n). */
+int morph_sumsq_total(const double* d_partials, int64_t n, double* d_out, int accumulate,
+                      void* stream);
+
 /* ---- Hybrid Muon: Newton-Schulz orthogonalisation on bf16 MFMA ---------- */
 
 /* Tile of morph_gemm_nt_bf16: M and N must be multiples of 256, K of 64. */

@@ -22,12 +22,14 @@ HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
 EXPORTS = (
     "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
-    "morph_adamw_multi_dev", "morph_step_end", "morph_gemm_nt_bf16",
+    "morph_adamw_multi_dev", "morph_step_end", "morph_grad_partials", "morph_grad_accumulate",
+    "morph_sumsq_total", "morph_gemm_nt_bf16",
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
     "morph_muon_prepare", "morph_muon_newton_schulz", "morph_muon_finish",
 )
 GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 256, 256, 64
 GEMM_SYMMETRIC = 1
+ACCUM_ELEMS_PER_BLOCK, ACCUM_OVERWRITE, ACCUM_FINAL = 2048, 1, 2
 FATAL_MIN_SCALE = 1
 
 
@@ -64,6 +66,11 @@ class AdamwSched(ctypes.Structure):
     """morph_adamw_sched."""
     _fields_ = [("lr", ctypes.c_double), ("bias_correction1", ctypes.c_void_p),
                 ("bias_correction2_sqrt", ctypes.c_void_p), ("table_len", ctypes.c_int64)]
+
+
+class AccumTensor(ctypes.Structure):
+    """morph_accum_tensor."""
+    _fields_ = [("grad", ctypes.c_void_p), ("dst", ctypes.c_void_p), ("numel", ctypes.c_int64)]
 
 
 class MuonMatrix(ctypes.Structure):
@@ -106,6 +113,10 @@ def lib():
                                        ctypes.POINTER(AdamwHP), ctypes.POINTER(AdamwSched), i32,
                                        vp, vp, vp], i32),
             "morph_step_end": ([vp, vp, vp, i32, vp], i32),
+            "morph_grad_partials": ([ctypes.POINTER(AccumTensor), i32], i64),
+            "morph_grad_accumulate": ([ctypes.POINTER(AccumTensor), i32, i32, ctypes.c_double, i32,
+                                       vp, vp, i64, vp], i32),
+            "morph_sumsq_total": ([vp, i64, vp, i32, vp], i32),
             "morph_gemm_nt_bf16": ([vp, vp, vp, vp, vp] + [i64] * 14 +
                                    [ctypes.c_float, ctypes.c_float, i32, vp], i32),
             "morph_muon_workspace_bytes": ([i64, i64, i32], ctypes.c_size_t),

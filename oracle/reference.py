@@ -12,9 +12,14 @@ Contents, each restating the reference (paths relative to the MORPH repo):
     the C restatement in oracle/morph_oracle.c (element arithmetic);
   * disk_update_torch() -- streamtrain/disk.py:203-216 run with torch CPU ops;
   * orthogonalize_fp32()/muon_reference_step() -- streamtrain/optimizer.py:13-22,
-    52-61 in FP32 torch CPU.
+    52-61 in FP32 torch CPU;
+  * accumulate_torch()/norm_squared_torch() -- the stage-gradient window of
+    streamtrain/sparse_disk.py:104-108 / disk.py:446-448 and the FP64 norm pass
+    disk.py:466-468 / sparse_disk.py:136, with torch CPU ops.
 
-Pinning (tests/test_oracle_*.py): the C restatement is checked bit-exact
+Pinning (tests/test_oracle_*.py): accumulate_torch against numpy's IEEE
+binary32 arithmetic, norm_squared_torch against exact rational sums (math.fsum)
+on inputs whose FP64 sums are exact; the C restatement is checked bit-exact
 against torch.optim.AdamW(foreach=False) and against disk_update_torch; both
 are checked against float64 closed forms of the first step; LossScale against
 the reference's known answers (tests/test_fp16.py:59-72); conversions against
@@ -273,6 +278,20 @@ def muon_reference_step(param, grad, momentum, lr, weight_decay):
     update *= max(1, param.shape[0] / param.shape[1]) ** .5
     param.mul_(1 - lr * weight_decay).add_(update, alpha=-lr)
     return update
+
+
+def accumulate_torch(destination, gradient, loss_scale):
+    """sparse_disk.py:106-107 (disk.py:447 on the CPU): the per-micro-batch unscale + add."""
+    destination.add_(gradient.detach().float() / loss_scale)
+
+
+def norm_squared_torch(gradients, chunk=1048576):
+    """disk.py:466-468 / sparse_disk.py:136: FP64 sum of squares over 1M-element pieces."""
+    total = 0.0
+    for g in gradients:
+        for piece in g.flatten().split(chunk):
+            total += piece.double().square().sum().item()
+    return total
 
 
 def cpu_threads():
