@@ -220,6 +220,98 @@ def muon_main(args):
     print(json.dumps(line), flush=True)
 
 
+GRADS_MICRO = 4            # micro-batches per stage window in the grads workload
+ACCUM_BYTES = 10           # plain pass: read g16 2 + read FP32 window 4 + write 4
+
+
+def time_grads(steps, warmup):
+    """Stage-gradient window (f1): 4 micro-batches of FP16 gradients x 2^16 into the FP32
+    config-2 window -- overwrite, 2 plain passes, final pass with flag + FP64 norm."""
+    from morph_amd.grads import StageGradients
+    device = torch.device("cuda", 0)
+    micro = [config2_grads(device, 2000 + k) for k in range(GRADS_MICRO)]
+    window = StageGradients(CONFIG2_SHAPES, device)
+    n = window.flat.numel()
+    stream = torch.cuda.current_stream()
+
+    def one_step(timer=None):
+        window.zero_()
+        for k, grads in enumerate(micro):
+            if timer is not None and 0 < k < GRADS_MICRO - 1:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                window.accumulate(grads, LOSS_SCALE)
+                b.record(stream)
+                timer.append((a, b))
+            else:
+                window.accumulate(grads, LOSS_SCALE, final=(k == GRADS_MICRO - 1))
+
+    for _ in range(warmup):
+        one_step()
+    torch.cuda.synchronize()
+    timer = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one_step(timer)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    if window.found_inf():
+        raise RuntimeError("synthetic finite gradients flagged")
+    ms = [a.elapsed_time(b) for a, b in timer]
+    return dict(n=n, elapsed=elapsed, avg_pass_s=sum(ms) / len(ms) / 1e3,
+                norm_squared=window.norm_squared())
+
+
+def cpu_baseline_grads():
+    """The reference's torch ops on the host (sparse_disk.py:106-107, disk.py:466-468): one
+    plain micro-batch pass over the config-2 window plus the chunked FP64 norm pass."""
+    from oracle import reference as R
+    threads = min(16, R.cpu_threads())
+    torch.set_num_threads(threads)
+    grads = config2_grads("cpu", 2000)
+    window = [torch.zeros(s) for s in CONFIG2_SHAPES]
+    n = sum(w.numel() for w in window)
+    for d, g in zip(window, grads):  # warm-up (first touch)
+        R.accumulate_torch(d, g, LOSS_SCALE)
+    t0 = time.perf_counter()
+    for d, g in zip(window, grads):
+        R.accumulate_torch(d, g, LOSS_SCALE)
+    t_acc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    R.norm_squared_torch(window)
+    t_norm = time.perf_counter() - t0
+    return dict(value=round(n / t_acc / 1e9, 4), unit="Gparams/s per micro-batch pass",
+                cores=threads, kind="port",
+                sample=f"config 2 window (N={n}): one add_(g.float()/scale) pass {t_acc * 1e3:.1f} ms; "
+                       f"the FP64 chunked norm pass {t_norm * 1e3:.1f} ms")
+
+
+def grads_main(args):
+    r = time_grads(args.steps, args.warmup)
+    n = r["n"]
+    ms = r["elapsed"] / args.steps * 1e3
+    achieved = ACCUM_BYTES * n / r["avg_pass_s"] / 1e9
+    line = {
+        "metric": "Stage-gradient accumulate Gparams/s per micro-batch pass, 5B SwiGLU window, 1 MI355X",
+        "value": round(n * GRADS_MICRO * args.steps / r["elapsed"] / 1e9, 3),
+        "unit": "Gparams/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"config 2 window, {GRADS_MICRO} micro-batches of FP16 gradients x "
+                               "2^16: overwrite, plain, plain, final (flag + FP64 norm partials)",
+                   "params": n, "shapes": CONFIG2_SHAPES, "grad_dtype": "f16",
+                   "loss_scale": LOSS_SCALE},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "accumulate_kernel<F16,false,false> (plain pass)",
+                     "avg_launch_us": round(r["avg_pass_s"] * 1e6, 2),
+                     "bytes_per_launch": ACCUM_BYTES * n},
+        "norm_squared": r["norm_squared"],
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_grads(),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def measured_traffic():
     """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
     try:
@@ -234,8 +326,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("adamw", "muon"), default="adamw",
-                    help="adamw: the headline config-2 step (default); muon: config 5")
+    ap.add_argument("--workload", choices=("adamw", "muon", "grads"), default="adamw",
+                    help="adamw: the headline config-2 step (default); muon: config 5; "
+                         "grads: the stage-gradient window")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()
@@ -257,6 +350,8 @@ def main():
         sys.exit(2)
     if args.workload == "muon":
         return muon_main(args)
+    if args.workload == "grads":
+        return grads_main(args)
     r = time_gpu(args.steps, args.warmup)
     n = r["n"]
     ms_per_step = r["elapsed"] / args.steps * 1e3
