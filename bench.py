@@ -18,6 +18,7 @@ library the reference's AdamW group runs -- on this host's cores.
 """
 import argparse
 import json
+import os
 import sys
 import time
 from pathlib import Path
@@ -312,6 +313,129 @@ def grads_main(args):
     print(json.dumps(line), flush=True)
 
 
+WINDOW_BYTES = 30  # fused update on the resident window: read g32 4 + w,m,v 12; write 12 + f16 copy 2
+
+
+class _FileStore:
+    """[3, N] float32 state files of the reference's DiskState (disk.py:45-70) in a temp dir."""
+
+    def __init__(self, root, names_shapes, seed=0):
+        import numpy as np
+        self.root = Path(root)
+        self.entries = {}
+        gen = torch.Generator().manual_seed(seed)
+        for i, (name, shape) in enumerate(names_shapes):
+            n = int(torch.Size(shape).numel())
+            self.entries[name] = dict(shape=list(shape), size=n, file=f"{i:05}.bin")
+            state = np.zeros((3, n), np.float32)
+            state[0] = (torch.randn(n, generator=gen) * .02).numpy()
+            state.tofile(self.root / f"{i:05}.bin")
+
+    def fault(self, point):
+        return None
+
+
+def time_window(steps, warmup, root):
+    """Resident window (f2): load the config-2 window's [3, N] files into HBM + FP16 compute
+    copy, then per step DiskState.update for the 3 parameters (fused update on the resident
+    state + FP16 copy, D2H write-back chunk by chunk, flush, fsync)."""
+    from morph_amd.window import ResidentWindow
+    device = torch.device("cuda", 0)
+    names = ["ffn.gate.weight", "ffn.up.weight", "ffn.down.weight"]
+    store = _FileStore(root, list(zip(names, CONFIG2_SHAPES)))
+    win = ResidentWindow(store, names, torch.float16)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    win.load()
+    torch.cuda.synchronize()
+    t_load = time.perf_counter() - t0
+    gen = torch.Generator(device=device).manual_seed(5)
+    grads = {n: torch.randn(s, generator=gen, device=device) * 1e-4 for n, s in zip(names, CONFIG2_SHAPES)}
+    step = 0
+    for _ in range(warmup):
+        step += 1
+        for n in names:
+            win.update(n, grads[n], step, 3e-4, 1.0)
+    torch.cuda.synchronize()
+    win.kernel_timer = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step += 1
+        for n in names:
+            win.update(n, grads[n], step, 3e-4, 1.0)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    kms = [a.elapsed_time(b) for a, b in win.kernel_timer]
+    return dict(n=sum(store.entries[n]["size"] for n in names), t_load=t_load, elapsed=elapsed,
+                avg_kernel_s=sum(kms) / len(kms) / 1e3, kernels=len(kms) // steps,
+                timing={k: round(v, 4) for k, v in win.timing.items()})
+
+
+def cpu_baseline_window(root):
+    """The reference's DiskState.update (disk.py:203-223: memmap, chunked torch ops, np.stack
+    write-back, flush, fsync) on one [6144, 3072] parameter file of the window."""
+    import numpy as np
+    from oracle import reference as R
+    threads = min(16, R.cpu_threads())
+    torch.set_num_threads(threads)
+    store = _FileStore(root, [("w", CONFIG2_SHAPES[0])], seed=1)
+    e = store.entries["w"]
+    g = torch.randn(e["size"], generator=torch.Generator().manual_seed(2)) * 1e-4
+    path = store.root / e["file"]
+    t0 = time.perf_counter()
+    mapped = np.memmap(path, dtype=np.float32, mode="r+", shape=(3, e["size"]))
+    R.disk_update_torch(mapped, g, 1, 3e-4, 1.0)
+    mapped.flush()
+    del mapped
+    fd = os.open(path, os.O_RDWR)
+    os.fsync(fd)
+    os.close(fd)
+    t = time.perf_counter() - t0
+    return dict(value=round(e["size"] / t / 1e9, 4), unit="Gparams/s", cores=threads, kind="port",
+                sample=f"DiskState.update of one [6144, 3072] state file ({e['size']} params): "
+                       f"{t * 1e3:.0f} ms incl. memmap I/O, flush and fsync")
+
+
+def window_main(args):
+    import shutil
+    import tempfile
+    root = Path(tempfile.mkdtemp(prefix="morph_window_"))
+    try:
+        (root / "gpu").mkdir()
+        r = time_window(args.steps, args.warmup, root / "gpu")
+        n = r["n"]
+        achieved = WINDOW_BYTES * n / (r["avg_kernel_s"] * r["kernels"]) / 1e9
+        line = {
+            "metric": "Resident stage-window DiskState.update Gparams/s (fused update, D2H write-back, fsync), 5B SwiGLU window, 1 MI355X",
+            "value": round(n * args.steps / r["elapsed"] / 1e9, 3), "unit": "Gparams/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(r["elapsed"] / args.steps * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "config 2 window as three [3, N] float32 state files: load into HBM "
+                                   "with FP16 compute copy once, then per step update + write-back "
+                                   "of every file (chunks of 1M elements, flush, fsync)",
+                       "params": n, "shapes": CONFIG2_SHAPES, "compute_dtype": "f16",
+                       "state_dir": "tempfile.mkdtemp() on the GPU box"},
+            "load_gparams_per_s": round(n / r["t_load"] / 1e9, 3),
+            "load_h2d_gbs": round(12 * n / r["t_load"] / 1e9, 2),
+            "write_back_gbs": round(12 * n * args.steps / r["elapsed"] / 1e9, 2),
+            "host_seconds": r["timing"],
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "adamw_multi_kernel<F32,F16,host> (resident [3, N] state)",
+                         "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
+                         "bytes_per_launch": WINDOW_BYTES * n // r["kernels"]},
+        }
+        if not args.no_cpu_baseline:
+            (root / "cpu").mkdir()
+            line["cpu_baseline"] = cpu_baseline_window(root / "cpu")
+        else:
+            line["cpu_baseline"] = None
+        print(json.dumps(line), flush=True)
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+
+
 def measured_traffic():
     """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
     try:
@@ -326,9 +450,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("adamw", "muon", "grads"), default="adamw",
+    ap.add_argument("--workload", choices=("adamw", "muon", "grads", "window"), default="adamw",
                     help="adamw: the headline config-2 step (default); muon: config 5; "
-                         "grads: the stage-gradient window")
+                         "grads: the stage-gradient window; window: the HBM-resident [3, N] state")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()
@@ -352,6 +476,8 @@ def main():
         return muon_main(args)
     if args.workload == "grads":
         return grads_main(args)
+    if args.workload == "window":
+        return window_main(args)
     r = time_gpu(args.steps, args.warmup)
     n = r["n"]
     ms_per_step = r["elapsed"] / args.steps * 1e3

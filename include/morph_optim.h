@@ -255,6 +255,17 @@ int morph_grad_accumulate(const morph_accum_tensor* tensors, int count, int grad
 int morph_sumsq_total(const double* d_partials, int64_t n, double* d_out, int accumulate,
                       void* stream);
 
+/* ---- Master-weight conversion --------------------------------------------
+ * dst = dtype(src) elementwise (FP16: round to nearest even, overflow -> inf;
+ * BF16: round to nearest even, NaN -> 0x7FC0; FP32: copy).  Replaces the CPU
+ * cast of the FP32 weight row before the stage's H2D copy
+ * (streamtrain/disk.py:316-327) and the FP16 encoding of the export
+ * (streamtrain/export.py:32-34).  d_range_flag (nullable): OR 1 when some
+ * source value is inf / NaN or, for FP16 output, |value| > 65504 -- the
+ * export's "cannot be represented by finite FP16" condition. */
+int morph_convert_f32(const float* src, void* dst, int dst_dtype, int64_t n,
+                      uint32_t* d_range_flag, void* stream);
+
 /* ---- Hybrid Muon: Newton-Schulz orthogonalisation on bf16 MFMA ---------- */
 
 /* Tile of morph_gemm_nt_bf16: M and N must be multiples of 256, K of 64. */

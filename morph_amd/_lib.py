@@ -23,7 +23,7 @@ EXPORTS = (
     "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
     "morph_adamw_multi_dev", "morph_step_end", "morph_grad_partials", "morph_grad_accumulate",
-    "morph_sumsq_total", "morph_gemm_nt_bf16",
+    "morph_sumsq_total", "morph_convert_f32", "morph_gemm_nt_bf16",
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
     "morph_muon_prepare", "morph_muon_newton_schulz", "morph_muon_finish",
 )
@@ -117,6 +117,7 @@ def lib():
             "morph_grad_accumulate": ([ctypes.POINTER(AccumTensor), i32, i32, ctypes.c_double, i32,
                                        vp, vp, i64, vp], i32),
             "morph_sumsq_total": ([vp, i64, vp, i32, vp], i32),
+            "morph_convert_f32": ([vp, vp, i32, i64, vp, vp], i32),
             "morph_gemm_nt_bf16": ([vp, vp, vp, vp, vp] + [i64] * 14 +
                                    [ctypes.c_float, ctypes.c_float, i32, vp], i32),
             "morph_muon_workspace_bytes": ([i64, i64, i32], ctypes.c_size_t),

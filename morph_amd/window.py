@@ -1,0 +1,240 @@
+"""A stage's canonical optimizer state resident in HBM.
+
+The reference keeps every parameter's state on disk as one [3, N] float32 file
+(rows: weight, exp_avg, exp_avg_sq; streamtrain/disk.py:45-70, 184-189).  For
+each stage it reads the weight row, casts it on the CPU to the compute dtype
+and copies it into the slot's device weights (disk.py:316-327), and after the
+backward it updates every parameter on the CPU chunk by chunk
+(DiskState.update, disk.py:203-223).
+
+ResidentWindow moves the state of one stage onto the GPU once: load() streams
+each [3, N] file through pinned staging into HBM (12 B/param host-to-device,
+chunked and double-buffered) and writes the compute copy on the device
+(morph_convert_f32), so the CPU cast and the separate weight copy disappear.
+update() has DiskState.update's signature and arithmetic: one fused launch
+over the resident state (FP32 gradient from the device window, DiskState's
+constants), which also writes the new compute copy; then the [3, N] result is
+written back to the file chunk by chunk with fault('partial_state_write')
+after every partial write, flush and fsync -- the reference's durability and
+fault order (disk.py:215-223).  If anything raises, the parameter's resident
+state is dropped (it may be ahead of the file; the journal rolls the file
+back) and must be loaded again.
+"""
+import ctypes
+import os
+import time
+
+import torch
+
+from . import kernels
+from ._lib import check, dtype_code, lib, stream_handle
+from .hyper import disk_constants
+
+
+def _fsync(path):
+    fd = os.open(path, os.O_RDWR)
+    try:
+        os.fsync(fd)
+    finally:
+        os.close(fd)
+
+
+class ResidentWindow:
+    """One stage's [3, N] optimizer state in HBM plus its compute copy.
+
+    store: the DiskState-like owner of the files (needs `root`, `entries`,
+    `fault`).  names: the stage's canonical parameter names, in slot order.
+    weights: optional flat device tensor (the slot's weights, dtype =
+    compute_dtype) whose consecutive slices receive each parameter's compute
+    copy, as Slot.weights does in the reference (engine.py:60-70, 128-140).
+    """
+
+    def __init__(self, store, names, compute_dtype=torch.float16, weights=None, device=None,
+                 chunk_elements=1 << 22):
+        self.store = store
+        self.names = list(names)
+        self.device = torch.device(device) if device is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        self.compute_dtype = compute_dtype
+        self.chunk = int(chunk_elements)
+        if self.chunk < 1:
+            raise ValueError("chunk_elements must be positive")
+        sizes = [int(store.entries[n]["size"]) for n in self.names]
+        total = sum(sizes)
+        if weights is None:
+            weights = torch.empty(total, dtype=compute_dtype, device=self.device)
+        if weights.dtype != compute_dtype or weights.numel() < total or weights.device != self.device:
+            raise ValueError("weights must be a device tensor of compute_dtype with room for the stage")
+        self.weights, self.state, off = {}, {}, 0
+        for name, n in zip(self.names, sizes):
+            self.weights[name] = weights.reshape(-1)[off:off + n].view(store.entries[name]["shape"])
+            off += n
+        self.transfer_bytes = dict(h2d_state=0, d2h_state=0)
+        self.timing = dict(file_read=0.0, d2h_wait=0.0, file_write=0.0, fsync=0.0)  # seconds
+        self.kernel_timer = None  # optional list: (start, end) HIP events around each update launch
+        self._copy = torch.cuda.Stream(self.device)
+        self._staging = None
+
+    # -- staging buffers ----------------------------------------------------
+    def _slots(self):
+        if self._staging is None:
+            c = self.chunk
+            self._staging = [dict(host=torch.empty((3, c), dtype=torch.float32, pin_memory=True),
+                                  event=torch.cuda.Event()) for _ in range(2)]
+        return self._staging
+
+    def _path(self, name):
+        return self.store.root / self.store.entries[name]["file"]
+
+    # -- load ---------------------------------------------------------------
+    def load(self, names=None):
+        """Read the [3, N] files into HBM and write the compute copies.  Synchronous on
+        return for the host staging; the device work is ordered on the current stream."""
+        compute = torch.cuda.current_stream(self.device)
+        slots = self._slots()
+        for name in (self.names if names is None else names):
+            size = int(self.store.entries[name]["size"])
+            dev = torch.empty((3, size), dtype=torch.float32, device=self.device)
+            fd = os.open(self._path(name), os.O_RDONLY)
+            try:
+                for k, start in enumerate(range(0, size, self.chunk)):
+                    end = min(start + self.chunk, size)
+                    n = end - start
+                    s = slots[k % 2]
+                    s["event"].synchronize()  # the H2D that last read this staging buffer is done
+                    t0 = time.perf_counter()
+                    host = s["host"].numpy()
+                    for row in range(3):  # row r of the file starts at r * N floats
+                        _read_exact(fd, host[row, :n], (row * size + start) * 4)
+                    self.timing["file_read"] += time.perf_counter() - t0
+                    with torch.cuda.stream(self._copy):
+                        for row in range(3):
+                            dev[row, start:end].copy_(s["host"][row, :n], non_blocking=True)
+                        s["event"].record(self._copy)
+            finally:
+                os.close(fd)
+            compute.wait_stream(self._copy)
+            self.state[name] = dev
+            self.transfer_bytes["h2d_state"] += 12 * size
+            self._compute_copy(name, compute)
+        for s in slots:
+            s["event"].synchronize()
+
+    def _compute_copy(self, name, stream):
+        w, out = self.state[name][0], self.weights[name]
+        check(lib().morph_convert_f32(ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                      dtype_code(self.compute_dtype), w.numel(), None,
+                                      stream_handle(stream)))
+
+    def drop(self, name):
+        self.state.pop(name, None)
+
+    # -- update (DiskState.update's contract) ---------------------------------
+    def update(self, name, gradient, step, lr, clip, chunk_elements=1048576):
+        """disk.py:203-223 on the resident state; the file is written back chunk by chunk."""
+        if name not in self.state:
+            raise KeyError(f"{name} is not resident; call load() first")
+        if chunk_elements < 1:
+            raise ValueError("chunk_elements must be positive")
+        dev = self.state[name]
+        size = dev.shape[1]
+        flat = gradient.detach().reshape(-1)
+        if flat.numel() != size:
+            raise ValueError(f"gradient has {flat.numel()} elements, state has {size}")
+        if flat.dtype != torch.float32:
+            raise TypeError("DiskState.update takes an FP32 gradient")
+        if flat.device != self.device:
+            flat = flat.to(self.device)
+        compute = torch.cuda.current_stream(self.device)
+        try:
+            if self.kernel_timer is not None:
+                t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                t0.record(compute)
+            kernels.adamw_step(dev[0], dev[1], dev[2], flat, disk_constants(step=step, lr=lr, clip=clip),
+                               out=self.weights[name].reshape(-1), stream=compute)
+            if self.kernel_timer is not None:
+                t1.record(compute)
+                self.kernel_timer.append((t0, t1))
+            self._write_back(name, dev, chunk_elements, compute)
+        except BaseException:
+            self.drop(name)
+            compute.synchronize()
+            raise
+
+    def _write_back(self, name, dev, chunk_elements, compute):
+        size = dev.shape[1]
+        path = self._path(name)
+        host = torch.empty((2, 3, min(chunk_elements, size)), dtype=torch.float32, pin_memory=True)
+        hnp = host.numpy()
+        done = [torch.cuda.Event(), torch.cuda.Event()]
+        starts = list(range(0, size, chunk_elements))
+
+        def fetch(k):
+            start = starts[k]
+            end = min(start + chunk_elements, size)
+            with torch.cuda.stream(self._copy):
+                if k == 0:
+                    self._copy.wait_stream(compute)  # after the update
+                for row in range(3):
+                    host[k % 2, row, :end - start].copy_(dev[row, start:end], non_blocking=True)
+                done[k % 2].record(self._copy)
+
+        fd = os.open(path, os.O_RDWR)
+        try:
+            if starts:
+                fetch(0)
+            for k, start in enumerate(starts):
+                end = min(start + chunk_elements, size)
+                t0 = time.perf_counter()
+                done[k % 2].synchronize()
+                self.timing["d2h_wait"] += time.perf_counter() - t0
+                if k + 1 < len(starts):
+                    fetch(k + 1)  # overlaps this chunk's file write
+                t0 = time.perf_counter()
+                for row in range(3):  # the chunk's columns of all three rows, then the fault hook
+                    _write_exact(fd, hnp[k % 2, row, :end - start], (row * size + start) * 4)
+                self.timing["file_write"] += time.perf_counter() - t0
+                self.transfer_bytes["d2h_state"] += 12 * (end - start)
+                self.store.fault('partial_state_write')
+            t0 = time.perf_counter()
+            os.fsync(fd)
+            self.timing["fsync"] += time.perf_counter() - t0
+        finally:
+            self._copy.synchronize()
+            os.close(fd)
+
+
+def _read_exact(fd, out, offset):
+    """Fill the contiguous float32 array `out` from the file at byte `offset`."""
+    view = memoryview(out).cast("B")
+    got = 0
+    while got < len(view):
+        n = os.preadv(fd, [view[got:]], offset + got)
+        if n <= 0:
+            raise OSError(f"short read of a state file at offset {offset + got}")
+        got += n
+
+
+def _write_exact(fd, data, offset):
+    view = memoryview(data).cast("B")
+    put = 0
+    while put < len(view):
+        put += os.pwrite(fd, view[put:], offset + put)
+
+
+class ResidentDiskUpdate:
+    """DiskState mixin: update() runs on the stage window when the parameter is resident.
+
+    class GpuDiskState(ResidentDiskUpdate, GpuDiskUpdate, DiskState): pass
+    store.window = ResidentWindow(store, stage_names, torch.float16, slot.weights)
+    store.window.load()          # when the stage is loaded (disk.py:316-327's place)
+    ...
+    store.update(name, grad, step, lr, clip)   # unchanged call sites (disk.py:464)
+    """
+
+    window = None
+
+    def update(self, name, gradient, step, lr, clip, chunk_elements=1048576):
+        if self.window is not None and name in self.window.state:
+            return self.window.update(name, gradient, step, lr, clip, chunk_elements)
+        return super().update(name, gradient, step, lr, clip, chunk_elements)
