@@ -13,6 +13,9 @@ Contents, each restating the reference (paths relative to the MORPH repo):
   * disk_update_torch() -- streamtrain/disk.py:203-216 run with torch CPU ops;
   * orthogonalize_fp32()/muon_reference_step() -- streamtrain/optimizer.py:13-22,
     52-61 in FP32 torch CPU;
+  * export_fp16_reference() -- streamtrain/export.py:16-43 (numpy FP16 encoding,
+    per-shard SHA-256, the morph-fp16-shards-v1 manifest) without the run lock
+    and with the model passed in;
   * accumulate_torch()/norm_squared_torch() -- the stage-gradient window of
     streamtrain/sparse_disk.py:104-108 / disk.py:446-448 and the FP64 norm pass
     disk.py:466-468 / sparse_disk.py:136, with torch CPU ops.
@@ -292,6 +295,49 @@ def norm_squared_torch(gradients, chunk=1048576):
         for piece in g.flatten().split(chunk):
             total += piece.double().square().sum().item()
     return total
+
+
+def export_fp16_reference(state_dir, output, model, chunk_elements=1048576):
+    """export.py:16-43 on the CPU: same checks, encoding, hashing, manifest."""
+    import hashlib
+    import json
+    from pathlib import Path
+    state_dir, output = Path(state_dir), Path(output)
+    manifest = json.loads((state_dir / "manifest.json").read_text())
+    if manifest["dirty"]:
+        raise ValueError("cannot export an incomplete optimizer transaction")
+    entries = {name: dict(shape=list(p.shape), size=p.numel(), file=f"{i:05}.bin")
+               for i, (name, p) in enumerate(model.named_parameters())}
+    if entries != manifest["entries"]:
+        raise ValueError("disk state tensor schema differs")
+    output.mkdir(parents=True, exist_ok=False)
+    weights = {}
+    for name, entry in entries.items():
+        source = np.memmap(state_dir / entry["file"], dtype=np.float32, mode="r", shape=(3, entry["size"]))
+        path = output / entry["file"]
+        digest = hashlib.sha256()
+        with path.open("wb") as handle:
+            for start in range(0, entry["size"], chunk_elements):
+                value = np.asarray(source[0, start:start + chunk_elements])
+                if not np.isfinite(value).all() or np.abs(value).max(initial=0) > 65504:
+                    raise ValueError("weights cannot be represented by finite FP16")
+                encoded = value.astype("<f2").tobytes()
+                handle.write(encoded)
+                digest.update(encoded)
+        del source
+        weights[name] = dict(file=path.name, shape=entry["shape"], dtype="float16",
+                             sha256=digest.hexdigest())
+    canonical = {id(p): n for n, p in model.named_parameters()}
+    aliases = {n: canonical[id(p)] for n, p in model.named_parameters(remove_duplicate=False)
+               if canonical[id(p)] != n}
+    result = dict(format="morph-fp16-shards-v1", config=model.config.to_dict(), step=manifest["step"],
+                  weights=weights, aliases=aliases,
+                  lm_head=dict(kind="tied_embedding_projection", weight="embedding.weight"),
+                  parameters=sum(e["size"] for e in entries.values()), optimizer_included=False,
+                  buffers="deterministically reconstructed from config",
+                  source_precision="float32 masters", export_precision="float16")
+    (output / "manifest.json").write_text(json.dumps(result))
+    return result
 
 
 def cpu_threads():

@@ -1,0 +1,129 @@
+"""FP16 shard export (morph_amd.export) against the oracle's restatement of export.py:16-43.
+
+Shard files byte-identical (numpy's FP16 encoding), SHA-256 and manifest equal, the
+same ValueError at the same chunk with the same partial output, the same refusals
+(dirty state, existing output, held run lock), and the same result when the FP32 rows
+come from an HBM-resident window instead of the files.
+"""
+import fcntl
+import json
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from morph_amd.export import export_fp16
+from morph_amd.window import ResidentWindow
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+
+class Config:
+    def to_dict(self):
+        return dict(vocab=64, width=32, layers=1)
+
+
+class Tiny(nn.Module):
+    """Parameter layout with a tied head, like the reference model's (export.py:37-38)."""
+
+    def __init__(self):
+        super().__init__()
+        self.config = Config()
+        self.embedding = nn.Embedding(64, 32)
+        self.gate = nn.Linear(32, 48, bias=False)
+        self.norm = nn.LayerNorm(32)
+        self.lm_head = nn.Linear(32, 64, bias=False)
+        self.lm_head.weight = self.embedding.weight
+
+
+def make_state(root, model, seed=0, step=7, dirty=False, edits=None):
+    root.mkdir(parents=True)
+    entries = {n: dict(shape=list(p.shape), size=p.numel(), file=f"{i:05}.bin")
+               for i, (n, p) in enumerate(model.named_parameters())}
+    rng = np.random.RandomState(seed)
+    for name, e in entries.items():
+        state = np.zeros((3, e["size"]), np.float32)
+        state[0] = (rng.randn(e["size"]) * 3).astype(np.float32)
+        state[1:] = rng.randn(2, e["size"]).astype(np.float32)  # moments are never exported
+        for (ename, idx), value in (edits or {}).items():
+            if ename == name:
+                state[0, idx] = value
+        state.tofile(root / e["file"])
+    (root / "manifest.json").write_text(json.dumps(dict(entries=entries, step=step, dirty=dirty,
+                                                        config=Config().to_dict())))
+    return entries
+
+
+def same_dirs(a, b):
+    fa, fb = sorted(p.name for p in a.iterdir()), sorted(p.name for p in b.iterdir())
+    assert fa == fb, (fa, fb)
+    for name in fa:
+        if name == "manifest.json":
+            assert json.loads((a / name).read_text()) == json.loads((b / name).read_text())
+        else:
+            assert (a / name).read_bytes() == (b / name).read_bytes(), name
+
+
+@pytest.mark.parametrize("chunk", [100, 1048576])
+def test_export_matches_reference_bytes_and_manifest(tmp_path, chunk):
+    model = Tiny()
+    make_state(tmp_path / "run" / "state", model,
+               edits={("gate.weight", 5): 65504.0, ("gate.weight", 6): -65504.0,
+                      ("norm.weight", 0): 65503.9, ("norm.weight", 1): 1e-8})
+    got = export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", chunk, model=model)
+    ref = R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, chunk)
+    assert got == ref
+    assert got["aliases"] == {"lm_head.weight": "embedding.weight"}
+    same_dirs(tmp_path / "gpu", tmp_path / "cpu")
+
+
+@pytest.mark.parametrize("bad", [65504.5, 65519.0, float("inf"), float("nan")])
+def test_unrepresentable_weight_raises_at_the_same_chunk(tmp_path, bad):
+    """65519 rounds to 65504 in FP16 but the reference still refuses it (|w| > 65504)."""
+    model = Tiny()
+    make_state(tmp_path / "run" / "state", model, edits={("gate.weight", 700): bad})
+    with pytest.raises(ValueError, match="finite FP16"):
+        export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", 256, model=model)
+    with pytest.raises(ValueError, match="finite FP16"):
+        R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, 256)
+    same_dirs(tmp_path / "gpu", tmp_path / "cpu")  # same complete and partial shards
+
+
+def test_refusals(tmp_path):
+    model = Tiny()
+    make_state(tmp_path / "run" / "state", model, dirty=True)
+    with pytest.raises(ValueError, match="incomplete optimizer transaction"):
+        export_fp16(tmp_path / "run" / "state", tmp_path / "out", model=model)
+    assert not (tmp_path / "out").exists()
+    make_state(tmp_path / "run2" / "state", model)
+    (tmp_path / "exists").mkdir()
+    with pytest.raises(FileExistsError):
+        export_fp16(tmp_path / "run2" / "state", tmp_path / "exists", model=model)
+    with open(tmp_path / "run2" / "run.lock", "a+") as held:
+        fcntl.flock(held, fcntl.LOCK_EX | fcntl.LOCK_NB)
+        with pytest.raises(RuntimeError, match="stop training"):
+            export_fp16(tmp_path / "run2" / "state", tmp_path / "out2", model=model)
+    other = nn.Linear(3, 3)
+    other.config = Config()
+    with pytest.raises(ValueError, match="schema differs"):
+        export_fp16(tmp_path / "run2" / "state", tmp_path / "out3", model=other)
+
+
+def test_export_from_resident_window_equals_file_export(tmp_path):
+    model = Tiny()
+    entries = make_state(tmp_path / "run" / "state", model)
+
+    class Store:
+        root = tmp_path / "run" / "state"
+
+        def fault(self, point):
+            return None
+    store = Store()
+    store.entries = entries
+    win = ResidentWindow(store, list(entries), torch.float16)
+    win.load()
+    export_fp16(tmp_path / "run" / "state", tmp_path / "win", 300, model=model, window=win)
+    R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, 300)
+    same_dirs(tmp_path / "win", tmp_path / "cpu")
