@@ -25,6 +25,11 @@
  *                                       DynamicLossScale.overflow (precision.py:9-11)
  *   torch/optim/adam.py:347-547         _single_tensor_adam, the AdamW group's
  *                                       arithmetic (torch.optim.AdamW foreach=False)
+ *   streamtrain/sparse_disk.py:82-108,  stage-gradient accumulation and the FP64
+ *     136; disk.py:446-448, 466-468     norm pass
+ *   streamtrain/disk.py:316-327         CPU cast of the weight row for the stage load
+ *   streamtrain/export.py:32-34         FP16 encoding + range check of the export
+ *   streamtrain/precision.py:24-37      block-scaled FP8 pack / unpack
  */
 #ifndef MORPH_OPTIM_H
 #define MORPH_OPTIM_H
@@ -265,6 +270,21 @@ int morph_sumsq_total(const double* d_partials, int64_t n, double* d_out, int ac
  * export's "cannot be represented by finite FP16" condition. */
 int morph_convert_f32(const float* src, void* dst, int dst_dtype, int64_t n,
                       uint32_t* d_range_flag, void* stream);
+
+/* ---- Block-scaled FP8 (E4M3FN) transport ---------------------------------
+ * streamtrain/precision.py:24-37 (pack_fp8 / unpack_fp8), the opt-in FP8
+ * weight transfer of disk.py:330-345.  Blocks of MORPH_FP8_BLOCK elements,
+ * the last one padded with zeros for the amax only. */
+#define MORPH_FP8_BLOCK 256
+
+/* scales[b] = max(amax(|src block b|) / 448, 1e-30) (NaN if the block holds a
+ * NaN); bytes[i] = e4m3fn(clamp(src[i] / scale, -448, 448)), round to nearest
+ * even.  bytes: n entries; scales: ceil(n / 256) entries. */
+int morph_fp8_pack(const void* src, int src_dtype, int64_t n, uint8_t* bytes, float* scales,
+                   void* stream);
+/* dst[i] = dst_dtype(float(e4m3fn bytes[i]) * scales[i / 256]). */
+int morph_fp8_unpack(const uint8_t* bytes, const float* scales, int64_t n, void* dst, int dst_dtype,
+                     void* stream);
 
 /* ---- Hybrid Muon: Newton-Schulz orthogonalisation on bf16 MFMA ---------- */
 

@@ -23,13 +23,15 @@ EXPORTS = (
     "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
     "morph_adamw_multi_dev", "morph_step_end", "morph_grad_partials", "morph_grad_accumulate",
-    "morph_sumsq_total", "morph_convert_f32", "morph_gemm_nt_bf16",
+    "morph_sumsq_total", "morph_convert_f32", "morph_fp8_pack", "morph_fp8_unpack",
+    "morph_gemm_nt_bf16",
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
     "morph_muon_prepare", "morph_muon_newton_schulz", "morph_muon_finish",
 )
 GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 256, 256, 64
 GEMM_SYMMETRIC = 1
 ACCUM_ELEMS_PER_BLOCK, ACCUM_OVERWRITE, ACCUM_FINAL = 2048, 1, 2
+FP8_BLOCK = 256
 FATAL_MIN_SCALE = 1
 
 
@@ -118,6 +120,8 @@ def lib():
                                        vp, vp, i64, vp], i32),
             "morph_sumsq_total": ([vp, i64, vp, i32, vp], i32),
             "morph_convert_f32": ([vp, vp, i32, i64, vp, vp], i32),
+            "morph_fp8_pack": ([vp, i32, i64, vp, vp, vp], i32),
+            "morph_fp8_unpack": ([vp, vp, i64, vp, i32, vp], i32),
             "morph_gemm_nt_bf16": ([vp, vp, vp, vp, vp] + [i64] * 14 +
                                    [ctypes.c_float, ctypes.c_float, i32, vp], i32),
             "morph_muon_workspace_bytes": ([i64, i64, i32], ctypes.c_size_t),

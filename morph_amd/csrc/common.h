@@ -40,8 +40,13 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
 __device__ __forceinline__ float bf16_bits_to_float(uint32_t b16) {
   return __builtin_bit_cast(float, b16 << 16);
 }
-// Round to nearest even (IEEE conversion; overflow -> inf).
+// Round to nearest even (IEEE conversion; overflow -> inf).  The empty asm
+// pins f as a finished FP32 value: without it the compiler may fold a
+// preceding multiply and this conversion into v_fma_mixlo_f16 (a * b + 0),
+// which turns a -0 product into +0 -- torch and numpy convert the rounded
+// FP32 product, sign of zero included.
 __device__ __forceinline__ uint32_t float_to_half_bits(float f) {
+  asm volatile("" : "+v"(f));
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
 }
 // Round to nearest even; NaN -> 0x7FC0 like torch's c10::BFloat16.

@@ -1,0 +1,197 @@
+// Block-scaled FP8 (E4M3FN) transport encoding for gfx950:
+//   pack:   per 256-element block, scale = max(amax(|x|) / 448, 1e-30);
+//           byte = e4m3fn(clamp(x / scale, -448, 448))
+//   unpack: y = dtype(float(byte) * scale)
+// following streamtrain/precision.py:24-37 (pack_fp8 / unpack_fp8, used for
+// the opt-in FP8 weight transfer of disk.py:330-345).  The reference computes
+// with torch ops; the arithmetic here is the same sequence of FP32 operations
+// (IEEE division, one rounding each) so the bytes and scales are identical.
+//
+// E4M3FN: 1 sign, 4 exponent (bias 7), 3 mantissa bits; no infinities, NaN =
+// S.1111.111, largest finite 448, smallest subnormal 2^-9.  The conversion is
+// round to nearest even, written from the format definition: normal results
+// round the FP32 bit pattern at mantissa bit 20 (a carry moves into the
+// exponent), subnormal results are rint(|x| * 2^9); NaN stays NaN.  Inputs
+// here are already clamped to +-448, so the out-of-range case only arises for
+// NaN.  Torch propagates NaN through amax, clamp_min and clamp, so a block
+// with a NaN has a NaN scale and all-NaN bytes; that is reproduced too.
+//
+// One wave per block: 64 lanes x 4 elements = 256 (the block size); the amax
+// is a butterfly over the wave.  A workgroup holds 4 waves / 4 blocks.
+#include "common.h"
+
+namespace morph {
+namespace {
+
+constexpr int kBlockElems = MORPH_FP8_BLOCK;
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+static_assert(kBlockElems == 256, "one wave x 4 elements per block");
+
+__device__ __forceinline__ bool is_nan(float x) { return x != x; }
+
+// torch.amax: NaN if any element is NaN
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (is_nan(a) || is_nan(b)) ? __builtin_nanf("") : (a > b ? a : b);
+}
+
+__device__ __forceinline__ uint32_t e4m3fn_from_float(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7Fu;  // NaN
+  uint32_t r;
+  if (a < 0x3C800000u) {  // below 2^-6: subnormal (or zero) result, step 2^-9
+    r = (uint32_t)__builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
+  } else {
+    r = ((a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20) - (120u << 3);  // rebias 127 -> 7
+    if (r > 0x7Eu) r = 0x7Fu;  // beyond 448 after rounding: NaN (no infinities)
+  }
+  return sign | r;
+}
+
+__device__ __forceinline__ float float_from_e4m3fn(uint32_t b) {
+  const uint32_t e = (b >> 3) & 0xFu, m = b & 7u;
+  float v;
+  if (e == 0)
+    v = (float)m * 0.001953125f;  // m * 2^-9, exact
+  else if (e == 0xFu && m == 7u)
+    v = __builtin_nanf("");
+  else
+    v = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
+  return (b & 0x80u) ? -v : v;
+}
+
+template <typename IT>
+__device__ __forceinline__ void load4(const void* src, int64_t i, int64_t n, float (&x)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t j = i + k;
+    if (j < n) {
+      if constexpr (std::is_same_v<IT, F32>)
+        x[k] = static_cast<const float*>(src)[j];
+      else
+        x[k] = to_float<IT>(static_cast<const uint16_t*>(src)[j]);
+    } else {
+      x[k] = 0.0f;  // the reference pads the last block with zeros
+    }
+  }
+}
+
+template <typename IT>
+__global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__ src, int64_t n,
+                                                        uint8_t* __restrict__ bytes,
+                                                        float* __restrict__ scales,
+                                                        int64_t blocks) {
+  const int64_t blk = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (blk >= blocks) return;  // whole waves exit together
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blk * kBlockElems + lane * 4;
+  float x[4];
+  load4<IT>(src, i, n, x);
+  float m = nan_max(nan_max(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
+                    nan_max(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = nan_max(m, __shfl_xor(m, o));
+  float s = m / 448.0f;
+  s = (s < 1e-30f) ? 1e-30f : s;  // clamp_min keeps NaN
+  if (lane == 0) scales[blk] = s;
+  uint32_t word = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float q = x[k] / s;
+    q = is_nan(q) ? q : (q < -448.0f ? -448.0f : (q > 448.0f ? 448.0f : q));
+    word |= e4m3fn_from_float(q) << (8 * k);
+  }
+  if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(bytes) + i) & 3) == 0) {
+    *reinterpret_cast<uint32_t*>(bytes + i) = word;
+  } else {
+    for (int k = 0; k < 4; ++k)
+      if (i + k < n) bytes[i + k] = (uint8_t)(word >> (8 * k));
+  }
+}
+
+template <typename OT>
+__global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restrict__ bytes,
+                                                          const float* __restrict__ scales,
+                                                          int64_t n, void* __restrict__ dst,
+                                                          int64_t blocks) {
+  const int64_t blk = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (blk >= blocks) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t i = blk * kBlockElems + lane * 4;
+  const float s = scales[blk];
+  uint32_t word = 0;
+  if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(bytes) + i) & 3) == 0) {
+    word = *reinterpret_cast<const uint32_t*>(bytes + i);
+  } else {
+    for (int k = 0; k < 4; ++k)
+      if (i + k < n) word |= (uint32_t)bytes[i + k] << (8 * k);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (i + k >= n) break;
+    const float y = float_from_e4m3fn((word >> (8 * k)) & 0xFFu) * s;
+    if constexpr (std::is_same_v<OT, F32>)
+      static_cast<float*>(dst)[i + k] = y;
+    else
+      static_cast<uint16_t*>(dst)[i + k] = (uint16_t)from_float<OT>(y);
+  }
+}
+
+int64_t nblocks(int64_t n) { return (n + kBlockElems - 1) / kBlockElems; }
+
+}  // namespace
+}  // namespace morph
+
+using namespace morph;
+
+extern "C" int morph_fp8_pack(const void* src, int src_dtype, int64_t n, uint8_t* bytes,
+                              float* scales, void* stream) {
+  if (n < 0 || (n > 0 && (src == nullptr || bytes == nullptr || scales == nullptr)))
+    return MORPH_EINVAL;
+  if (n == 0) return MORPH_OK;
+  const int64_t blocks = nblocks(n);
+  const int64_t groups = (blocks + kWaves - 1) / kWaves;
+  if (groups > 0x7FFFFFFF) return MORPH_ERANGE;
+  hipStream_t s = as_stream(stream);
+  switch (src_dtype) {
+    case MORPH_DTYPE_F32:
+      hipLaunchKernelGGL(pack_kernel<F32>, dim3((unsigned)groups), dim3(kThreads), 0, s, src, n, bytes, scales, blocks);
+      break;
+    case MORPH_DTYPE_F16:
+      hipLaunchKernelGGL(pack_kernel<F16>, dim3((unsigned)groups), dim3(kThreads), 0, s, src, n, bytes, scales, blocks);
+      break;
+    case MORPH_DTYPE_BF16:
+      hipLaunchKernelGGL(pack_kernel<BF16>, dim3((unsigned)groups), dim3(kThreads), 0, s, src, n, bytes, scales, blocks);
+      break;
+    default:
+      return MORPH_EDTYPE;
+  }
+  return launch_status();
+}
+
+extern "C" int morph_fp8_unpack(const uint8_t* bytes, const float* scales, int64_t n, void* dst,
+                                int dst_dtype, void* stream) {
+  if (n < 0 || (n > 0 && (bytes == nullptr || scales == nullptr || dst == nullptr)))
+    return MORPH_EINVAL;
+  if (n == 0) return MORPH_OK;
+  const int64_t blocks = nblocks(n);
+  const int64_t groups = (blocks + kWaves - 1) / kWaves;
+  if (groups > 0x7FFFFFFF) return MORPH_ERANGE;
+  hipStream_t s = as_stream(stream);
+  switch (dst_dtype) {
+    case MORPH_DTYPE_F32:
+      hipLaunchKernelGGL(unpack_kernel<F32>, dim3((unsigned)groups), dim3(kThreads), 0, s, bytes, scales, n, dst, blocks);
+      break;
+    case MORPH_DTYPE_F16:
+      hipLaunchKernelGGL(unpack_kernel<F16>, dim3((unsigned)groups), dim3(kThreads), 0, s, bytes, scales, n, dst, blocks);
+      break;
+    case MORPH_DTYPE_BF16:
+      hipLaunchKernelGGL(unpack_kernel<BF16>, dim3((unsigned)groups), dim3(kThreads), 0, s, bytes, scales, n, dst, blocks);
+      break;
+    default:
+      return MORPH_EDTYPE;
+  }
+  return launch_status();
+}

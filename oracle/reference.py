@@ -16,6 +16,8 @@ Contents, each restating the reference (paths relative to the MORPH repo):
   * export_fp16_reference() -- streamtrain/export.py:16-43 (numpy FP16 encoding,
     per-shard SHA-256, the morph-fp16-shards-v1 manifest) without the run lock
     and with the model passed in;
+  * pack_fp8_torch()/unpack_fp8_torch() -- streamtrain/precision.py:24-37 with
+    torch CPU ops (float8_e4m3fn conversion);
   * accumulate_torch()/norm_squared_torch() -- the stage-gradient window of
     streamtrain/sparse_disk.py:104-108 / disk.py:446-448 and the FP64 norm pass
     disk.py:466-468 / sparse_disk.py:136, with torch CPU ops.
@@ -295,6 +297,40 @@ def norm_squared_torch(gradients, chunk=1048576):
         for piece in g.flatten().split(chunk):
             total += piece.double().square().sum().item()
     return total
+
+
+def pack_fp8_torch(value, block_size=256):
+    """precision.py:24-30: E4M3FN bytes + FP32 per-block scale."""
+    import torch
+    flat = value.detach().float().flatten()
+    padding = (-flat.numel()) % block_size
+    padded = torch.nn.functional.pad(flat, (0, padding)).reshape(-1, block_size)
+    scales = (padded.abs().amax(1) / 448.).clamp_min(1e-30)
+    encoded = (padded / scales[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(
+        torch.uint8).flatten()[:flat.numel()]
+    return encoded, scales
+
+
+def unpack_fp8_torch(encoded, scales, dtype=None, block_size=256):
+    """precision.py:33-37."""
+    import torch
+    dtype = dtype or torch.float16
+    size = encoded.numel()
+    padding = (-size) % block_size
+    padded = torch.nn.functional.pad(encoded, (0, padding))
+    values = padded.view(torch.float8_e4m3fn).float().reshape(-1, block_size)
+    return (values * scales[:, None]).to(dtype).flatten()[:size]
+
+
+def e4m3fn_value(byte):
+    """E4M3FN decoded from the format definition (1-4-3, bias 7, no inf, S.1111.111 = NaN)."""
+    sign = -1.0 if byte & 0x80 else 1.0
+    e, m = (byte >> 3) & 0xF, byte & 7
+    if e == 15 and m == 7:
+        return float("nan")
+    if e == 0:
+        return sign * m * 2.0 ** -9
+    return sign * (1 + m / 8) * 2.0 ** (e - 7)
 
 
 def export_fp16_reference(state_dir, output, model, chunk_elements=1048576):

@@ -1,0 +1,90 @@
+"""GPU FP8 block-scaled pack/unpack (morph_amd.fp8) against the oracle (precision.py:24-37).
+
+Bytes and scales bit-exact for FP32/FP16/BF16 inputs, ragged sizes and wide dynamic
+range (subnormal codes); an exhaustive conversion sweep over every finite FP16 value
+with |v| <= 448 at scale 1; zero and NaN blocks; unpack of all 256 codes at several
+scales into FP16/BF16/FP32; the reference's 4% roundtrip bound.
+"""
+import numpy as np
+import pytest
+import torch
+
+from morph_amd import fp8
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def same(a, b):
+    """Bitwise equality, with any NaN equal to any NaN."""
+    a, b = a.cpu(), b.cpu()
+    if a.dtype == torch.uint8:
+        nan = lambda t: (t & 0x7F) == 0x7F
+        return torch.equal(nan(a), nan(b)) and torch.equal(a[~nan(a)], b[~nan(b)])
+    an, bn = torch.isnan(a.float()), torch.isnan(b.float())
+    view = {torch.float32: torch.int32, torch.float16: torch.int16, torch.bfloat16: torch.int16}[a.dtype]
+    return torch.equal(an, bn) and torch.equal(a[~an].view(view), b[~bn].view(view))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("n", [1, 255, 256, 257, 519, 70001])
+def test_pack_bitexact_vs_reference(dtype, n):
+    gen = torch.Generator().manual_seed(n)
+    x = torch.randn(n, generator=gen) * torch.exp(torch.randn(n, generator=gen) * 4)  # wide range
+    x = x.to(dtype)
+    enc, sc = fp8.pack_fp8(x.to(DEV))
+    renc, rsc = R.pack_fp8_torch(x)
+    assert same(sc, rsc) and same(enc, renc)
+
+
+def test_conversion_exhaustive_over_fp16_values():
+    """Blocks led by 448 have scale exactly 1, so bytes are the plain conversion of every
+    finite FP16 value in [-448, 448] (and of random FP32 values)."""
+    h = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(torch.float16).float()
+    vals = h[torch.isfinite(h) & (h.abs() <= 448)]
+    vals = torch.cat([vals, (torch.rand(100000, generator=torch.Generator().manual_seed(1)) - .5) * 896])
+    blocks = vals.split(255)
+    x = torch.cat([torch.cat([torch.tensor([448.0]), b, torch.zeros(255 - b.numel())]) for b in blocks])
+    enc, sc = fp8.pack_fp8(x.to(DEV))
+    assert torch.equal(sc.cpu(), torch.ones_like(sc.cpu()))
+    assert torch.equal(enc.cpu(), x.to(torch.float8_e4m3fn).view(torch.uint8))
+
+
+def test_zero_and_nan_blocks():
+    x = torch.zeros(1024)
+    x[300] = float("nan")
+    x[600:700] = torch.linspace(-1, 1, 100)
+    enc, sc = fp8.pack_fp8(x.to(DEV))
+    renc, rsc = R.pack_fp8_torch(x)
+    assert same(sc, rsc) and same(enc, renc)
+    assert sc[0].item() == np.float32(1e-30) and torch.isnan(sc[1].cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_unpack_all_codes_bitexact(dtype):
+    codes = torch.arange(256, dtype=torch.uint8).repeat(5)
+    scales = torch.tensor([1.0, 1e-30, 0.01, 3.5, 2.0 ** 20], dtype=torch.float32)
+    got = fp8.unpack_fp8(codes.to(DEV), scales.to(DEV), dtype)
+    assert same(got, R.unpack_fp8_torch(codes, scales, dtype))
+
+
+def test_reference_roundtrip_bound_on_gpu():
+    torch.manual_seed(2)
+    values = torch.randn(519)
+    enc, sc = fp8.pack_fp8(values.to(DEV))
+    restored = fp8.unpack_fp8(enc, sc, torch.float32).cpu()
+    assert (restored - values).norm() / values.norm() < .04
+    assert not fp8.fp8_eligible('embedding.weight') and fp8.fp8_eligible('blocks.3.ffn.up.weight')
+
+
+def test_config2_window_roundtrip_matches_reference_full_size():
+    """A full [6144, 3072] FP16 weight against the reference's ops on the CPU, where the
+    reference packs (disk.py:330-345 packs slot.host).  torch's GPU kernels would not do:
+    they divide by the Python scalar 448 as a multiply by its rounded reciprocal."""
+    gen = torch.Generator(device=DEV).manual_seed(4)
+    w = (torch.randn(6144, 3072, generator=gen, device=DEV) * .02).half()
+    enc, sc = fp8.pack_fp8(w)
+    renc, rsc = R.pack_fp8_torch(w.cpu())
+    assert same(sc, rsc) and same(enc, renc)
+    assert same(fp8.unpack_fp8(enc, sc, torch.float16), R.unpack_fp8_torch(renc, rsc, torch.float16))
