@@ -436,6 +436,90 @@ def window_main(args):
         shutil.rmtree(root, ignore_errors=True)
 
 
+FP8_PACK_BYTES, FP8_UNPACK_BYTES = 3, 3  # FP16 in 2 + byte out 1 (+ 4 B per 256); byte in 1 + FP16 out 2
+
+
+def time_fp8(steps, warmup):
+    """FP8 transport (precision.py:24-37) of the config-2 window's FP16 compute weights."""
+    from morph_amd import fp8
+    device = torch.device("cuda", 0)
+    gen = torch.Generator(device=device).manual_seed(9)
+    w = [(torch.randn(s, generator=gen, device=device) * .02).half() for s in CONFIG2_SHAPES]
+    n = sum(t.numel() for t in w)
+    stream = torch.cuda.current_stream()
+
+    def one(tp=None, tu=None):
+        packed = []
+        for t in w:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            packed.append(fp8.pack_fp8(t))
+            b.record(stream)
+            if tp is not None:
+                tp.append((a, b))
+        for (enc, sc) in packed:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fp8.unpack_fp8(enc, sc, torch.float16)
+            b.record(stream)
+            if tu is not None:
+                tu.append((a, b))
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    tp, tu = [], []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one(tp, tu)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    pack_s = sum(a.elapsed_time(b) for a, b in tp) / 1e3 / steps
+    unpack_s = sum(a.elapsed_time(b) for a, b in tu) / 1e3 / steps
+    return dict(n=n, elapsed=elapsed, pack_s=pack_s, unpack_s=unpack_s)
+
+
+def cpu_baseline_fp8():
+    """The reference's pack_fp8 / unpack_fp8 (torch CPU ops) on one [6144, 3072] FP16 weight."""
+    from oracle import reference as R
+    threads = min(16, R.cpu_threads())
+    torch.set_num_threads(threads)
+    w = (torch.randn(6144, 3072, generator=torch.Generator().manual_seed(9)) * .02).half()
+    t0 = time.perf_counter()
+    enc, sc = R.pack_fp8_torch(w)
+    t_pack = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    R.unpack_fp8_torch(enc, sc, torch.float16)
+    t_unpack = time.perf_counter() - t0
+    return dict(value=round(w.numel() / t_pack / 1e9, 4), unit="Gparams/s (pack)", cores=threads,
+                kind="port", sample=f"one [6144, 3072] FP16 weight: pack {t_pack * 1e3:.0f} ms, "
+                                    f"unpack {t_unpack * 1e3:.0f} ms ({w.numel() / t_unpack / 1e9:.3f} Gparam/s)")
+
+
+def fp8_main(args):
+    r = time_fp8(args.steps, args.warmup)
+    n = r["n"]
+    achieved = FP8_UNPACK_BYTES * n / r["unpack_s"] / 1e9
+    line = {
+        "metric": "FP8 E4M3FN block-scaled pack + unpack Gparams/s, 5B SwiGLU window, 1 MI355X",
+        "value": round(n * args.steps / r["elapsed"] / 1e9, 3), "unit": "Gparams/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(r["elapsed"] / args.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "config 2 window FP16 compute weights: pack to E4M3FN + per-256 FP32 "
+                               "scales, unpack back to FP16 (3 tensors)", "params": n,
+                   "shapes": CONFIG2_SHAPES},
+        "pack_gparams_per_s": round(n / r["pack_s"] / 1e9, 2),
+        "unpack_gparams_per_s": round(n / r["unpack_s"] / 1e9, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "unpack_kernel<F16>", "avg_launch_us": round(r["unpack_s"] / 3 * 1e6, 2),
+                     "bytes_per_launch": FP8_UNPACK_BYTES * n // 3},
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_fp8(),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def measured_traffic():
     """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
     try:
@@ -450,9 +534,11 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("adamw", "muon", "grads", "window"), default="adamw",
+    ap.add_argument("--workload", choices=("adamw", "muon", "grads", "window", "fp8"),
+                    default="adamw",
                     help="adamw: the headline config-2 step (default); muon: config 5; "
-                         "grads: the stage-gradient window; window: the HBM-resident [3, N] state")
+                         "grads: the stage-gradient window; window: the HBM-resident [3, N] "
+                         "state; fp8: block-scaled FP8 transport encoding")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()
@@ -478,6 +564,8 @@ def main():
         return grads_main(args)
     if args.workload == "window":
         return window_main(args)
+    if args.workload == "fp8":
+        return fp8_main(args)
     r = time_gpu(args.steps, args.warmup)
     n = r["n"]
     ms_per_step = r["elapsed"] / args.steps * 1e3

@@ -64,6 +64,18 @@ __device__ __forceinline__ float float_from_e4m3fn(uint32_t b) {
 
 template <typename IT>
 __device__ __forceinline__ void load4(const void* src, int64_t i, int64_t n, float (&x)[4]) {
+  constexpr int kBytes = Fmt<IT>::bytes;
+  if (i + 4 <= n && (reinterpret_cast<uintptr_t>(src) + i * kBytes) % (4 * kBytes) == 0) {
+    if constexpr (std::is_same_v<IT, F32>) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + i);
+      x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    } else {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(static_cast<const uint16_t*>(src) + i);
+      x[0] = to_float<IT>(v.x & 0xFFFFu); x[1] = to_float<IT>(v.x >> 16);
+      x[2] = to_float<IT>(v.y & 0xFFFFu); x[3] = to_float<IT>(v.y >> 16);
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int64_t j = i + k;
@@ -128,14 +140,27 @@ __global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restr
     for (int k = 0; k < 4; ++k)
       if (i + k < n) word |= (uint32_t)bytes[i + k] << (8 * k);
   }
+  float y[4];
 #pragma unroll
+  for (int k = 0; k < 4; ++k) y[k] = float_from_e4m3fn((word >> (8 * k)) & 0xFFu) * s;
+  constexpr int kBytes = Fmt<OT>::bytes;
+  if (i + 4 <= n && (reinterpret_cast<uintptr_t>(dst) + i * kBytes) % (4 * kBytes) == 0) {
+    if constexpr (std::is_same_v<OT, F32>) {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(dst) + i) = f32x4{y[0], y[1], y[2], y[3]};
+    } else {
+      u32x2 v;
+      v.x = from_float<OT>(y[0]) | (from_float<OT>(y[1]) << 16);
+      v.y = from_float<OT>(y[2]) | (from_float<OT>(y[3]) << 16);
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(dst) + i) = v;
+    }
+    return;
+  }
   for (int k = 0; k < 4; ++k) {
     if (i + k >= n) break;
-    const float y = float_from_e4m3fn((word >> (8 * k)) & 0xFFu) * s;
     if constexpr (std::is_same_v<OT, F32>)
-      static_cast<float*>(dst)[i + k] = y;
+      static_cast<float*>(dst)[i + k] = y[k];
     else
-      static_cast<uint16_t*>(dst)[i + k] = (uint16_t)from_float<OT>(y);
+      static_cast<uint16_t*>(dst)[i + k] = (uint16_t)from_float<OT>(y[k]);
   }
 }
 
