@@ -39,13 +39,14 @@
 // transposed into the mirror position, halving the work of those products.
 //
 // Epilogue.  Each lane combines alpha * acc + beta * D in fp32 and rounds once
-// to bf16 (packed converter, round to nearest even).  In the MFMA output layout
+// to bf16 (packed converter, round to nearest even).  D and C pass through an
+// LDS copy of the tile for coalesced 16-byte rows.  In the MFMA output layout
 // four consecutive registers of a lane are four consecutive rows of one
 // column, i.e. 8 contiguous bytes of a row of the transposed tile: Ct and the
-// mirror tile of a symmetric product are stored straight from registers.  The
-// row-major C and D pass through an LDS copy of the tile for coalesced 16-byte
-// rows.  Loads are issued in batches ahead of their use so the epilogue pays
-// memory latency a few times, not per element.
+// mirror tile of a symmetric product are written into the same LDS with one
+// 64-bit write per four values, then leave as coalesced rows too.  Loads are
+// issued in batches ahead of their use so the epilogue pays memory latency a
+// few times, not per element.
 //
 // MFMA 32x32x16 lane layout (checked on the device): lane l holds
 // A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32] for i < 8; output
@@ -124,19 +125,41 @@ __device__ __forceinline__ void tile_of(const GemmArgs& g, int t, int& tr, int& 
 
 enum DMode { kNoD, kDRowMajor };
 
+// dst rows (256 x 256 bf16, leading dimension ld) from the LDS tile E, in
+// coalesced 16-byte chunks; reads are batched 8 per lane ahead of the stores.
+__device__ __forceinline__ void store_tile(const uint16_t* E, uint16_t* dst, uint32_t ld) {
+  constexpr int kChunks = BM * (BN / 8) / kThreads;  // 32 per lane
+  constexpr int kBatch = 8;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int b = 0; b < kChunks; b += kBatch) {
+    u32x4 v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int c = tid + (b + i) * kThreads;
+      v[i] = *reinterpret_cast<const u32x4*>(E + (c / (BN / 8)) * LDE + (c % (BN / 8)) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int c = tid + (b + i) * kThreads;
+      *reinterpret_cast<u32x4*>(dst + ((uint32_t)(c / (BN / 8)) * ld + (c % (BN / 8)) * 8)) = v[i];
+    }
+  }
+}
+
 // Epilogue of one tile.  acc[i][j][r] of lane (fh, fr) of wave (wr, wc) is tile
 // element (wr + 32 i + 8 (r / 4) + 4 fh + r % 4, wc + 32 j + fr).  The D mode
 // and the alpha multiply are template parameters so that each variant is
 // straight-line code.
 template <int kDMode, bool kScaled>
-__device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[4][4],
+__device__ __forceinline__ void epilogue(const GemmArgs& g, f32x16 (&acc)[4][4],
                                          uint16_t* smem, const uint16_t* D, uint16_t* C,
                                          uint16_t* T, int64_t ldt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
   const int fr = lane & 31, fh = lane >> 5;
   uint16_t* E = smem;  // [BM][LDE] bf16 copy of the output tile
-  const uint32_t ldd = (uint32_t)g.ldd, lt = (uint32_t)ldt;
+  const uint32_t ldd = (uint32_t)g.ldd;
 
   if (kDMode == kDRowMajor) {
     // Row-major D into the LDS tile, all 32 loads of a lane in flight at once.
@@ -155,8 +178,9 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
     __syncthreads();
   }
   // Per element: (alpha *) acc, fma with beta * D, one RNE rounding to bf16 by
-  // the packed converter (two rows per instruction; the packed pairs are the
-  // transposed tile's 4-byte halves as they are).
+  // the packed converter (two rows per instruction).  The FP32 result goes
+  // back into acc (accumulation registers, free by now) so the transposed pass
+  // can round it again to the same bits without holding 128 packed words.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -165,10 +189,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
       const int rbase = wr + i * 32 + fh * 4;
       float dval[16];
       if (kDMode == kDRowMajor) {
-        // all 16 reads of the block before its writes: one LDS round trip
+        // all 16 reads of the block before its arithmetic and writes: one LDS round
+        // trip (the barrier keeps the scheduler from splitting them into short batches)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           dval[r] = bf16_bits_to_float(E[(rbase + (r >> 2) * 8 + (r & 3)) * LDE + col]);
+        __builtin_amdgcn_sched_barrier(0);
       }
       float x[16];
 #pragma unroll
@@ -176,40 +202,41 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, const f32x16 (&acc)[
         x[r] = kScaled ? g.alpha * acc[i][j][r] : acc[i][j][r];
         if (kDMode != kNoD) x[r] = __fmaf_rn(g.beta, dval[r], x[r]);
       }
-      uint32_t w[8];  // w[k]: rows rbase + 8 (k / 2) + 2 (k % 2) + {0, 1} of column col
-#pragma unroll
-      for (int k = 0; k < 8; ++k) w[k] = pack_bf16x2(x[2 * k], x[2 * k + 1]);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
+        // w: rows row and row + 1 of column col
+        const uint32_t w = pack_bf16x2(x[2 * k], x[2 * k + 1]);
         const int row = rbase + (k >> 1) * 8 + (k & 1) * 2;
-        E[row * LDE + col] = (uint16_t)w[k];
-        E[(row + 1) * LDE + col] = (uint16_t)(w[k] >> 16);
+        E[row * LDE + col] = (uint16_t)w;
+        E[(row + 1) * LDE + col] = (uint16_t)(w >> 16);
       }
-      if (T) {
+      if (kDMode != kNoD || kScaled) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          u32x2 v;
-          v.x = w[2 * q];
-          v.y = w[2 * q + 1];
-          *reinterpret_cast<u32x2*>(T + ((uint32_t)col * lt + (uint32_t)(rbase + q * 8))) = v;
-        }
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = x[r];
       }
     }
   }
   __syncthreads();
-  // C rows from the LDS tile: all 32 reads of a lane, then the 32 stores.
-  constexpr int kCChunks = BM * (BN / 8) / kThreads;
-  const uint32_t ldc = (uint32_t)g.ldc;
-  u32x4 cv[kCChunks];
+  store_tile(E, C, (uint32_t)g.ldc);  // C rows from the LDS tile
+  if (T) {
+    // Transposed copy (Ct, or the mirror tile): ET[c][r] = tile[r][c] in the
+    // same LDS.  Four consecutive rows of one column are 8 contiguous bytes of
+    // an ET row, so every two packed pairs go out with one 64-bit LDS write;
+    // then ET's rows leave as coalesced 16-byte stores like C's.
+    __syncthreads();  // every lane has read its C rows out of E
 #pragma unroll
-  for (int i = 0; i < kCChunks; ++i) {
-    const int c = tid + i * kThreads;
-    cv[i] = *reinterpret_cast<const u32x4*>(E + (c / (BN / 8)) * LDE + (c % (BN / 8)) * 8);
-  }
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-  for (int i = 0; i < kCChunks; ++i) {
-    const int c = tid + i * kThreads;
-    *reinterpret_cast<u32x4*>(C + ((uint32_t)(c / (BN / 8)) * ldc + (c % (BN / 8)) * 8)) = cv[i];
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x2 v;
+          v.x = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+          v.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          *reinterpret_cast<u32x2*>(E + (wc + j * 32 + fr) * LDE + wr + i * 32 + fh * 4 + q * 8) = v;
+        }
+    __syncthreads();
+    store_tile(E, T, (uint32_t)ldt);
   }
 }
 
