@@ -11,22 +11,24 @@
 //
 // Tiling.  A workgroup (256 lanes, 4 wave64) owns a 256 x 256 tile of C; wave w
 // owns the 128 x 128 quarter (w / 2, w % 2) as 4 x 4 tiles of
-// v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane).  Per 32x32x16
-// step a wave reads 8 fragments (8 KiB) from LDS for 16 MFMAs.
+// v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane).  Per 16-deep
+// sub-step a wave reads 8 fragments (8 KiB) from LDS for 16 MFMAs.
 //
-// Operand pipeline.  K advances 32 per stage through a ring of kStages LDS
-// buffers (32 KiB each: P and Q sub-tiles of 256 x 32 bf16) plus one stage of
-// fragments in registers.  Operands go global -> LDS directly
+// Operand pipeline.  K advances 64 per stage through two LDS buffers (64 KiB
+// each: P and Q sub-tiles of 256 x 64 bf16) and two register sets of
+// fragments, one per 16-deep sub-step.  Operands go global -> LDS directly
 // (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS
-// base + 16 l), so no registers are spent on staging; a stage is issued three
-// steps before it is read (about 3000 MFMA cycles of cover).  One LDS-only
-// barrier per stage; the fragment reads of the next stage and the DMA issue of
-// a later one are interleaved one per MFMA with the current stage's MFMAs.
-// Because the DMA writes LDS linearly, rows cannot be padded; instead the four
-// 16-byte chunks of each 64-byte row are stored XOR-swizzled (slot = chunk ^
-// ((row >> 2) & 3)), chosen on the load side by which global chunk each lane
-// fetches, so the 128-bit fragment reads of 16 consecutive rows hit distinct
-// banks.
+// base + 16 l), so no registers are spent on staging.  A row of a stage is one
+// 128-byte line and its eight chunks are fetched by eight adjacent lanes, so
+// every L2 request is a full line (32-deep stages fetch half lines and double
+// the request count for the same bytes).  The DMA of stage s + 2 is issued in
+// the last sub-step of stage s, right after the one LDS-only barrier per
+// stage; each sub-step's 16 MFMAs run under the fragment reads of the next.
+// Because the DMA writes LDS linearly, rows cannot be padded; instead the
+// eight 16-byte chunks of each 128-byte row are stored XOR-swizzled (slot =
+// chunk ^ ((row ^ (row >> 3)) & 7)), chosen on the load side by which global
+// chunk each lane fetches, so the 128-bit fragment reads of 8 or 16
+// consecutive rows hit distinct banks.
 //
 // Workgroup order.  The dispatcher hands workgroup i to XCD i % 8; each XCD
 // has its own L2.  Tiles are therefore numbered so that the workgroups one
@@ -64,16 +66,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = MORPH_GEMM_TILE_M;
 constexpr int BN = MORPH_GEMM_TILE_N;
-constexpr int BKS = 32;              // K per pipeline stage
-constexpr int kStages = 4;
+constexpr int BK = 64;               // K per pipeline stage: one 128-byte line per row
+constexpr int kStages = 2;
 constexpr int LDE = BN + 8;          // padded LDS row of the output tile (bf16)
 constexpr int kThreads = 256;
-constexpr int kSubTile = BM * BKS;                   // bf16 per operand sub-tile (256 x 32)
+constexpr int kSubTile = BM * BK;                    // bf16 per operand sub-tile (256 x 64)
 constexpr int kStageElems = 2 * kSubTile;            // P and Q
-constexpr int kLoadsPerOperand = kSubTile * 2 / 1024 / (kThreads / 64);  // 1 KiB DMA per wave-instr (4)
 constexpr int kSmemElems = (kStages * kStageElems > BM * LDE) ? kStages * kStageElems : BM * LDE;
 constexpr int kGroupM = 4;
-static_assert(BM == BN && BM == 256 && MORPH_GEMM_TILE_K % BKS == 0, "256 x 256 tiles, K % 32");
+static_assert(BM == BN && BM == 256 && MORPH_GEMM_TILE_K % BK == 0, "256 x 256 tiles, K % 64");
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -259,21 +260,19 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
   const uint16_t* P = g.P + b * g.sp + row0 * g.ldp;
   const uint16_t* Q = g.Q + b * g.sq + col0 * g.ldq;
 
-  // DMA assignment: wave w, load j covers rows (w * 4 + j) * 16 .. +16 of a sub-tile;
-  // lane l -> row base + l / 4, LDS slot l % 4 holding global chunk slot ^ swz(row).
-  const int lrow = lane >> 2, lslot = lane & 3;
-  // DMA load j (0..7) of a stage: operand j & 1 (P, Q), 16-row block j >> 1 of this wave.
+  // DMA assignment: per stage a wave loads 64 rows of each operand, 8 rows per
+  // instruction; lane l -> row base + l / 8, LDS slot l % 8, which holds the
+  // global 16-byte chunk slot ^ swz(row).  The eight lanes of a row fetch the
+  // eight chunks of one 128-byte line (one full-line request).
+  const int lrow = lane >> 3, lslot = lane & 7;
+  auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
+  // DMA load j (0..15) of a stage: operand j & 1 (P, Q), 8-row block j >> 1 of this wave.
   auto issue_load = [&](int buf, int64_t k0, int j) {
-    const int blk = wave * kLoadsPerOperand + (j >> 1);
-    const int r = blk * 16 + lrow;
-    const int c = lslot ^ ((r >> 2) & 3);
-    uint16_t* dst = smem + buf * kStageElems + (j & 1) * kSubTile + blk * 16 * BKS;
+    const int r = wave * 64 + (j >> 1) * 8 + lrow;
+    const int c = lslot ^ swz(r);
+    uint16_t* dst = smem + buf * kStageElems + (j & 1) * kSubTile + (wave * 64 + (j >> 1) * 8) * BK;
     const uint16_t* src = (j & 1) ? Q + r * g.ldq : P + r * g.ldp;
     __builtin_amdgcn_global_load_lds(src + k0 + c * 8, (lds_void*)dst, 16, 0, 0);
-  };
-  auto issue_stage = [&](int buf, int64_t k0) {
-#pragma unroll
-    for (int j = 0; j < 2 * kLoadsPerOperand; ++j) issue_load(buf, k0, j);
   };
 
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
@@ -284,93 +283,106 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  // Fragment of row R, 16-byte chunk c (c = 2 kk16 + k half): swizzled slot.
+  // Fragment of row R, 16-byte chunk c (c = 2 kk + k half, kk < 4): swizzled slot.
   auto frag = [&](const uint16_t* sub, int R, int c) {
-    return *reinterpret_cast<const bf16x8*>(sub + R * BKS + ((c ^ ((R >> 2) & 3)) * 8));
+    return *reinterpret_cast<const bf16x8*>(sub + R * BK + ((c ^ swz(R)) * 8));
   };
 
   // Workgroup barrier for LDS only: the memory clobber keeps the compiler from
-  // moving LDS accesses across it and no vmcnt wait is attached, so younger
-  // stages stay in flight (__syncthreads would drain every outstanding load).
+  // moving LDS accesses across it and no vmcnt wait is attached, so the DMA
+  // of the next stage stays in flight (__syncthreads would drain it).
   auto lds_barrier = []() { asm volatile("s_barrier" ::: "memory"); };
-  auto read_frags = [&](int stage, bf16x8 (&a)[BKS / 16][4], bf16x8 (&q)[BKS / 16][4]) {
-    const uint16_t* sP = smem + stage * kStageElems;
-    const uint16_t* sQ = sP + kSubTile;
-#pragma unroll
-    for (int kk = 0; kk < BKS / 16; ++kk)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[kk][i] = frag(sP, wr + i * 32 + fr, kk * 2 + fh);
-        q[kk][i] = frag(sQ, wc + i * 32 + fr, kk * 2 + fh);
-      }
+  // Fragments of one 16-deep sub-step: 4 P rows-blocks and 4 Q row-blocks.
+  struct Frags {
+    bf16x8 a[4], q[4];
   };
-  auto mfma = [&](int n, const bf16x8 (&ca)[BKS / 16][4], const bf16x8 (&cq)[BKS / 16][4]) {
-    const int kk = n >> 4, i = (n >> 2) & 3, j = n & 3;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[kk][i], cq[kk][j], acc[i][j], 0, 0, 0);
+  auto mfma = [&](int n, const Frags& f) {
+    const int i = n >> 2, j = n & 3;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.q[j], acc[i][j], 0, 0, 0);
+  };
+  auto read = [&](int n, Frags& f, int buf, int kk) {
+    const uint16_t* sP = smem + buf * kStageElems;
+    const int i = n >> 1;
+    if (n & 1)
+      f.q[i] = frag(sP + kSubTile, wc + i * 32 + fr, kk * 2 + fh);
+    else
+      f.a[i] = frag(sP, wr + i * 32 + fr, kk * 2 + fh);
   };
 
-  // Pipeline: kStages LDS buffers plus one register stage.  At step kt the
-  // registers hold stage kt, buffer (kt + 1) % kStages holds stage kt + 1 and
-  // the two after it are in flight.  After the barrier the buffer of stage kt
-  // is refilled with stage kt + kStages (past the end: the last stage again, so
-  // every step keeps the same number of loads in flight and has no branch),
-  // and the LDS reads of stage kt + 1 run under the 32 MFMAs of stage kt.
-  // The scheduling barriers pin that order: without them the compiler is free
-  // to hoist the final LDS wait above the MFMAs.
-  const int64_t KT = g.K / BKS;  // even, >= 2
-  auto issue = [&](int buf, int64_t stage) {
-    issue_stage(buf, (stage < KT ? stage : KT - 1) * BKS);
-  };
-  for (int s = 0; s < kStages; ++s) issue(s, s);
-  __builtin_amdgcn_s_waitcnt(0x4F78);  // vmcnt(24): stage 0 landed
-  lds_barrier();
-  bf16x8 a0[BKS / 16][4], q0[BKS / 16][4], a1[BKS / 16][4], q1[BKS / 16][4];
-  read_frags(0, a0, q0);
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-
-  auto step = [&](int64_t kt, const bf16x8 (&ca)[BKS / 16][4], const bf16x8 (&cq)[BKS / 16][4],
-                  bf16x8 (&na)[BKS / 16][4], bf16x8 (&nq)[BKS / 16][4]) {
-    // Two MFMAs of the registered stage go first so the unit is busy across
-    // the barrier; then one LDS fragment read or one DMA issue per MFMA.
-    mfma(0, ca, cq);
-    mfma(1, ca, cq);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): stage kt + 1 landed for this wave
-    lds_barrier();
-    const uint16_t* sP = smem + (int)((kt + 1) % kStages) * kStageElems;
-    const uint16_t* sQ = sP + kSubTile;
+  // Pipeline: two LDS stages of K = 64 and two register sets of fragments
+  // (F0, F1) of one 16-deep sub-step each.  Step s computes stage s from
+  // buffer s % 2 in four sub-steps; each sub-step's 16 MFMAs run while the
+  // next sub-step's 8 fragments are read.  Before the last sub-step one
+  // barrier (after this wave's vmcnt(0)) both frees buffer s % 2 -- every
+  // wave has its last fragments in registers -- and publishes stage s + 1 in
+  // the other buffer; the last sub-step then reads the first fragments of
+  // stage s + 1 and issues the DMA of stage s + 2 into buffer s % 2, which
+  // has about three sub-steps of MFMA time to land.  The scheduling barriers
+  // pin the interleave: without them the compiler is free to hoist the LDS
+  // waits above the MFMAs.
+  const int64_t KT = g.K / BK;  // >= 1
+  Frags f0, f1;
+  auto substep = [&](const Frags& cur, Frags& nxt, int buf, int kk) {
 #pragma unroll
     for (int n = 0; n < 16; ++n) {
-      mfma(n + 2, ca, cq);
+      mfma(n, cur);
       __builtin_amdgcn_sched_barrier(0);
-      const int kk = n >> 3, i = (n >> 1) & 3;
-      if (n & 1)
-        nq[kk][i] = frag(sQ, wc + i * 32 + fr, kk * 2 + fh);
-      else
-        na[kk][i] = frag(sP, wr + i * 32 + fr, kk * 2 + fh);
+      if (n < 8) read(n, nxt, buf, kk);
       __builtin_amdgcn_sched_barrier(0);
     }
-    const int64_t next = kt + kStages;
-    const int64_t k0 = (next < KT ? next : KT - 1) * BKS;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      mfma(j + 18, ca, cq);
-      __builtin_amdgcn_sched_barrier(0);
-      issue_load((int)(kt % kStages), k0, j);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int n = 26; n < 32; ++n) mfma(n, ca, cq);
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): stage kt + 1 is in registers
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): next fragments in registers
   };
-  for (int64_t kt = 0; kt + 2 < KT; kt += 2) {
-    step(kt, a0, q0, a1, q1);
-    step(kt + 1, a1, q1, a0, q0);
-  }
-  step(KT - 2, a0, q0, a1, q1);
+  // kNext: a stage s + 1 exists; kIssue: a stage s + 2 exists.
+  auto step = [&](int64_t s, auto next_tag, auto issue_tag) {
+    constexpr bool kNext = decltype(next_tag)::value, kIssue = decltype(issue_tag)::value;
+    const int buf = (int)(s & 1);
+    substep(f0, f1, buf, 1);
+    substep(f1, f0, buf, 2);
+    substep(f0, f1, buf, 3);
+    mfma(0, f1);
+    mfma(1, f1);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kNext) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): stage s + 1 landed for this wave
+      lds_barrier();
+    }
+    const int64_t k0 = (s + 2) * BK;
 #pragma unroll
-  for (int n = 0; n < 32; ++n) mfma(n, a1, q1);
+    for (int n = 2; n < 16; ++n) {
+      mfma(n, f1);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (kNext) {
+        if (n < 10) read(n - 2, f0, buf ^ 1, 0);
+      }
+      if constexpr (kIssue) {
+        issue_load(buf, k0, n - 2);
+        if (n == 15) issue_load(buf, k0, 14), issue_load(buf, k0, 15);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (kNext) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+
+#pragma unroll
+  for (int j = 0; j < 16; ++j) issue_load(0, 0, j);
+  if (KT > 1) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) issue_load(1, BK, j);
+    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): stage 0 landed for this wave
+  } else {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  }
+  lds_barrier();
+#pragma unroll
+  for (int n = 0; n < 8; ++n) read(n, f0, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+
+  int64_t s = 0;
+  for (; s + 2 < KT; ++s) step(s, T_{}, T_{});
+  if (s + 1 < KT) step(s++, T_{}, F_{});
+  step(s, F_{}, F_{});
   __syncthreads();  // all fragment reads and trailing loads done before the epilogue reuses the LDS
 
   // ---- epilogue ------------------------------------------------------------
