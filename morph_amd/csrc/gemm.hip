@@ -21,9 +21,10 @@
 // base + 16 l), so no registers are spent on staging.  A row of a stage is one
 // 128-byte line and its eight chunks are fetched by eight adjacent lanes, so
 // every L2 request is a full line (32-deep stages fetch half lines and double
-// the request count for the same bytes).  The DMA of stage s + 2 is issued in
-// the last sub-step of stage s, right after the one LDS-only barrier per
-// stage; each sub-step's 16 MFMAs run under the fragment reads of the next.
+// the request count for the same bytes).  The DMA of stage s + 2 is issued
+// over the last sub-step of stage s (right after the one LDS-only barrier per
+// stage) and the first of stage s + 1; each sub-step's 16 MFMAs run under the
+// fragment reads of the next.
 // Because the DMA writes LDS linearly, rows cannot be padded; instead the
 // eight 16-byte chunks of each 128-byte row are stored XOR-swizzled (slot =
 // chunk ^ ((row ^ (row >> 3)) & 7)), chosen on the load side by which global
@@ -67,12 +68,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = MORPH_GEMM_TILE_M;
 constexpr int BN = MORPH_GEMM_TILE_N;
 constexpr int BK = 64;               // K per pipeline stage: one 128-byte line per row
-constexpr int kStages = 2;
+constexpr int kSlots = 5;            // LDS ring of operand sub-tiles (P or Q of one stage)
 constexpr int LDE = BN + 8;          // padded LDS row of the output tile (bf16)
 constexpr int kThreads = 256;
-constexpr int kSubTile = BM * BK;                    // bf16 per operand sub-tile (256 x 64)
-constexpr int kStageElems = 2 * kSubTile;            // P and Q
-constexpr int kSmemElems = (kStages * kStageElems > BM * LDE) ? kStages * kStageElems : BM * LDE;
+constexpr int kSubTile = BM * BK;                    // bf16 per operand sub-tile (256 x 64, 32 KiB)
+constexpr int kSmemElems = (kSlots * kSubTile > BM * LDE) ? kSlots * kSubTile : BM * LDE;
+static_assert(kSmemElems * 2 <= 160 * 1024, "LDS of one workgroup");
 constexpr int kGroupM = 4;
 static_assert(BM == BN && BM == 256 && MORPH_GEMM_TILE_K % BK == 0, "256 x 256 tiles, K % 64");
 
@@ -260,18 +261,23 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
   const uint16_t* P = g.P + b * g.sp + row0 * g.ldp;
   const uint16_t* Q = g.Q + b * g.sq + col0 * g.ldq;
 
-  // DMA assignment: per stage a wave loads 64 rows of each operand, 8 rows per
-  // instruction; lane l -> row base + l / 8, LDS slot l % 8, which holds the
-  // global 16-byte chunk slot ^ swz(row).  The eight lanes of a row fetch the
-  // eight chunks of one 128-byte line (one full-line request).
+  // DMA assignment: a wave loads rows [64 w, 64 w + 64) of an operand
+  // sub-tile, 8 rows per instruction; lane l -> row base + l / 8, LDS slot
+  // l % 8, which holds the global 16-byte chunk slot ^ swz(row).  The eight
+  // lanes of a row fetch the eight chunks of one 128-byte line (one full-line
+  // request).
   const int lrow = lane >> 3, lslot = lane & 7;
   auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
-  // DMA load j (0..15) of a stage: operand j & 1 (P, Q), 8-row block j >> 1 of this wave.
-  auto issue_load = [&](int buf, int64_t k0, int j) {
-    const int r = wave * 64 + (j >> 1) * 8 + lrow;
+  const int64_t KT = g.K / BK;  // >= 1
+  // Load j (0..7) of operand Q (or P) of stage `stage` into ring slot `slot`;
+  // stages past the end load the last one again (never read; it keeps every
+  // step's load count, and so the vmcnt bookkeeping, the same).
+  auto issue_load = [&](bool q, int slot, int64_t stage, int j) {
+    const int64_t k0 = (stage < KT ? stage : KT - 1) * BK;
+    const int r = wave * 64 + j * 8 + lrow;
     const int c = lslot ^ swz(r);
-    uint16_t* dst = smem + buf * kStageElems + (j & 1) * kSubTile + (wave * 64 + (j >> 1) * 8) * BK;
-    const uint16_t* src = (j & 1) ? Q + r * g.ldq : P + r * g.ldp;
+    uint16_t* dst = smem + slot * kSubTile + (wave * 64 + j * 8) * BK;
+    const uint16_t* src = q ? Q + r * g.ldq : P + r * g.ldp;
     __builtin_amdgcn_global_load_lds(src + k0 + c * 8, (lds_void*)dst, 16, 0, 0);
   };
 
@@ -289,10 +295,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
   };
 
   // Workgroup barrier for LDS only: the memory clobber keeps the compiler from
-  // moving LDS accesses across it and no vmcnt wait is attached, so the DMA
-  // of the next stage stays in flight (__syncthreads would drain it).
+  // moving LDS accesses across it and no vmcnt wait is attached, so younger
+  // loads stay in flight (__syncthreads would drain them).
   auto lds_barrier = []() { asm volatile("s_barrier" ::: "memory"); };
-  // Fragments of one 16-deep sub-step: 4 P rows-blocks and 4 Q row-blocks.
+  // Fragments of one 16-deep sub-step: 4 P row-blocks and 4 Q row-blocks.
   struct Frags {
     bf16x8 a[4], q[4];
   };
@@ -300,89 +306,101 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     const int i = n >> 2, j = n & 3;
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.q[j], acc[i][j], 0, 0, 0);
   };
-  auto read = [&](int n, Frags& f, int buf, int kk) {
-    const uint16_t* sP = smem + buf * kStageElems;
+  auto read = [&](int n, Frags& f, int pslot, int qslot, int kk) {
     const int i = n >> 1;
     if (n & 1)
-      f.q[i] = frag(sP + kSubTile, wc + i * 32 + fr, kk * 2 + fh);
+      f.q[i] = frag(smem + qslot * kSubTile, wc + i * 32 + fr, kk * 2 + fh);
     else
-      f.a[i] = frag(sP, wr + i * 32 + fr, kk * 2 + fh);
+      f.a[i] = frag(smem + pslot * kSubTile, wr + i * 32 + fr, kk * 2 + fh);
   };
 
-  // Pipeline: two LDS stages of K = 64 and two register sets of fragments
-  // (F0, F1) of one 16-deep sub-step each.  Step s computes stage s from
-  // buffer s % 2 in four sub-steps; each sub-step's 16 MFMAs run while the
-  // next sub-step's 8 fragments are read.  Before the last sub-step one
-  // barrier (after this wave's vmcnt(0)) both frees buffer s % 2 -- every
-  // wave has its last fragments in registers -- and publishes stage s + 1 in
-  // the other buffer; the last sub-step then reads the first fragments of
-  // stage s + 1 and issues the DMA of stage s + 2 into buffer s % 2, which
-  // has about three sub-steps of MFMA time to land.  The scheduling barriers
-  // pin the interleave: without them the compiler is free to hoist the LDS
-  // waits above the MFMAs.
-  const int64_t KT = g.K / BK;  // >= 1
+  // Pipeline.  The LDS is a ring of five 32 KiB slots holding operand
+  // sub-tiles in the order P0 Q0 P1 Q1 P2 ... (item x = 2 stage + operand in
+  // slot x % 5), and two register sets of fragments (F0, F1) hold one 16-deep
+  // sub-step each.  Step t computes stage t in four sub-steps; each
+  // sub-step's 16 MFMAs run while the next sub-step's 8 fragments are read.
+  // Before the last sub-step one barrier (after this wave's vmcnt) frees the
+  // two slots of stage t -- every wave has its last fragments in registers --
+  // and publishes stage t + 1; the last sub-step then reads the first
+  // fragments of stage t + 1.  Loads: the load path accepts about 64 bytes per
+  // clock per CU, so a stage (64 KiB) issued in one sub-step stalls the
+  // issuing waves; here every sub-step issues 4 of a wave's loads (a quarter
+  // stage): Q of stage t + 2 into the freed P slot of stage t in the last
+  // sub-step of step t and the first of step t + 1 (due at the barrier of step
+  // t + 1), P of stage t + 3 into the freed Q slot in the second and third
+  // sub-steps of step t + 1 (due a step later).  The scheduling barriers pin
+  // the interleave: without them the compiler is free to hoist the LDS waits
+  // above the MFMAs.
   Frags f0, f1;
-  auto substep = [&](const Frags& cur, Frags& nxt, int buf, int kk) {
+  // One sub-step: 16 MFMAs on `cur`, the 8 fragments of `nxt` read from the
+  // slots (rp, rq) at depth kk, and loads j0 .. j0 + 3 of (lq ? Q : P) of
+  // stage lstage into slot ls_.
+  auto substep = [&](const Frags& cur, Frags& nxt, int rp, int rq, int kk, bool lq, int ls_,
+                     int64_t lstage, int j0) {
 #pragma unroll
     for (int n = 0; n < 16; ++n) {
       mfma(n, cur);
       __builtin_amdgcn_sched_barrier(0);
-      if (n < 8) read(n, nxt, buf, kk);
+      if (n < 8) read(n, nxt, rp, rq, kk);
+      if (n >= 2 && n < 10 && (n & 1) == 0) issue_load(lq, ls_, lstage, j0 + ((n - 2) >> 1));
       __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): next fragments in registers
   };
-  // kNext: a stage s + 1 exists; kIssue: a stage s + 2 exists.
-  auto step = [&](int64_t s, auto next_tag, auto issue_tag) {
-    constexpr bool kNext = decltype(next_tag)::value, kIssue = decltype(issue_tag)::value;
-    const int buf = (int)(s & 1);
-    substep(f0, f1, buf, 1);
-    substep(f1, f0, buf, 2);
-    substep(f0, f1, buf, 3);
+  // ps/qs: slots of stage t's P and Q; the slots of stage t + 1 and of P of
+  // stage t + 2 follow in ring order.
+  auto step = [&](int64_t t, int ps, auto next_tag) {
+    constexpr bool kNext = decltype(next_tag)::value;
+    const int qs = ps + 1 == kSlots ? 0 : ps + 1;
+    const int ps1 = qs + 1 == kSlots ? 0 : qs + 1;
+    const int qs1 = ps1 + 1 == kSlots ? 0 : ps1 + 1;
+    const int ps2 = qs1 + 1 == kSlots ? 0 : qs1 + 1;
+    substep(f0, f1, ps, qs, 1, true, qs1, t + 1, 4);   // Q of t + 1, loads 4..7
+    substep(f1, f0, ps, qs, 2, false, ps2, t + 2, 0);  // P of t + 2, loads 0..3
+    substep(f0, f1, ps, qs, 3, false, ps2, t + 2, 4);  // P of t + 2, loads 4..7
     mfma(0, f1);
     mfma(1, f1);
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kNext) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): stage s + 1 landed for this wave
+      __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8): all but P of t + 2 landed for this wave
       lds_barrier();
     }
-    const int64_t k0 = (s + 2) * BK;
 #pragma unroll
     for (int n = 2; n < 16; ++n) {
       mfma(n, f1);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (kNext) {
-        if (n < 10) read(n - 2, f0, buf ^ 1, 0);
-      }
-      if constexpr (kIssue) {
-        issue_load(buf, k0, n - 2);
-        if (n == 15) issue_load(buf, k0, 14), issue_load(buf, k0, 15);
+        if (n < 10) read(n - 2, f0, ps1, qs1, 0);
+        // Q of t + 2 into the freed P slot of t, loads 0..3
+        if (n >= 6 && n < 14 && (n & 1) == 0) issue_load(true, ps, t + 2, (n - 6) >> 1);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (kNext) __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   };
-  using T_ = std::true_type;
-  using F_ = std::false_type;
 
+  // Prologue: P0 Q0 P1 in full and the first half of Q1 (slots 0..3), then
+  // stage 0 is waited for and its first fragments read.
 #pragma unroll
-  for (int j = 0; j < 16; ++j) issue_load(0, 0, j);
-  if (KT > 1) {
+  for (int j = 0; j < 8; ++j) issue_load(false, 0, 0, j);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) issue_load(1, BK, j);
-    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): stage 0 landed for this wave
-  } else {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  }
+  for (int j = 0; j < 8; ++j) issue_load(true, 1, 0, j);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) issue_load(false, 2, 1, j);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) issue_load(true, 3, 1, j);
+  __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): P0 and Q0 landed for this wave
   lds_barrier();
 #pragma unroll
-  for (int n = 0; n < 8; ++n) read(n, f0, 0, 0);
+  for (int n = 0; n < 8; ++n) read(n, f0, 0, 1, 0);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 
-  int64_t s = 0;
-  for (; s + 2 < KT; ++s) step(s, T_{}, T_{});
-  if (s + 1 < KT) step(s++, T_{}, F_{});
-  step(s, F_{}, F_{});
+  int ps = 0;
+  for (int64_t t = 0; t + 1 < KT; ++t) {
+    step(t, ps, std::true_type{});
+    ps = ps + 2 >= kSlots ? ps + 2 - kSlots : ps + 2;
+  }
+  step(KT - 1, ps, std::false_type{});
   __syncthreads();  // all fragment reads and trailing loads done before the epilogue reuses the LDS
 
   // ---- epilogue ------------------------------------------------------------
