@@ -14,17 +14,18 @@
 // v_mfma_f32_32x32x16_bf16 (256 fp32 accumulators per lane).  Per 16-deep
 // sub-step a wave reads 8 fragments (8 KiB) from LDS for 16 MFMAs.
 //
-// Operand pipeline.  K advances 64 per stage through two LDS buffers (64 KiB
-// each: P and Q sub-tiles of 256 x 64 bf16) and two register sets of
-// fragments, one per 16-deep sub-step.  Operands go global -> LDS directly
-// (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS
-// base + 16 l), so no registers are spent on staging.  A row of a stage is one
-// 128-byte line and its eight chunks are fetched by eight adjacent lanes, so
-// every L2 request is a full line (32-deep stages fetch half lines and double
-// the request count for the same bytes).  The DMA of stage s + 2 is issued
-// over the last sub-step of stage s (right after the one LDS-only barrier per
-// stage) and the first of stage s + 1; each sub-step's 16 MFMAs run under the
-// fragment reads of the next.
+// Operand pipeline.  K advances 64 per stage.  The LDS holds a ring of five
+// 32 KiB slots, each the P or the Q sub-tile (256 x 64 bf16) of one stage, and
+// two register sets of fragments hold one 16-deep sub-step each.  Operands go
+// global -> LDS directly (buffer_load_dwordx4 ... lds: lane l's 16 bytes land
+// at the instruction's LDS base + 16 l), so no registers are spent on staging.
+// A row of a stage is one 128-byte line and its eight chunks are fetched by
+// eight adjacent lanes, so every L2 request is a full line (32-deep stages
+// fetch half lines and double the request count for the same bytes).  The
+// load path accepts about 64 bytes per clock per CU, so loads are spread a
+// quarter stage per sub-step under the MFMAs; five slots give the loads of a
+// stage two steps of cover.  Each sub-step's 16 MFMAs run under the fragment
+// reads of the next; one LDS-only barrier per stage.
 // Because the DMA writes LDS linearly, rows cannot be padded; instead the
 // eight 16-byte chunks of each 128-byte row are stored XOR-swizzled (slot =
 // chunk ^ ((row ^ (row >> 3)) & 7)), chosen on the load side by which global
@@ -257,28 +258,48 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const uint16_t* P = g.P + b * g.sp + row0 * g.ldp;
-  const uint16_t* Q = g.Q + b * g.sq + col0 * g.ldq;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
+  // The tile's operand bases are wave-uniform; readfirstlane states it, so the
+  // buffer descriptors built from them live in scalar registers.
+  auto uniform = [](const uint16_t* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint16_t*>(lo | (hi << 32));
+  };
+  const uint16_t* P = uniform(g.P + b * g.sp + row0 * g.ldp);
+  const uint16_t* Q = uniform(g.Q + b * g.sq + col0 * g.ldq);
 
   // DMA assignment: a wave loads rows [64 w, 64 w + 64) of an operand
   // sub-tile, 8 rows per instruction; lane l -> row base + l / 8, LDS slot
   // l % 8, which holds the global 16-byte chunk slot ^ swz(row).  The eight
   // lanes of a row fetch the eight chunks of one 128-byte line (one full-line
-  // request).
+  // request).  A lane's byte offset from the operand's stage base is the same
+  // for every stage, so it is computed once; each load is then a uniform base
+  // (scalar registers) plus a 32-bit per-lane offset, the cheapest form to
+  // issue (the host keeps 256 rows of a leading dimension under 4 GiB).
   const int lrow = lane >> 3, lslot = lane & 7;
   auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
   const int64_t KT = g.K / BK;  // >= 1
+  uint32_t offp[8], offq[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = wave * 64 + j * 8 + lrow;
+    const uint32_t c = (uint32_t)(lslot ^ swz(r));
+    offp[j] = (uint32_t)r * (uint32_t)g.ldp * 2u + c * 16u;
+    offq[j] = (uint32_t)r * (uint32_t)g.ldq * 2u + c * 16u;
+  }
   // Load j (0..7) of operand Q (or P) of stage `stage` into ring slot `slot`;
   // stages past the end load the last one again (never read; it keeps every
   // step's load count, and so the vmcnt bookkeeping, the same).
   auto issue_load = [&](bool q, int slot, int64_t stage, int j) {
     const int64_t k0 = (stage < KT ? stage : KT - 1) * BK;
-    const int r = wave * 64 + j * 8 + lrow;
-    const int c = lslot ^ swz(r);
+    // raw buffer over the stage's columns: base in scalar registers, no range limit
+    // beyond the 32-bit offsets
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>((q ? Q : P) + k0), (short)0, (int)0xFFFFFFFF, 0x00020000);
     uint16_t* dst = smem + slot * kSubTile + (wave * 64 + j * 8) * BK;
-    const uint16_t* src = q ? Q + r * g.ldq : P + r * g.ldp;
-    __builtin_amdgcn_global_load_lds(src + k0 + c * 8, (lds_void*)dst, 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)dst, 16, q ? offq[j] : offp[j], 0, 0, 0);
   };
 
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
@@ -460,9 +481,12 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
       (D && (ldd | stride_d) % 8) || (Ct && (ldct | stride_ct) % 8))
     return MORPH_EINVAL;
   if (symmetric && (M != N || Ct != nullptr)) return MORPH_EINVAL;
-  // epilogue offsets inside a tile are 32-bit: 255 rows of the widest leading dimension
+  // operand-load and epilogue offsets inside a tile are 32-bit: 255 rows of
+  // the widest leading dimension
   constexpr int64_t kMaxLd = int64_t(1) << 23;
-  if (ldc > kMaxLd || (D && ldd > kMaxLd) || (Ct && ldct > kMaxLd)) return MORPH_ERANGE;
+  if (ldp > kMaxLd || ldq > kMaxLd || ldc > kMaxLd || (D && ldd > kMaxLd) ||
+      (Ct && ldct > kMaxLd))
+    return MORPH_ERANGE;
   if (M == 0 || N == 0 || batch == 0) return MORPH_OK;
   const int64_t tm = M / BM, tn = N / BN;
   const int64_t per = symmetric ? tm * (tm + 1) / 2 : tm * tn;
