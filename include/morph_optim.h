@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 1
+#define MORPH_ABI_VERSION 2
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -315,19 +315,28 @@ int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D, 
                        int64_t stride_p, int64_t stride_q, int64_t stride_d, int64_t stride_c,
                        int64_t stride_ct, float alpha, float beta, int flags, void* stream);
 
-/* One Muon matrix: FP32 [rows, cols] row-major device buffers. */
+/*
+ * One Muon matrix: FP32 row-major device buffers of shape [rows, cols], or
+ * [cols, rows] when `transposed` is 1.  Both orientations have the same
+ * Newton-Schulz operand (optimizer.py:15-17 transposes the taller one), so one
+ * batch can hold both, e.g. a SwiGLU block's [6144, 3072] and [3072, 6144]
+ * weights.
+ */
 typedef struct morph_muon_matrix {
   const float* grad;
   float* momentum; /* updated in place (unused by morph_muon_orthogonalize) */
   float* param;    /* FP32 master, updated in place (the output of morph_muon_orthogonalize) */
+  int32_t transposed; /* 0 or 1 */
+  int32_t reserved;   /* 0 */
 } morph_muon_matrix;
 
 /*
  * Constants of one Muon step (streamtrain/optimizer.py:52-61), fp32 values of
  * the reference's Python scalars: momentum_weight = .05 (lerp_(g, .05)),
  * nesterov_weight = .95 (g.lerp(m, .95)), a/b/c = 3.4445, -4.775, 2.0315,
- * update_scale = sqrt(max(1, rows/cols)), decay = 1 - lr * weight_decay,
- * neg_lr = -lr; ns_steps = 5.
+ * update_scale = sqrt(max(1, rows/cols)) for matrices stored [rows, cols] and
+ * update_scale_transposed = sqrt(max(1, cols/rows)) for those stored
+ * [cols, rows], decay = 1 - lr * weight_decay, neg_lr = -lr; ns_steps = 5.
  */
 typedef struct morph_muon_hp {
   float momentum_weight;
@@ -337,19 +346,21 @@ typedef struct morph_muon_hp {
   float decay;
   float neg_lr;
   int32_t ns_steps;
-  int32_t reserved;
+  float update_scale_transposed;
 } morph_muon_hp;
 
-/* Workspace bytes morph_muon_step needs for `count` matrices of [rows, cols]. */
+/* Workspace bytes morph_muon_step needs for `count` matrices of [rows, cols] (either orientation). */
 size_t morph_muon_workspace_bytes(int64_t rows, int64_t cols, int count);
 
 /*
- * One Muon step for `count` (<= 64) matrices of the same shape, batched:
- * momentum and Nesterov blend (fp32, torch's rounding), Frobenius
- * normalisation, ns_steps Newton-Schulz iterations in bf16 on MFMA (A = X X^T,
- * B = b A + c A A, X = a X + B X, fp32 accumulation), and the fp32 master update
- * p = p * decay + (U * update_scale) * neg_lr with U in p's layout (transposed
- * back when rows > cols, optimizer.py:15-17, 22).  The workspace must be
+ * One Muon step for `count` (<= 64) matrices of one shape (in either
+ * orientation), batched: momentum and Nesterov blend (fp32, torch's rounding),
+ * Frobenius normalisation, ns_steps Newton-Schulz iterations in bf16 on MFMA
+ * (A = X X^T, B = b A + c A A, X = a X + B X, fp32 accumulation), and the fp32
+ * master update p = p * decay + (U * scale) * neg_lr with U in p's layout
+ * (transposed back when p has more rows than columns, optimizer.py:15-17, 22)
+ * and scale = update_scale or update_scale_transposed by the matrix's
+ * orientation.  The workspace must be
  * 256-byte aligned and zero-filled once before first use (its zero padding is
  * kept by every call).  Replaces optimizer.py:13-22 and 52-61.
  */

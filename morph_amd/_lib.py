@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmorph_optim.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_NONE, DTYPE_F32, DTYPE_F16, DTYPE_BF16 = -1, 0, 1, 2
 HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
@@ -78,14 +78,15 @@ class AccumTensor(ctypes.Structure):
 class MuonMatrix(ctypes.Structure):
     """morph_muon_matrix."""
     _fields_ = [("grad", ctypes.c_void_p), ("momentum", ctypes.c_void_p),
-                ("param", ctypes.c_void_p)]
+                ("param", ctypes.c_void_p), ("transposed", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
 
 
 class MuonHP(ctypes.Structure):
     """morph_muon_hp."""
     _fields_ = [(name, ctypes.c_float) for name in (
         "momentum_weight", "nesterov_weight", "a", "b", "c", "update_scale", "decay",
-        "neg_lr")] + [("ns_steps", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+        "neg_lr")] + [("ns_steps", ctypes.c_int32), ("update_scale_transposed", ctypes.c_float)]
 
 
 _lib = None

@@ -1,7 +1,8 @@
 // Hybrid Muon step for gfx950: momentum, Nesterov blend, Frobenius
 // normalisation, Newton-Schulz quintic on bf16 MFMA, FP32 master update.
 // Follows streamtrain/optimizer.py:13-22 (orthogonalize) and 52-61 (the Muon
-// loop) for a batch of matrices that share one shape:
+// loop) for a batch of matrices that share one Newton-Schulz operand shape
+// (each stored [rows, cols] or, with its transposed flag, [cols, rows]):
 //
 //   momentum.lerp_(g, mom_w)                    fma(mom_w, g - m, m)           (58)
 //   u = g.lerp(momentum, nesterov_w)            fma(nesterov_w - 1, m - g, m)  (59)
@@ -39,6 +40,7 @@ struct MatPtrs {
   const float* grad[kMaxMats];
   float* mom[kMaxMats];
   float* param[kMaxMats];
+  int32_t transposed[kMaxMats];  // stored [cols, rows] instead of [rows, cols]
 };
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -134,33 +136,38 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const double* part_all, fl
   if (threadIdx.x == 0) den[mat] = (float)sqrt(t) + 1e-7f;
 }
 
-// X / Xt (bf16, padded) from u / den.  The param layout is [rows, cols]; X is
-// [m, n] with m = min: when rows <= cols X has the param layout and Xt is the
-// transpose, otherwise the other way round.  One 64 x 64 tile of u per block,
-// transposed through LDS so both writes are coalesced.
-__global__ __launch_bounds__(kBlock) void scale_kernel(const float* u_all, const float* den,
-                                                       uint16_t* x_all, uint16_t* xt_all,
-                                                       int64_t rows, int64_t cols, int64_t mp,
-                                                       int64_t np, int64_t ldm, int64_t ldn,
-                                                       int64_t numel) {
+// X / Xt (bf16, padded) from u / den.  A matrix's stored layout is
+// [pr, pc] = [rows, cols], or [cols, rows] when transposed; X is [m, n] with
+// m = min: when pr <= pc X has the stored layout and Xt is the transpose,
+// otherwise the other way round.  One 64 x 64 tile of u per block, transposed
+// through LDS so both writes are coalesced.  The grid covers [rows, cols] in
+// 64-tiles; a transposed matrix reads block (x, y) as its tile (y, x).
+__global__ __launch_bounds__(kBlock) void scale_kernel(MatPtrs mats, const float* u_all,
+                                                       const float* den, uint16_t* x_all,
+                                                       uint16_t* xt_all, int64_t rows,
+                                                       int64_t cols, int64_t mp, int64_t np,
+                                                       int64_t ldm, int64_t ldn, int64_t numel) {
   __shared__ uint16_t tile[kTile][kTile + 2];
   const int mat = blockIdx.z;
+  const bool tr = mats.transposed[mat] != 0;
+  const int64_t pr = tr ? cols : rows, pc = tr ? rows : cols;  // stored shape
   const float d = den[mat];
   const float* u = u_all + (int64_t)mat * numel;
-  const bool same_is_x = rows <= cols;  // X has the param layout
+  const bool same_is_x = pr <= pc;  // X has the stored layout
   uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
   uint16_t* xtm = xt_all + (int64_t)mat * np * ldm;
   uint16_t* same = same_is_x ? xm : xtm;
   uint16_t* trans = same_is_x ? xtm : xm;
-  const int64_t ld_same = same_is_x ? ldn : ldm;   // row length of the param-layout copy
+  const int64_t ld_same = same_is_x ? ldn : ldm;   // row length of the stored-layout copy
   const int64_t ld_trans = same_is_x ? ldm : ldn;  // row length of the transposed copy
-  const int64_t r0 = (int64_t)blockIdx.y * kTile, c0 = (int64_t)blockIdx.x * kTile;
+  const int64_t r0 = (int64_t)(tr ? blockIdx.x : blockIdx.y) * kTile;
+  const int64_t c0 = (int64_t)(tr ? blockIdx.y : blockIdx.x) * kTile;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int rr = ty; rr < kTile; rr += kBlock / 64) {
     const int64_t r = r0 + rr, c = c0 + tx;
     uint16_t h = 0;
-    if (r < rows && c < cols) {
-      h = (uint16_t)float_to_bf16_bits(u[r * cols + c] / d);
+    if (r < pr && c < pc) {
+      h = (uint16_t)float_to_bf16_bits(u[r * pc + c] / d);
       same[r * ld_same + c] = h;
     }
     tile[rr][tx] = h;
@@ -168,27 +175,32 @@ __global__ __launch_bounds__(kBlock) void scale_kernel(const float* u_all, const
   __syncthreads();
   for (int cc = ty; cc < kTile; cc += kBlock / 64) {
     const int64_t c = c0 + cc, r = r0 + tx;
-    if (r < rows && c < cols) trans[c * ld_trans + r] = tile[tx][cc];
+    if (r < pr && c < pc) trans[c * ld_trans + r] = tile[tx][cc];
   }
 }
 
-// p = p * decay + (U * scale) * neg_lr, U read from the bf16 copy in p's layout.
+// p = p * decay + (U * scale) * neg_lr, U read from the bf16 copy in p's
+// layout; scale is scale_t for a transposed matrix.
 // kExtract: p = U instead (orthogonalize alone returns the fp32 value of U).
 template <bool kExtract>
 __global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint16_t* x_all,
                                                        const uint16_t* xt_all, int64_t rows,
                                                        int64_t cols, int64_t mp, int64_t np,
-                                                       int64_t ldm, int64_t ldn, float scale,
-                                                       float decay, float neg_lr) {
+                                                       int64_t ldm, int64_t ldn, float scale_n,
+                                                       float scale_t, float decay,
+                                                       float neg_lr) {
   const int mat = blockIdx.y;
   float* p = mats.param[mat];
-  const bool same_is_x = rows <= cols;
+  const bool tr = mats.transposed[mat] != 0;
+  const int64_t pc = tr ? rows : cols;  // stored row length
+  const bool same_is_x = (tr ? cols : rows) <= pc;
+  const float scale = tr ? scale_t : scale_n;
   const uint16_t* U = same_is_x ? x_all + (int64_t)mat * mp * ldn : xt_all + (int64_t)mat * np * ldm;
   const int64_t ld = same_is_x ? ldn : ldm;
   const int64_t numel = rows * cols;
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
   for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
-    const int64_t r = i / cols, c = i - r * cols;
+    const int64_t r = i / pc, c = i - r * pc;
     if constexpr (kExtract) {
       p[i] = bf16_bits_to_float(U[r * ld + c]);
     } else {
@@ -233,7 +245,8 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
     if (count > 0 && mats == nullptr) return MORPH_EINVAL;
     for (int i = 0; i < count; ++i)
       if (mats[i].grad == nullptr || mats[i].param == nullptr ||
-          (need_momentum && mats[i].momentum == nullptr))
+          (need_momentum && mats[i].momentum == nullptr) ||
+          (mats[i].transposed != 0 && mats[i].transposed != 1) || mats[i].reserved != 0)
         return MORPH_EINVAL;
   }
   const Layout L = make_layout(rows, cols, count > 0 ? count : 1);
@@ -259,6 +272,7 @@ MatPtrs pointers(const morph_muon_matrix* mats, int count) {
     m.grad[i] = mats[i].grad;
     m.mom[i] = mats[i].momentum;
     m.param[i] = mats[i].param;
+    m.transposed[i] = mats[i].transposed;
   }
   return m;
 }
@@ -285,7 +299,7 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
   hipLaunchKernelGGL(scale_kernel,
                      dim3((unsigned)((cols + kTile - 1) / kTile),
                           (unsigned)((rows + kTile - 1) / kTile), count),
-                     dim3(kBlock), 0, s, W.u, W.den, W.X, W.Xt[0], rows, cols, L.mp, L.np,
+                     dim3(kBlock), 0, s, mp_, W.u, W.den, W.X, W.Xt[0], rows, cols, L.mp, L.np,
                      L.ldm, L.ldn, L.numel);
   return launch_status();
 }
@@ -330,10 +344,12 @@ int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   hipStream_t s = as_stream(stream);
   if (orth_only)
     hipLaunchKernelGGL(apply_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
-                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->decay, hp->neg_lr);
+                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->update_scale_transposed,
+                       hp->decay, hp->neg_lr);
   else
     hipLaunchKernelGGL(apply_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
-                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->decay, hp->neg_lr);
+                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->update_scale_transposed,
+                       hp->decay, hp->neg_lr);
   return launch_status();
 }
 

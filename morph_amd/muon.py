@@ -82,16 +82,25 @@ _WORKSPACES = _Workspaces()
 
 
 def _hp(momentum_weight=.05, nesterov_weight=.95, update_scale=1.0, decay=1.0, neg_lr=0.0,
-        steps=NS_STEPS, coeffs=NS_COEFFS):
+        steps=NS_STEPS, coeffs=NS_COEFFS, update_scale_transposed=1.0):
     a, b, c = coeffs
     return MuonHP(to_f32(momentum_weight), to_f32(nesterov_weight), to_f32(a), to_f32(b),
-                  to_f32(c), to_f32(update_scale), to_f32(decay), to_f32(neg_lr), steps, 0)
+                  to_f32(c), to_f32(update_scale), to_f32(decay), to_f32(neg_lr), steps,
+                  to_f32(update_scale_transposed))
 
 
 def _by_shape(items):
+    """Batches by Newton-Schulz operand: {(m, n): [(item, transposed)]} with m <= n.
+
+    A [rows, cols] and a [cols, rows] matrix share the operand (optimizer.py:15-17
+    transposes the taller one), so a SwiGLU block's up/gate and down weights run
+    as one batch; `transposed` marks the ones stored [n, m].
+    """
     groups = {}
     for item in items:
-        groups.setdefault(tuple(item[0].shape), []).append(item)
+        rows, cols = item[0].shape
+        key = (min(rows, cols), max(rows, cols))
+        groups.setdefault(key, []).append((item, int(rows != key[0])))
     return groups
 
 
@@ -102,18 +111,21 @@ def ns_flops(rows, cols, count, steps=NS_STEPS):
 
 
 def _run(mats, rows, cols, hp, orth_only, stream, workspaces, timer=None):
-    """prepare -> Newton-Schulz -> finish for up to 64 same-shape matrices per batch.
+    """prepare -> Newton-Schulz -> finish for up to 64 matrices per batch.
 
-    timer: optional list; (start_event, end_event, flops) around each NS chain.
+    mats: [((param, grad, momentum), transposed)], each stored [rows, cols], or
+    [cols, rows] when transposed.  timer: optional list; (start_event,
+    end_event, flops) around each NS chain.
     """
     L = lib()
     for start in range(0, len(mats), 64):
         chunk = mats[start:start + 64]
-        ws = workspaces.get(rows, cols, len(chunk), chunk[0][0].device)
+        ws = workspaces.get(rows, cols, len(chunk), chunk[0][0][0].device)
         arr = (MuonMatrix * len(chunk))()
-        for i, (p, g, m) in enumerate(chunk):
+        for i, ((p, g, m), transposed) in enumerate(chunk):
             arr[i].grad, arr[i].param = g.data_ptr(), p.data_ptr()
             arr[i].momentum = m.data_ptr() if m is not None else None
+            arr[i].transposed = transposed
         args = (ctypes.byref(hp),)
         wsp, wsn, sh = ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream_handle(stream)
         check(L.morph_muon_prepare(arr, len(chunk), rows, cols, *args, int(orth_only), wsp, wsn, sh))
@@ -137,7 +149,8 @@ def _check_matrix(t, name):
 def orthogonalize(gradients, steps=NS_STEPS, stream=None, workspaces=_WORKSPACES):
     """optimizer.py:13-22 on the GPU: NS(g / (|g|_F + 1e-7)), bf16 MFMA, returned as fp32.
 
-    gradients: one 2-D tensor or a list; same-shape matrices run as one batch.
+    gradients: one 2-D tensor or a list; matrices with the same Newton-Schulz
+    operand ([r, c] and [c, r] alike) run as one batch.
     """
     single = torch.is_tensor(gradients)
     gs = [gradients] if single else list(gradients)
@@ -167,7 +180,7 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
         items.append((p, g, m))
     for (rows, cols), group in _by_shape(items).items():
         hp = _hp(update_scale=max(1, rows / cols) ** .5, decay=1 - lr * weight_decay,
-                 neg_lr=-lr, steps=steps)
+                 neg_lr=-lr, steps=steps, update_scale_transposed=max(1, cols / rows) ** .5)
         _run(group, rows, cols, hp, False, stream, workspaces, timer)
 
 

@@ -1,6 +1,8 @@
 """The C-ABI library loads and exports every symbol include/*.h declares (no GPU calls)."""
 import ctypes
 import re
+import shutil
+import subprocess
 from pathlib import Path
 
 import pytest
@@ -31,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_status_strings():
     from morph_amd import _lib
     lib = _lib.lib()
-    assert lib.morph_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.morph_abi_version() == _lib.ABI_VERSION == 2
     assert lib.morph_strerror(0) == b"ok"
     for code in (-1, -2, -3, -4, -5):
         assert lib.morph_strerror(code) not in (b"ok", b"unknown morph status")
@@ -61,6 +63,50 @@ def test_argument_validation_happens_before_any_launch():
     assert gemm(256, 256, 64, _lib.GEMM_SYMMETRIC, Ct=p) == -1
     assert gemm(100, 256, 64, 0) == -4                    # not a tile multiple
     assert gemm(256, 256, 0, 0) == -1
+
+
+def test_muon_matrix_flags_are_validated():
+    """transposed must be 0 or 1 and reserved 0, checked before any launch."""
+    from morph_amd import _lib
+    lib = _lib.lib()
+    p = 0x10000
+    hp = _lib.MuonHP()
+    hp.ns_steps = 5
+    for transposed, reserved in ((2, 0), (-1, 0), (0, 1)):
+        arr = (_lib.MuonMatrix * 1)()
+        arr[0].grad, arr[0].momentum, arr[0].param = p, p, p
+        arr[0].transposed, arr[0].reserved = transposed, reserved
+        assert lib.morph_muon_step(arr, 1, 256, 512, ctypes.byref(hp), ctypes.c_void_p(p),
+                                   1 << 40, None) == -1
+
+
+# (ctypes class, C type) pairs whose layouts must agree field by field
+STRUCTS = [("AdamwHP", "morph_adamw_hp"), ("AdamwTensor", "morph_adamw_tensor"),
+           ("StepState", "morph_step_state"), ("AdamwSched", "morph_adamw_sched"),
+           ("AccumTensor", "morph_accum_tensor"), ("MuonMatrix", "morph_muon_matrix"),
+           ("MuonHP", "morph_muon_hp")]
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="needs a host C compiler")
+def test_ctypes_struct_layouts_match_the_header(tmp_path):
+    """sizeof and every field offset of the ctypes mirrors equal the C compiler's."""
+    from morph_amd import _lib
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "morph_optim.h"',
+             'int main(void) {']
+    for cls, ctype in STRUCTS:
+        lines.append(f'  printf("{cls} size %zu\\n", sizeof({ctype}));')
+        for field, *_ in getattr(_lib, cls)._fields_:
+            lines.append(f'  printf("{cls} {field} %zu\\n", offsetof({ctype}, {field}));')
+    lines += ['  return 0;', '}']
+    (tmp_path / "layout.c").write_text("\n".join(lines))
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), "-o", str(tmp_path / "layout"),
+                    str(tmp_path / "layout.c")], check=True)
+    out = subprocess.run([str(tmp_path / "layout")], check=True, capture_output=True, text=True)
+    for line in out.stdout.splitlines():
+        cls, field, value = line.split()
+        struct = getattr(_lib, cls)
+        got = ctypes.sizeof(struct) if field == "size" else getattr(struct, field).offset
+        assert got == int(value), (cls, field, got, value)
 
 
 def test_gemm_flag_values_match_header():

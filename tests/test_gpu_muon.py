@@ -272,3 +272,51 @@ def test_one_call_c_entry_equals_phased_path():
                                           ctypes.c_void_p(ws.data_ptr()), ws.numel(),
                                           _lib.stream_handle()))
     assert torch.equal(pa, pb) and torch.equal(ma, mb)
+
+
+def test_mixed_orientation_batch_equals_separate_batches():
+    """[r, c] and [c, r] matrices share one batch (one Newton-Schulz operand shape);
+    every matrix comes out bit-identical to running it alone, scale sqrt(max(1, r/c))
+    per matrix as optimizer.py:60 computes it."""
+    gen = torch.Generator().manual_seed(11)
+    shapes = [(192, 448), (448, 192), (192, 448), (448, 192)]
+    p0 = [torch.randn(s, generator=gen) * .02 for s in shapes]
+    m0 = [torch.randn(s, generator=gen) * 1e-3 for s in shapes]
+    g = [(torch.randn(s, generator=gen) * 1e-3).to(DEV) for s in shapes]
+    pa, ma = [t.to(DEV) for t in p0], [t.to(DEV) for t in m0]
+    muon.muon_step(pa, g, ma, .02, .01)  # one batch of four
+    for i in range(len(shapes)):
+        pb, mb = p0[i].to(DEV), m0[i].to(DEV)
+        muon.muon_step([pb], [g[i]], [mb], .02, .01)
+        assert torch.equal(pa[i], pb) and torch.equal(ma[i], mb), i
+    outs = muon.orthogonalize(g)
+    for i in range(len(shapes)):
+        assert torch.equal(outs[i], muon.orthogonalize(g[i])), i
+
+
+def test_transposed_flag_equals_passing_the_transposed_shape():
+    """C ABI: a [c, r] matrix flagged transposed under (rows, cols) = (r, c) equals the
+    same matrix passed unflagged as (c, r)."""
+    import ctypes
+    from morph_amd import _lib
+    gen = torch.Generator().manual_seed(12)
+    r, c = 256, 576
+    p0, m0, g = (torch.randn(c, r, generator=gen) * s for s in (.02, 1e-3, 1e-3))
+    g = g.to(DEV)
+    results = []
+    for rows, cols, transposed in ((r, c, 1), (c, r, 0)):
+        p, m = p0.to(DEV), m0.to(DEV)
+        ws = torch.zeros(_lib.lib().morph_muon_workspace_bytes(rows, cols, 1), dtype=torch.uint8,
+                         device=DEV)
+        arr = (_lib.MuonMatrix * 1)()
+        arr[0].grad, arr[0].momentum, arr[0].param = g.data_ptr(), m.data_ptr(), p.data_ptr()
+        arr[0].transposed = transposed
+        scale = (c / r) ** .5
+        hp = muon._hp(update_scale=scale if not transposed else 1.0,
+                      update_scale_transposed=scale if transposed else 1.0,
+                      decay=1 - .02 * .01, neg_lr=-.02)
+        _lib.check(_lib.lib().morph_muon_step(arr, 1, rows, cols, ctypes.byref(hp),
+                                              ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                              _lib.stream_handle()))
+        results.append((p, m))
+    assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])
