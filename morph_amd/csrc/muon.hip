@@ -95,7 +95,20 @@ __device__ __forceinline__ double block_sum(double x, double* lds) {
 }
 
 // momentum + Nesterov blend + partial sums of u^2 (one partial per block).
-// kMomentum = false: u = grad (orthogonalize alone).
+// kMomentum = false: u = grad (orthogonalize alone).  A block covers
+// kElemsPerBlock consecutive elements; a lane moves 4 consecutive elements per
+// 128-bit access when the matrix's buffers are 16-byte aligned (one
+// contiguous 4 KiB segment per wave access), else one element per access.
+template <bool kMomentum>
+__device__ __forceinline__ void momentum_one(float gi, float& m, float& ui, float mom_w,
+                                             float nest_w, bool large_m, bool large_n) {
+  ui = gi;
+  if constexpr (kMomentum) {
+    m = large_m ? __fmaf_rn(mom_w - 1.0f, gi - m, gi) : __fmaf_rn(mom_w, gi - m, m);
+    ui = large_n ? __fmaf_rn(nest_w - 1.0f, m - gi, m) : __fmaf_rn(nest_w, m - gi, gi);
+  }
+}
+
 template <bool kMomentum>
 __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u_all,
                                                           double* part_all, int64_t numel,
@@ -108,18 +121,35 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u
   float* u = u_all + (int64_t)mat * numel;
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
   const bool large_m = mom_w >= 0.5f, large_n = nest_w >= 0.5f;
+  const bool vec = ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(mom)) & 15) == 0 &&
+                   base + kElemsPerBlock <= numel;  // u is 256-byte aligned, numel * 4 per matrix
   double ss = 0.0;
-  for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
-    const float gi = g[i];
-    float ui = gi;
-    if constexpr (kMomentum) {
-      float m = mom[i];
-      m = large_m ? __fmaf_rn(mom_w - 1.0f, gi - m, gi) : __fmaf_rn(mom_w, gi - m, m);
-      ui = large_n ? __fmaf_rn(nest_w - 1.0f, m - gi, m) : __fmaf_rn(nest_w, m - gi, gi);
-      mom[i] = m;
+  if (vec && (numel & 3) == 0) {
+#pragma unroll
+    for (int k = 0; k < kElemsPerBlock / (4 * kBlock); ++k) {
+      const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
+      const f32x4 gv = *reinterpret_cast<const f32x4*>(g + i);
+      f32x4 mv = f32x4{0.f, 0.f, 0.f, 0.f}, uv;
+      if constexpr (kMomentum) mv = *reinterpret_cast<const f32x4*>(mom + i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float m = mv[e], ui;
+        momentum_one<kMomentum>(gv[e], m, ui, mom_w, nest_w, large_m, large_n);
+        mv[e] = m;
+        uv[e] = ui;
+        ss += (double)ui * (double)ui;
+      }
+      if constexpr (kMomentum) *reinterpret_cast<f32x4*>(mom + i) = mv;
+      *reinterpret_cast<f32x4*>(u + i) = uv;
     }
-    u[i] = ui;
-    ss += (double)ui * (double)ui;
+  } else {
+    for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
+      float m = kMomentum ? mom[i] : 0.f, ui;
+      momentum_one<kMomentum>(g[i], m, ui, mom_w, nest_w, large_m, large_n);
+      if constexpr (kMomentum) mom[i] = m;
+      u[i] = ui;
+      ss += (double)ui * (double)ui;
+    }
   }
   const double s = block_sum(ss, lds);
   if (threadIdx.x == 0) part_all[(int64_t)mat * blocks + blockIdx.x] = s;
@@ -140,14 +170,16 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const double* part_all, fl
 // [pr, pc] = [rows, cols], or [cols, rows] when transposed; X is [m, n] with
 // m = min: when pr <= pc X has the stored layout and Xt is the transpose,
 // otherwise the other way round.  One 64 x 64 tile of u per block, transposed
-// through LDS so both writes are coalesced.  The grid covers [rows, cols] in
+// through LDS so both writes are coalesced; a lane moves 4 consecutive
+// elements per access (128-bit u reads, 64-bit bf16 writes) where the tile is
+// whole and the rows are a multiple of 4 long.  The grid covers [rows, cols] in
 // 64-tiles; a transposed matrix reads block (x, y) as its tile (y, x).
 __global__ __launch_bounds__(kBlock) void scale_kernel(MatPtrs mats, const float* u_all,
                                                        const float* den, uint16_t* x_all,
                                                        uint16_t* xt_all, int64_t rows,
                                                        int64_t cols, int64_t mp, int64_t np,
                                                        int64_t ldm, int64_t ldn, int64_t numel) {
-  __shared__ uint16_t tile[kTile][kTile + 2];
+  __shared__ __attribute__((aligned(8))) uint16_t tile[kTile][kTile + 4];
   const int mat = blockIdx.z;
   const bool tr = mats.transposed[mat] != 0;
   const int64_t pr = tr ? cols : rows, pc = tr ? rows : cols;  // stored shape
@@ -158,30 +190,64 @@ __global__ __launch_bounds__(kBlock) void scale_kernel(MatPtrs mats, const float
   uint16_t* xtm = xt_all + (int64_t)mat * np * ldm;
   uint16_t* same = same_is_x ? xm : xtm;
   uint16_t* trans = same_is_x ? xtm : xm;
-  const int64_t ld_same = same_is_x ? ldn : ldm;   // row length of the stored-layout copy
-  const int64_t ld_trans = same_is_x ? ldm : ldn;  // row length of the transposed copy
+  // row lengths of the stored-layout and transposed copies (multiples of 64)
+  const int64_t ld_same = same_is_x ? ldn : ldm;
+  const int64_t ld_trans = same_is_x ? ldm : ldn;
   const int64_t r0 = (int64_t)(tr ? blockIdx.x : blockIdx.y) * kTile;
   const int64_t c0 = (int64_t)(tr ? blockIdx.y : blockIdx.x) * kTile;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int rr = ty; rr < kTile; rr += kBlock / 64) {
-    const int64_t r = r0 + rr, c = c0 + tx;
-    uint16_t h = 0;
-    if (r < pr && c < pc) {
-      h = (uint16_t)float_to_bf16_bits(u[r * pc + c] / d);
-      same[r * ld_same + c] = h;
+  const int q = threadIdx.x & 15, w = threadIdx.x >> 4;  // 4-element group, row of a pass
+  // u is 256-byte aligned per matrix when numel % 4 == 0 (then pc % 4 == 0 or pr % 4 == 0)
+  const bool vec = (pc & 3) == 0 && (pr & 3) == 0 && r0 + kTile <= pr && c0 + kTile <= pc;
+  for (int rr = w; rr < kTile; rr += kBlock / 16) {
+    const int64_t r = r0 + rr, c = c0 + 4 * q;
+    uint32_t h[4] = {0, 0, 0, 0};
+    if (vec) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(u + r * pc + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = float_to_bf16_bits(v[e] / d);
+      *reinterpret_cast<u32x2*>(same + r * ld_same + c) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r < pr && c + e < pc) {
+          h[e] = float_to_bf16_bits(u[r * pc + c + e] / d);
+          same[r * ld_same + c + e] = (uint16_t)h[e];
+        }
     }
-    tile[rr][tx] = h;
+    *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
   }
   __syncthreads();
-  for (int cc = ty; cc < kTile; cc += kBlock / 64) {
-    const int64_t c = c0 + cc, r = r0 + tx;
-    if (r < pr && c < pc) trans[c * ld_trans + r] = tile[tx][cc];
+  for (int cc = w; cc < kTile; cc += kBlock / 16) {
+    const int64_t c = c0 + cc, r = r0 + 4 * q;
+    uint32_t h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = tile[4 * q + e][cc];
+    if (vec) {
+      *reinterpret_cast<u32x2*>(trans + c * ld_trans + r) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c < pc && r + e < pr) trans[c * ld_trans + r + e] = (uint16_t)h[e];
+    }
   }
 }
 
 // p = p * decay + (U * scale) * neg_lr, U read from the bf16 copy in p's
 // layout; scale is scale_t for a transposed matrix.
 // kExtract: p = U instead (orthogonalize alone returns the fp32 value of U).
+// When p is 16-byte aligned and its rows a multiple of 4 long, a lane moves 4
+// consecutive elements of one row per access (128-bit p, 64-bit U).
+template <bool kExtract>
+__device__ __forceinline__ float apply_one(float p, uint32_t u16, float scale, float decay,
+                                           float neg_lr) {
+  if constexpr (kExtract) {
+    return bf16_bits_to_float(u16);
+  } else {
+    const float upd = bf16_bits_to_float(u16) * scale;
+    return __fmaf_rn(upd, neg_lr, p * decay);
+  }
+}
+
 template <bool kExtract>
 __global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint16_t* x_all,
                                                        const uint16_t* xt_all, int64_t rows,
@@ -196,17 +262,28 @@ __global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint1
   const bool same_is_x = (tr ? cols : rows) <= pc;
   const float scale = tr ? scale_t : scale_n;
   const uint16_t* U = same_is_x ? x_all + (int64_t)mat * mp * ldn : xt_all + (int64_t)mat * np * ldm;
-  const int64_t ld = same_is_x ? ldn : ldm;
+  const int64_t ld = same_is_x ? ldn : ldm;  // a multiple of 64: U rows are 128-byte aligned
   const int64_t numel = rows * cols;
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
+  if ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && (pc & 3) == 0 && base + kElemsPerBlock <= numel) {
+#pragma unroll
+    for (int k = 0; k < kElemsPerBlock / (4 * kBlock); ++k) {
+      const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
+      const int64_t r = i / pc, c = i - r * pc;  // 4 elements of one row
+      const u32x2 uv = *reinterpret_cast<const u32x2*>(U + r * ld + c);
+      f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (!kExtract) pv = *reinterpret_cast<const f32x4*>(p + i);
+      pv[0] = apply_one<kExtract>(pv[0], uv.x & 0xFFFFu, scale, decay, neg_lr);
+      pv[1] = apply_one<kExtract>(pv[1], uv.x >> 16, scale, decay, neg_lr);
+      pv[2] = apply_one<kExtract>(pv[2], uv.y & 0xFFFFu, scale, decay, neg_lr);
+      pv[3] = apply_one<kExtract>(pv[3], uv.y >> 16, scale, decay, neg_lr);
+      *reinterpret_cast<f32x4*>(p + i) = pv;
+    }
+    return;
+  }
   for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
     const int64_t r = i / pc, c = i - r * pc;
-    if constexpr (kExtract) {
-      p[i] = bf16_bits_to_float(U[r * ld + c]);
-    } else {
-      const float upd = bf16_bits_to_float(U[r * ld + c]) * scale;
-      p[i] = __fmaf_rn(upd, neg_lr, p[i] * decay);
-    }
+    p[i] = apply_one<kExtract>(kExtract ? 0.f : p[i], U[r * ld + c], scale, decay, neg_lr);
   }
 }
 

@@ -125,9 +125,10 @@ def test_orthogonalize_batches_same_shape_matrices():
         assert torch.equal(muon.orthogonalize(g.to(DEV)), b)
 
 
-@pytest.mark.parametrize("shape", [(128, 256), (300, 100)])
+@pytest.mark.parametrize("shape", [(128, 256), (300, 100), (70, 45), (4100, 1024)])
 def test_muon_step_elementwise_bitexact(shape):
-    """momentum/Nesterov and the master update match the oracle bit for bit."""
+    """momentum/Nesterov and the master update match the oracle bit for bit (128-bit
+    paths, their partial blocks and tiles, and the element-wise paths of odd shapes)."""
     from oracle import reference as R
     gen = torch.Generator().manual_seed(7)
     p0 = torch.randn(shape, generator=gen) * .02
