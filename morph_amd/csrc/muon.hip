@@ -32,7 +32,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kMaxMats = 64;
-constexpr int kElemsPerBlock = kBlock * 16;  // 16 elements per lane, lane-strided (coalesced)
+constexpr int kElemsPerBlock = kBlock * 4;   // one 128-bit access per lane (many short blocks stream best)
 constexpr int kTile = 64;                       // transpose tile
 constexpr int64_t kRowPad = 64;                 // bf16 elements appended to every X/Xt/A/B row
 
