@@ -295,6 +295,7 @@ int morph_fp8_unpack(const uint8_t* bytes, const float* scales, int64_t n, void*
 
 /* Flags of morph_gemm_nt_bf16. */
 #define MORPH_GEMM_SYMMETRIC 1 /* C symmetric: compute the upper triangle of tiles, mirror */
+#define MORPH_GEMM_Q_KN 2      /* Q stored [K, N] (ldq >= N): C = alpha P Q + beta D */
 
 /*
  * Batched bf16 GEMM, "NT" layout, fp32 accumulation:
@@ -306,8 +307,11 @@ int morph_fp8_unpack(const uint8_t* bytes, const float* scales, int64_t n, void*
  * iteration of optimizer.py:19-21 are all of this form (see gemm.hip).
  * flags: MORPH_GEMM_SYMMETRIC (requires M == N, Ct == NULL, and D symmetric
  * if given): C is known to be symmetric, so only the upper triangle of tiles
- * is computed and each off-diagonal tile is mirrored.  Pointers 16-byte aligned, leading dimensions and strides multiples of 8;
- * MORPH_ERANGE when a dimension is not a tile multiple.
+ * is computed and each off-diagonal tile is mirrored.  MORPH_GEMM_Q_KN: Q is
+ * stored [K, N] (ldq >= N) and the product is P . Q (not with SYMMETRIC).
+ * C must not overlap P or Q.  Pointers 16-byte aligned, leading dimensions
+ * and strides multiples of 8, at most 2^23; MORPH_ERANGE when a dimension is
+ * not a tile multiple.
  */
 int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D, uint16_t* C,
                        uint16_t* Ct, int64_t M, int64_t N, int64_t K, int64_t batch,

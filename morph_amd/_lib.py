@@ -30,6 +30,7 @@ EXPORTS = (
 )
 GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 256, 256, 64
 GEMM_SYMMETRIC = 1
+GEMM_Q_KN = 2
 ACCUM_ELEMS_PER_BLOCK, ACCUM_OVERWRITE, ACCUM_FINAL = 2048, 1, 2
 FP8_BLOCK = 256
 FATAL_MIN_SCALE = 1

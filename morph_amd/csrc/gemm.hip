@@ -243,7 +243,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, f32x16 (&acc)[4][4],
   }
 }
 
-__global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) {
+// kQKN: Q is stored [K, N] (row-major, N contiguous) instead of [N, K]; its
+// fragments come from the LDS through transposing reads.
+template <bool kQKN>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[kSmemElems];
 
   // XCD-aware numbering: the grid is a multiple of 8; XCD x = id % 8 runs the
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     return reinterpret_cast<const uint16_t*>(lo | (hi << 32));
   };
   const uint16_t* P = uniform(g.P + b * g.sp + row0 * g.ldp);
-  const uint16_t* Q = uniform(g.Q + b * g.sq + col0 * g.ldq);
+  const uint16_t* Q = uniform(g.Q + b * g.sq + (kQKN ? col0 : col0 * g.ldq));
 
   // DMA assignment: a wave loads rows [64 w, 64 w + 64) of an operand
   // sub-tile, 8 rows per instruction; lane l -> row base + l / 8, LDS slot
@@ -287,19 +290,54 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     const int r = wave * 64 + j * 8 + lrow;
     const uint32_t c = (uint32_t)(lslot ^ swz(r));
     offp[j] = (uint32_t)r * (uint32_t)g.ldp * 2u + c * 16u;
-    offq[j] = (uint32_t)r * (uint32_t)g.ldq * 2u + c * 16u;
+    if constexpr (kQKN) {
+      // [K, N] operand: an instruction loads two 512-byte k-rows of the stage;
+      // lane l -> k-row 16 w + 2 j + l / 32, slot l % 32 holding global chunk
+      // slot ^ (4 (row % 4)).  Eight adjacent lanes still cover one 128-byte line.
+      const int rk = wave * 16 + j * 2 + (lane >> 5);
+      const uint32_t ck = (uint32_t)((lane & 31) ^ (4 * (rk & 3)));
+      offq[j] = (uint32_t)rk * (uint32_t)g.ldq * 2u + ck * 16u;
+    } else {
+      offq[j] = (uint32_t)r * (uint32_t)g.ldq * 2u + c * 16u;
+    }
   }
   // Load j (0..7) of operand Q (or P) of stage `stage` into ring slot `slot`;
   // stages past the end load the last one again (never read; it keeps every
   // step's load count, and so the vmcnt bookkeeping, the same).
+  //
+  // With a [K, N] Q the load is written as inline assembly, not the
+  // compiler's builtin: the compiler then tracks no LDS-DMA writes and cannot
+  // add vmcnt(0) waits in front of the transposing LDS reads, which it does
+  // for every one of them (it cannot prove them disjoint from a pending DMA),
+  // serializing the pipeline.  Completion is managed explicitly anyway: the
+  // vmcnt waits before the per-stage barriers, and the vmcnt(0) of the
+  // barrier before the epilogue.  The [N, K] form keeps the builtin, which
+  // the compiler schedules a little tighter (about 120 cycles per stage).
   auto issue_load = [&](bool q, int slot, int64_t stage, int j) {
     const int64_t k0 = (stage < KT ? stage : KT - 1) * BK;
-    // raw buffer over the stage's columns: base in scalar registers, no range limit
-    // beyond the 32-bit offsets
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>((q ? Q : P) + k0), (short)0, (int)0xFFFFFFFF, 0x00020000);
-    uint16_t* dst = smem + slot * kSubTile + (wave * 64 + j * 8) * BK;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)dst, 16, q ? offq[j] : offp[j], 0, 0, 0);
+    const uint16_t* base = q ? (kQKN ? Q + k0 * g.ldq : Q + k0) : P + k0;
+    const uint16_t* dst = smem + slot * kSubTile +
+                          ((q && kQKN) ? (wave * 16 + j * 2) * BN : (wave * 64 + j * 8) * BK);
+    const uint32_t off = q ? offq[j] : offp[j];
+    if constexpr (kQKN) {
+      // raw buffer descriptor: 48-bit base, stride 0, no range limit beyond
+      // the 32-bit offsets, 32-bit data format
+      const uint64_t addr = reinterpret_cast<uint64_t>(base);
+      const u32x4 rsrc = u32x4{(uint32_t)addr, (uint32_t)(addr >> 32) & 0xFFFFu, 0xFFFFFFFFu,
+                               0x00020000u};
+      const uint32_t m0 = (uint32_t)reinterpret_cast<uintptr_t>(
+          (__attribute__((address_space(3))) const uint16_t*)dst);
+      // M0 (the instruction's LDS base) is an input the compiler sets; the
+      // s_nop is the wait state between an M0 write and an LDS DMA
+      asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                   :
+                   : "v"(off), "s"(rsrc), "{m0}"(m0)
+                   : "memory");
+    } else {
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(base), (short)0, (int)0xFFFFFFFF, 0x00020000);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)dst, 16, off, 0, 0, 0);
+    }
   };
 
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
@@ -327,12 +365,47 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     const int i = n >> 2, j = n & 3;
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.q[j], acc[i][j], 0, 0, 0);
   };
+  // [K, N] operand: half h (k 4h .. 4h + 3 of this lane's 8) of the Q
+  // fragment of columns n0 .. n0 + 31 at depth kk.  In each 16-lane group
+  // ds_read_b64_tr_b16 hands destination lane j, slot e, element j % 4 of
+  // source lane 4 e + j / 4 (checked on the device); so source lane s reads
+  // row kbase + s / 4, columns n0' + 4 (s % 4) .. + 3, and lane j receives
+  // rows kbase .. kbase + 3 of column n0' + j: the MFMA B layout.  The chunk
+  // swizzle puts the 4 rows x 4 chunks a half-wave reads on 16 distinct banks.
+  auto frag_kn = [&](const uint16_t* sub, int n0, int kk, int h) {
+    const int j = lane & 15;
+    const int row = kk * 16 + 8 * (lane >> 5) + 4 * h + (j >> 2);
+    const int col = n0 + 16 * ((lane >> 4) & 1) + 4 * (j & 3);
+    const uint16_t* at = sub + row * BN + ((((col >> 3) ^ (4 * (row & 3))) << 3) | (col & 7));
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+    // the result is used only as a whole: extracting elements of this
+    // builtin's vector has been miscompiled
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4*)(__attribute__((address_space(3))) uint16_t*)at));
+  };
+  // Fragment reads of one sub-step: 8 (P and Q rows), or 12 with a [K, N]
+  // Q (4 P rows and two halves per Q fragment), read n of them.
+  constexpr int kReads = kQKN ? 12 : 8;
   auto read = [&](int n, Frags& f, int pslot, int qslot, int kk) {
-    const int i = n >> 1;
-    if (n & 1)
-      f.q[i] = frag(smem + qslot * kSubTile, wc + i * 32 + fr, kk * 2 + fh);
-    else
-      f.a[i] = frag(smem + pslot * kSubTile, wr + i * 32 + fr, kk * 2 + fh);
+    if constexpr (kQKN) {
+      const int i = n / 3, part = n % 3;
+      if (part == 0) {
+        f.a[i] = frag(smem + pslot * kSubTile, wr + i * 32 + fr, kk * 2 + fh);
+      } else {
+        const u32x2 half = frag_kn(smem + qslot * kSubTile, wc + i * 32, kk, part - 1);
+        u32x4 q = __builtin_bit_cast(u32x4, f.q[i]);
+        if (part == 1) q.x = half.x, q.y = half.y;
+        else q.z = half.x, q.w = half.y;
+        f.q[i] = __builtin_bit_cast(bf16x8, q);
+      }
+    } else {
+      const int i = n >> 1;
+      if (n & 1)
+        f.q[i] = frag(smem + qslot * kSubTile, wc + i * 32 + fr, kk * 2 + fh);
+      else
+        f.a[i] = frag(smem + pslot * kSubTile, wr + i * 32 + fr, kk * 2 + fh);
+    }
   };
 
   // Pipeline.  The LDS is a ring of five 32 KiB slots holding operand
@@ -362,7 +435,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
     for (int n = 0; n < 16; ++n) {
       mfma(n, cur);
       __builtin_amdgcn_sched_barrier(0);
-      if (n < 8) read(n, nxt, rp, rq, kk);
+      if (n < kReads) read(n, nxt, rp, rq, kk);
       if (n >= 2 && n < 10 && (n & 1) == 0) issue_load(lq, ls_, lstage, j0 + ((n - 2) >> 1));
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -391,7 +464,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
       mfma(n, f1);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (kNext) {
-        if (n < 10) read(n - 2, f0, ps1, qs1, 0);
+        if (n - 2 < kReads) read(n - 2, f0, ps1, qs1, 0);
         // Q of t + 2 into the freed P slot of t, loads 0..3
         if (n >= 6 && n < 14 && (n & 1) == 0) issue_load(true, ps, t + 2, (n - 6) >> 1);
       }
@@ -413,7 +486,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_nt_kernel(const GemmArgs g) 
   __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): P0 and Q0 landed for this wave
   lds_barrier();
 #pragma unroll
-  for (int n = 0; n < 8; ++n) read(n, f0, 0, 1, 0);
+  for (int n = 0; n < kReads; ++n) read(n, f0, 0, 1, 0);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 
   int ps = 0;
@@ -473,14 +546,16 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
       misaligned(Ct, 16))
     return MORPH_EINVAL;
   if (M % BM || N % BN || K % MORPH_GEMM_TILE_K) return MORPH_ERANGE;
-  if (flags & ~MORPH_GEMM_SYMMETRIC) return MORPH_EINVAL;
+  if (flags & ~(MORPH_GEMM_SYMMETRIC | MORPH_GEMM_Q_KN)) return MORPH_EINVAL;
   const bool symmetric = (flags & MORPH_GEMM_SYMMETRIC) != 0;
-  if (ldp < K || ldq < K || ldc < N || (D && ldd < N) || (Ct && ldct < M)) return MORPH_EINVAL;
+  const bool qkn = (flags & MORPH_GEMM_Q_KN) != 0;
+  if (ldp < K || ldq < (qkn ? N : K) || ldc < N || (D && ldd < N) || (Ct && ldct < M))
+    return MORPH_EINVAL;
   // 16-byte loads and stores of rows: every leading dimension and batch stride a multiple of 8
   if ((ldp | ldq | ldc | stride_p | stride_q | stride_c) % 8 ||
       (D && (ldd | stride_d) % 8) || (Ct && (ldct | stride_ct) % 8))
     return MORPH_EINVAL;
-  if (symmetric && (M != N || Ct != nullptr)) return MORPH_EINVAL;
+  if (symmetric && (M != N || Ct != nullptr || qkn)) return MORPH_EINVAL;
   // operand-load and epilogue offsets inside a tile are 32-bit: 255 rows of
   // the widest leading dimension
   constexpr int64_t kMaxLd = int64_t(1) << 23;
@@ -496,7 +571,11 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
   GemmArgs g{P, Q, D, C, Ct, K, ldp, ldq, ldd, ldc, ldct,
              stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta,
              (int32_t)tm, (int32_t)tn, (int32_t)per, flags, total};
-  hipLaunchKernelGGL(gemm_nt_kernel, dim3((unsigned)grid), dim3(kThreads), 0, as_stream(stream),
-                     g);
+  if (qkn)
+    hipLaunchKernelGGL(gemm_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0,
+                       as_stream(stream), g);
+  else
+    hipLaunchKernelGGL(gemm_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0,
+                       as_stream(stream), g);
   return launch_status();
 }

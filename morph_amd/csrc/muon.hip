@@ -18,10 +18,11 @@
 //
 // Workspace (caller-allocated, zero-filled once; morph_muon_workspace_bytes):
 // u fp32 [count][rows*cols]; per-block partial sums f64; denominators f32;
-// X [count][Mp][Np], Xt0/Xt1 [count][Np][Mp], A and B [count][Mp][Mp], bf16,
-// with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.  The
-// zero padding is exact for Newton-Schulz: padded rows of X give zero rows and
-// columns of A and B, which keep the padding of X zero in every iteration.
+// X0/X1 [count][Mp][Np] (iterations alternate: X' = a X + B X reads all of X
+// as its [K, N] operand, so it cannot overwrite it), A and B [count][Mp][Mp],
+// bf16, with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.
+// The zero padding is exact for Newton-Schulz: padded rows of X give zero rows
+// and columns of A and B, which keep the padding of X zero in every iteration.
 // Rows are stored kRowPad elements longer than Mp / Np (never read): with
 // rows a multiple of 4 KiB apart, the 256 rows of a GEMM operand tile fall
 // on few L2 channels; the pad spreads them (about 6% on the K = Mp products).
@@ -34,7 +35,7 @@ constexpr int kBlock = 256;
 constexpr int kMaxMats = 64;
 constexpr int kElemsPerBlock = kBlock * 4;   // one 128-bit access per lane (many short blocks stream best)
 constexpr int kTile = 64;                       // transpose tile
-constexpr int64_t kRowPad = 64;                 // bf16 elements appended to every X/Xt/A/B row
+constexpr int64_t kRowPad = 64;                 // bf16 elements appended to every X/A/B row
 
 struct MatPtrs {
   const float* grad[kMaxMats];
@@ -47,8 +48,8 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct Layout {
   int64_t rows, cols, m, n, mp, np, count, numel, blocks;
-  int64_t ldn, ldm;  // row lengths of X ([Mp][ldn]) and of Xt, A, B ([*][ldm])
-  size_t off_u, off_part, off_den, off_x, off_xt0, off_xt1, off_a, off_b, total;
+  int64_t ldn, ldm;  // row lengths of X ([Mp][ldn]) and of A, B ([Mp][ldm])
+  size_t off_u, off_part, off_den, off_x0, off_x1, off_a, off_b, total;
 };
 
 Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
@@ -73,9 +74,8 @@ Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
   L.off_u = take((size_t)count * L.numel * 4);
   L.off_part = take((size_t)count * L.blocks * 8);
   L.off_den = take((size_t)count * 4);
-  L.off_x = take((size_t)count * L.mp * L.ldn * 2);
-  L.off_xt0 = take((size_t)count * L.np * L.ldm * 2);
-  L.off_xt1 = take((size_t)count * L.np * L.ldm * 2);
+  L.off_x0 = take((size_t)count * L.mp * L.ldn * 2);
+  L.off_x1 = take((size_t)count * L.mp * L.ldn * 2);
   L.off_a = take((size_t)count * L.mp * L.ldm * 2);
   L.off_b = take((size_t)count * L.mp * L.ldm * 2);
   L.total = off;
@@ -166,77 +166,90 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(const double* part_all, fl
   if (threadIdx.x == 0) den[mat] = (float)sqrt(t) + 1e-7f;
 }
 
-// X / Xt (bf16, padded) from u / den.  A matrix's stored layout is
-// [pr, pc] = [rows, cols], or [cols, rows] when transposed; X is [m, n] with
-// m = min: when pr <= pc X has the stored layout and Xt is the transpose,
-// otherwise the other way round.  One 64 x 64 tile of u per block, transposed
-// through LDS so both writes are coalesced; a lane moves 4 consecutive
-// elements per access (128-bit u reads, 64-bit bf16 writes) where the tile is
-// whole and the rows are a multiple of 4 long.  The grid covers [rows, cols] in
-// 64-tiles; a transposed matrix reads block (x, y) as its tile (y, x).
+// Tile geometry shared by scale_kernel and apply_kernel.  A matrix's stored
+// layout is [pr, pc] = [rows, cols], or [cols, rows] when transposed; X is
+// [m, n] with m = min.  When pr <= pc X has the stored layout, otherwise it is
+// the transpose.  One 64 x 64 tile of the stored layout per block; the grid
+// covers [rows, cols] in 64-tiles and a transposed matrix reads block (x, y)
+// as its tile (y, x).  `vec`: a whole tile with rows a multiple of 4, moved 4
+// consecutive elements per lane access.
+struct TileGeo {
+  int64_t pr, pc, r0, c0;
+  bool same_is_x, vec;
+};
+
+__device__ __forceinline__ TileGeo tile_geo(const MatPtrs& mats, int mat, int64_t rows,
+                                            int64_t cols) {
+  TileGeo t;
+  const bool tr = mats.transposed[mat] != 0;
+  t.pr = tr ? cols : rows;
+  t.pc = tr ? rows : cols;
+  t.same_is_x = t.pr <= t.pc;
+  t.r0 = (int64_t)(tr ? blockIdx.x : blockIdx.y) * kTile;
+  t.c0 = (int64_t)(tr ? blockIdx.y : blockIdx.x) * kTile;
+  t.vec = (t.pc & 3) == 0 && (t.pr & 3) == 0 && t.r0 + kTile <= t.pr && t.c0 + kTile <= t.pc;
+  return t;
+}
+
+// X (bf16, padded [Mp][ldn]) from u / den.  X in the stored layout is
+// written straight from the tile; otherwise the tile is transposed through
+// LDS so both the u reads and the X writes are coalesced.
 __global__ __launch_bounds__(kBlock) void scale_kernel(MatPtrs mats, const float* u_all,
                                                        const float* den, uint16_t* x_all,
-                                                       uint16_t* xt_all, int64_t rows,
-                                                       int64_t cols, int64_t mp, int64_t np,
-                                                       int64_t ldm, int64_t ldn, int64_t numel) {
+                                                       int64_t rows, int64_t cols, int64_t mp,
+                                                       int64_t ldn, int64_t numel) {
   __shared__ __attribute__((aligned(8))) uint16_t tile[kTile][kTile + 4];
   const int mat = blockIdx.z;
-  const bool tr = mats.transposed[mat] != 0;
-  const int64_t pr = tr ? cols : rows, pc = tr ? rows : cols;  // stored shape
+  const TileGeo t = tile_geo(mats, mat, rows, cols);
   const float d = den[mat];
-  const float* u = u_all + (int64_t)mat * numel;
-  const bool same_is_x = pr <= pc;  // X has the stored layout
+  const float* u = u_all + (int64_t)mat * numel;  // 16-byte aligned when pc % 4 == 0
   uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
-  uint16_t* xtm = xt_all + (int64_t)mat * np * ldm;
-  uint16_t* same = same_is_x ? xm : xtm;
-  uint16_t* trans = same_is_x ? xtm : xm;
-  // row lengths of the stored-layout and transposed copies (multiples of 64)
-  const int64_t ld_same = same_is_x ? ldn : ldm;
-  const int64_t ld_trans = same_is_x ? ldm : ldn;
-  const int64_t r0 = (int64_t)(tr ? blockIdx.x : blockIdx.y) * kTile;
-  const int64_t c0 = (int64_t)(tr ? blockIdx.y : blockIdx.x) * kTile;
   const int q = threadIdx.x & 15, w = threadIdx.x >> 4;  // 4-element group, row of a pass
-  // u is 256-byte aligned per matrix when numel % 4 == 0 (then pc % 4 == 0 or pr % 4 == 0)
-  const bool vec = (pc & 3) == 0 && (pr & 3) == 0 && r0 + kTile <= pr && c0 + kTile <= pc;
   for (int rr = w; rr < kTile; rr += kBlock / 16) {
-    const int64_t r = r0 + rr, c = c0 + 4 * q;
+    const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
     uint32_t h[4] = {0, 0, 0, 0};
-    if (vec) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(u + r * pc + c);
+    if (t.vec) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(u + r * t.pc + c);
 #pragma unroll
       for (int e = 0; e < 4; ++e) h[e] = float_to_bf16_bits(v[e] / d);
-      *reinterpret_cast<u32x2*>(same + r * ld_same + c) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (r < pr && c + e < pc) {
-          h[e] = float_to_bf16_bits(u[r * pc + c + e] / d);
-          same[r * ld_same + c + e] = (uint16_t)h[e];
-        }
+        if (r < t.pr && c + e < t.pc) h[e] = float_to_bf16_bits(u[r * t.pc + c + e] / d);
     }
-    *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    if (t.same_is_x) {
+      if (t.vec) {
+        *reinterpret_cast<u32x2*>(xm + r * ldn + c) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (r < t.pr && c + e < t.pc) xm[r * ldn + c + e] = (uint16_t)h[e];
+      }
+    } else {
+      *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    }
   }
+  if (t.same_is_x) return;  // block-uniform
   __syncthreads();
   for (int cc = w; cc < kTile; cc += kBlock / 16) {
-    const int64_t c = c0 + cc, r = r0 + 4 * q;
+    const int64_t c = t.c0 + cc, r = t.r0 + 4 * q;  // X row c, columns r .. r + 3
     uint32_t h[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) h[e] = tile[4 * q + e][cc];
-    if (vec) {
-      *reinterpret_cast<u32x2*>(trans + c * ld_trans + r) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    if (t.vec) {
+      *reinterpret_cast<u32x2*>(xm + c * ldn + r) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (c < pc && r + e < pr) trans[c * ld_trans + r + e] = (uint16_t)h[e];
+        if (c < t.pc && r + e < t.pr) xm[c * ldn + r + e] = (uint16_t)h[e];
     }
   }
 }
 
-// p = p * decay + (U * scale) * neg_lr, U read from the bf16 copy in p's
-// layout; scale is scale_t for a transposed matrix.
-// kExtract: p = U instead (orthogonalize alone returns the fp32 value of U).
-// When p is 16-byte aligned and its rows a multiple of 4 long, a lane moves 4
-// consecutive elements of one row per access (128-bit p, 64-bit U).
+// p = p * decay + (U * scale) * neg_lr with U = X in p's layout; scale is
+// scale_t for a transposed matrix.  kExtract: p = U instead (orthogonalize
+// alone returns the fp32 value of U).  Same tiles as scale_kernel: when X is
+// the transpose of p's layout the tile of X is staged through LDS first.
 template <bool kExtract>
 __device__ __forceinline__ float apply_one(float p, uint32_t u16, float scale, float decay,
                                            float neg_lr) {
@@ -250,40 +263,63 @@ __device__ __forceinline__ float apply_one(float p, uint32_t u16, float scale, f
 
 template <bool kExtract>
 __global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint16_t* x_all,
-                                                       const uint16_t* xt_all, int64_t rows,
-                                                       int64_t cols, int64_t mp, int64_t np,
-                                                       int64_t ldm, int64_t ldn, float scale_n,
-                                                       float scale_t, float decay,
-                                                       float neg_lr) {
-  const int mat = blockIdx.y;
+                                                       int64_t rows, int64_t cols, int64_t mp,
+                                                       int64_t ldn, float scale_n, float scale_t,
+                                                       float decay, float neg_lr) {
+  __shared__ __attribute__((aligned(8))) uint16_t tile[kTile][kTile + 4];
+  const int mat = blockIdx.z;
+  const TileGeo t = tile_geo(mats, mat, rows, cols);
   float* p = mats.param[mat];
-  const bool tr = mats.transposed[mat] != 0;
-  const int64_t pc = tr ? rows : cols;  // stored row length
-  const bool same_is_x = (tr ? cols : rows) <= pc;
-  const float scale = tr ? scale_t : scale_n;
-  const uint16_t* U = same_is_x ? x_all + (int64_t)mat * mp * ldn : xt_all + (int64_t)mat * np * ldm;
-  const int64_t ld = same_is_x ? ldn : ldm;  // a multiple of 64: U rows are 128-byte aligned
-  const int64_t numel = rows * cols;
-  const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
-  if ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && (pc & 3) == 0 && base + kElemsPerBlock <= numel) {
+  const float scale = mats.transposed[mat] ? scale_t : scale_n;
+  const uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
+  const bool vec = t.vec && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+  const int q = threadIdx.x & 15, w = threadIdx.x >> 4;
+  if (!t.same_is_x) {
+    // tile[c - c0][r - r0] = X[c][r]: X rows c0 .. c0 + 63, columns r0 .. r0 + 63
+    for (int cc = w; cc < kTile; cc += kBlock / 16) {
+      const int64_t c = t.c0 + cc, r = t.r0 + 4 * q;
+      u32x2 v = u32x2{0, 0};
+      if (t.vec) {
+        v = *reinterpret_cast<const u32x2*>(xm + c * ldn + r);
+      } else {
+        uint32_t h[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int k = 0; k < kElemsPerBlock / (4 * kBlock); ++k) {
-      const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
-      const int64_t r = i / pc, c = i - r * pc;  // 4 elements of one row
-      const u32x2 uv = *reinterpret_cast<const u32x2*>(U + r * ld + c);
-      f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (!kExtract) pv = *reinterpret_cast<const f32x4*>(p + i);
-      pv[0] = apply_one<kExtract>(pv[0], uv.x & 0xFFFFu, scale, decay, neg_lr);
-      pv[1] = apply_one<kExtract>(pv[1], uv.x >> 16, scale, decay, neg_lr);
-      pv[2] = apply_one<kExtract>(pv[2], uv.y & 0xFFFFu, scale, decay, neg_lr);
-      pv[3] = apply_one<kExtract>(pv[3], uv.y >> 16, scale, decay, neg_lr);
-      *reinterpret_cast<f32x4*>(p + i) = pv;
+        for (int e = 0; e < 4; ++e)
+          if (c < t.pc && r + e < t.pr) h[e] = xm[c * ldn + r + e];
+        v = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      }
+      *reinterpret_cast<u32x2*>(&tile[cc][4 * q]) = v;
     }
-    return;
+    __syncthreads();
   }
-  for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
-    const int64_t r = i / pc, c = i - r * pc;
-    p[i] = apply_one<kExtract>(kExtract ? 0.f : p[i], U[r * ld + c], scale, decay, neg_lr);
+  for (int rr = w; rr < kTile; rr += kBlock / 16) {
+    const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
+    uint32_t h[4];
+    if (t.same_is_x) {
+      if (t.vec) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(xm + r * ldn + c);
+        h[0] = v.x & 0xFFFFu, h[1] = v.x >> 16, h[2] = v.y & 0xFFFFu, h[3] = v.y >> 16;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = (r < t.pr && c + e < t.pc) ? xm[r * ldn + c + e] : 0u;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = tile[4 * q + e][rr];
+    }
+    float* pr_ = p + r * t.pc + c;
+    if (vec) {
+      f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (!kExtract) pv = *reinterpret_cast<const f32x4*>(pr_);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pv[e] = apply_one<kExtract>(pv[e], h[e], scale, decay, neg_lr);
+      *reinterpret_cast<f32x4*>(pr_) = pv;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (r < t.pr && c + e < t.pc)
+          pr_[e] = apply_one<kExtract>(kExtract ? 0.f : pr_[e], h[e], scale, decay, neg_lr);
+    }
   }
 }
 
@@ -305,8 +341,7 @@ struct Bufs {
   float* u;
   double* part;
   float* den;
-  uint16_t* X;
-  uint16_t* Xt[2];
+  uint16_t* X[2];
   uint16_t* A;
   uint16_t* B;
 };
@@ -329,18 +364,23 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   const Layout L = make_layout(rows, cols, count > 0 ? count : 1);
   if (workspace == nullptr || workspace_bytes < L.total) return MORPH_EWORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return MORPH_EINVAL;
-  if ((rows + kTile - 1) / kTile > 65535) return MORPH_ERANGE;  // grid y of scale_kernel
+  if ((rows + kTile - 1) / kTile > 65535) return MORPH_ERANGE;  // grid y of scale/apply
   char* ws = static_cast<char*>(workspace);
   out->L = L;
   out->u = reinterpret_cast<float*>(ws + L.off_u);
   out->part = reinterpret_cast<double*>(ws + L.off_part);
   out->den = reinterpret_cast<float*>(ws + L.off_den);
-  out->X = reinterpret_cast<uint16_t*>(ws + L.off_x);
-  out->Xt[0] = reinterpret_cast<uint16_t*>(ws + L.off_xt0);
-  out->Xt[1] = reinterpret_cast<uint16_t*>(ws + L.off_xt1);
+  out->X[0] = reinterpret_cast<uint16_t*>(ws + L.off_x0);
+  out->X[1] = reinterpret_cast<uint16_t*>(ws + L.off_x1);
   out->A = reinterpret_cast<uint16_t*>(ws + L.off_a);
   out->B = reinterpret_cast<uint16_t*>(ws + L.off_b);
   return MORPH_OK;
+}
+
+// 64 x 64 tiles of [rows, cols] per matrix (scale_kernel, apply_kernel).
+dim3 tile_grid(int64_t rows, int64_t cols, int count) {
+  return dim3((unsigned)((cols + kTile - 1) / kTile), (unsigned)((rows + kTile - 1) / kTile),
+              (unsigned)count);
 }
 
 MatPtrs pointers(const morph_muon_matrix* mats, int count) {
@@ -373,11 +413,8 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, W.part, W.den, L.blocks);
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(scale_kernel,
-                     dim3((unsigned)((cols + kTile - 1) / kTile),
-                          (unsigned)((rows + kTile - 1) / kTile), count),
-                     dim3(kBlock), 0, s, mp_, W.u, W.den, W.X, W.Xt[0], rows, cols, L.mp, L.np,
-                     L.ldm, L.ldn, L.numel);
+  hipLaunchKernelGGL(scale_kernel, tile_grid(rows, cols, count), dim3(kBlock), 0, s, mp_, W.u,
+                     W.den, W.X[0], rows, cols, L.mp, L.ldn, L.numel);
   return launch_status();
 }
 
@@ -387,21 +424,22 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
   int rc = setup(nullptr, count, rows, cols, hp, workspace, workspace_bytes, false, false, &W);
   if (rc || count == 0) return rc;
   const Layout& L = W.L;
-  const int64_t sx = L.mp * L.ldn, st = L.np * L.ldm, ss = L.mp * L.ldm;
+  const int64_t sx = L.mp * L.ldn, ss = L.mp * L.ldm;
   const int64_t n = L.ldn, m = L.ldm;  // leading dimensions
   int cur = 0;
   for (int it = 0; it < hp->ns_steps; ++it) {
+    uint16_t* X = W.X[cur];
     // A = X X^T (symmetric: upper triangle of tiles, mirrored)
-    rc = morph_gemm_nt_bf16(W.X, W.X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, n, n, 0, m, 0,
+    rc = morph_gemm_nt_bf16(X, X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, n, n, 0, m, 0,
                             sx, sx, 0, ss, 0, 1.0f, 0.0f, MORPH_GEMM_SYMMETRIC, stream);
     if (rc) return rc;
     // B = c (A A^T) + b A (symmetric)
     rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, m, m, m, m, 0,
                             ss, ss, ss, ss, 0, hp->c, hp->b, MORPH_GEMM_SYMMETRIC, stream);
     if (rc) return rc;
-    // X' = (B Xt^T) + a X, written in place over X and transposed into the other Xt
-    rc = morph_gemm_nt_bf16(W.B, W.Xt[cur], W.X, W.X, W.Xt[cur ^ 1], L.mp, L.np, L.mp, count, m, m,
-                            n, n, m, ss, st, sx, sx, st, 1.0f, hp->a, 0, stream);
+    // X' = B X + a X: X as the [K, N] operand (transposing LDS reads), into the other buffer
+    rc = morph_gemm_nt_bf16(W.B, X, X, W.X[cur ^ 1], nullptr, L.mp, L.np, L.mp, count, m, n, n, n,
+                            0, ss, sx, sx, sx, 0, 1.0f, hp->a, MORPH_GEMM_Q_KN, stream);
     if (rc) return rc;
     cur ^= 1;
   }
@@ -416,17 +454,17 @@ int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   if (rc || count == 0) return rc;
   const Layout& L = W.L;
   const MatPtrs mp_ = pointers(mats, count);
-  const dim3 ew((unsigned)L.blocks, count);
-  uint16_t* xt = W.Xt[hp->ns_steps & 1];  // the copy the last iteration wrote
+  const uint16_t* x = W.X[hp->ns_steps & 1];  // the buffer the last iteration wrote
   hipStream_t s = as_stream(stream);
+  const dim3 grid = tile_grid(rows, cols, count);
   if (orth_only)
-    hipLaunchKernelGGL(apply_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
-                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->update_scale_transposed,
-                       hp->decay, hp->neg_lr);
+    hipLaunchKernelGGL(apply_kernel<true>, grid, dim3(kBlock), 0, s, mp_, x, rows, cols, L.mp,
+                       L.ldn, hp->update_scale, hp->update_scale_transposed, hp->decay,
+                       hp->neg_lr);
   else
-    hipLaunchKernelGGL(apply_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.X, xt, rows, cols,
-                       L.mp, L.np, L.ldm, L.ldn, hp->update_scale, hp->update_scale_transposed,
-                       hp->decay, hp->neg_lr);
+    hipLaunchKernelGGL(apply_kernel<false>, grid, dim3(kBlock), 0, s, mp_, x, rows, cols, L.mp,
+                       L.ldn, hp->update_scale, hp->update_scale_transposed, hp->decay,
+                       hp->neg_lr);
   return launch_status();
 }
 

@@ -30,22 +30,24 @@ def _bf16_ptr(t):
 
 
 def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, symmetric=False,
-            stream=None):
+            stream=None, q_kn=False):
     """out = alpha * P @ Q^T + beta * D (bf16, fp32 accumulation); out_t = out^T if given.
 
     P [.., M, K], Q [.., N, K], D/out [.., M, N], out_t [.., N, M]; a leading batch
     dimension is optional.  M, N multiples of 256 and K of 64.  symmetric=True:
     the result is known to be symmetric (M == N, D symmetric): only the upper
-    triangle of tiles is computed and mirrored.
+    triangle of tiles is computed and mirrored.  q_kn=True: Q is [.., K, N] and
+    the product is P @ Q (transposing LDS reads; out must not overlap Q).
     """
     batched = P.dim() == 3
     if not batched:
         P, Q = P.unsqueeze(0), Q.unsqueeze(0)
         D = D.unsqueeze(0) if D is not None else None
     b, M, K = P.shape
-    N = Q.shape[1]
-    if Q.shape != (b, N, K) or (D is not None and D.shape != (b, M, N)):
-        raise ValueError("gemm_nt: shapes do not match P [b,M,K], Q [b,N,K], D [b,M,N]")
+    N = Q.shape[2] if q_kn else Q.shape[1]
+    if Q.shape != ((b, K, N) if q_kn else (b, N, K)) or (D is not None and D.shape != (b, M, N)):
+        raise ValueError("gemm_nt: shapes do not match P [b,M,K], Q [b,N,K] (or [b,K,N]), "
+                         "D [b,M,N]")
     if out is None:
         out = torch.empty((b, M, N), dtype=torch.bfloat16, device=P.device)
     elif not batched:
@@ -54,10 +56,10 @@ def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, symmetric=F
         out_t = out_t.unsqueeze(0)
     if out.shape != (b, M, N) or (out_t is not None and out_t.shape != (b, N, M)):
         raise ValueError("gemm_nt: output shapes do not match")
-    flags = _lib.GEMM_SYMMETRIC if symmetric else 0
+    flags = (_lib.GEMM_SYMMETRIC if symmetric else 0) | (_lib.GEMM_Q_KN if q_kn else 0)
     check(lib().morph_gemm_nt_bf16(
         _bf16_ptr(P), _bf16_ptr(Q), _bf16_ptr(D), _bf16_ptr(out), _bf16_ptr(out_t),
-        M, N, K, b, K, K, N, N, M, M * K, N * K, M * N, M * N, N * M,
+        M, N, K, b, K, N if q_kn else K, N, N, M, M * K, N * K, M * N, M * N, N * M,
         float(alpha), float(beta), flags, stream_handle(stream)))
     return out if batched else out[0]
 

@@ -58,7 +58,8 @@ def test_argument_validation_happens_before_any_launch():
     p = ctypes.c_void_p(0x10000)
     gemm = lambda M, N, K, flags, Ct=None: lib.morph_gemm_nt_bf16(
         p, p, None, p, Ct, M, N, K, 1, K, K, 0, N, M, 0, 0, 0, 0, 0, 1.0, 0.0, flags, None)
-    assert gemm(256, 256, 64, 2) == -1                   # unknown flag bit
+    assert gemm(256, 256, 64, 4) == -1                   # unknown flag bit
+    assert gemm(256, 256, 64, _lib.GEMM_SYMMETRIC | _lib.GEMM_Q_KN) == -1
     assert gemm(256, 512, 64, _lib.GEMM_SYMMETRIC) == -1  # symmetric needs M == N
     assert gemm(256, 256, 64, _lib.GEMM_SYMMETRIC, Ct=p) == -1
     assert gemm(100, 256, 64, 0) == -4                    # not a tile multiple
@@ -113,6 +114,7 @@ def test_gemm_flag_values_match_header():
     from morph_amd import _lib
     text = (ROOT / "include" / "morph_optim.h").read_text()
     for name, value in (("MORPH_GEMM_SYMMETRIC", _lib.GEMM_SYMMETRIC),
+                        ("MORPH_GEMM_Q_KN", _lib.GEMM_Q_KN),
                         ("MORPH_GEMM_TILE_M", _lib.GEMM_TILE_M),
                         ("MORPH_GEMM_TILE_K", _lib.GEMM_TILE_K)):
         assert re.search(rf"#define {name} {value}\b", text), name

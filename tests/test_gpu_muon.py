@@ -46,6 +46,24 @@ def test_gemm_nt_against_exact_product(b, M, N, K):
     assert torch.equal(out_t.cpu(), C.transpose(1, 2))
 
 
+@pytest.mark.parametrize("b,M,N,K", [(1, 256, 256, 64), (3, 512, 768, 192), (2, 768, 512, 512)])
+def test_gemm_q_kn_equals_the_nt_form_bit_for_bit(b, M, N, K):
+    """Q stored [K, N] (transposing LDS reads) gives the same fragments, so the same bits as
+    passing Q^T in [N, K]; with D, alpha, beta and the transposed copy."""
+    P, Q, D = rand_bf16((b, M, K), 4), rand_bf16((b, N, K), 5), rand_bf16((b, M, N), 6)
+    Pd, Qd, Dd = P.to(DEV), Q.to(DEV), D.to(DEV)
+    Qkn = Qd.transpose(1, 2).contiguous()
+    ta = torch.empty((b, N, M), dtype=torch.bfloat16, device=DEV)
+    tb = torch.empty((b, N, M), dtype=torch.bfloat16, device=DEV)
+    ca = muon.gemm_nt(Pd, Qd, Dd, 3.4445, 1.0, out_t=ta)
+    cb = muon.gemm_nt(Pd, Qkn, Dd, 3.4445, 1.0, out_t=tb, q_kn=True)
+    assert torch.equal(ca, cb) and torch.equal(ta, tb)
+    exact = P.double() @ Q.double().transpose(1, 2)
+    C = muon.gemm_nt(Pd, Qkn, q_kn=True).cpu().double()
+    mag = P.double().abs() @ Q.double().abs().transpose(1, 2)
+    assert ((C - exact).abs() <= 2 ** -8 * exact.abs() + 1e-6 * K * mag + 1e-30).all()
+
+
 @pytest.mark.parametrize("alpha", [1 + 2 ** -8, 1 + 3 * 2 ** -8, 1 / 3, -0.7, 2.0 ** -140, 7.5e37])
 def test_gemm_output_rounding_is_round_to_nearest_even(alpha):
     """C = alpha * I Q^T is one fp32 product alpha * q rounded once to bf16.  With q a
