@@ -213,7 +213,7 @@ def muon_main(args):
         "ns_ms_per_step": round(r["ns_s"] * 1e3, 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "gemm_nt_kernel (3 launches per Newton-Schulz iteration, all 42 matrices batched)",
+                     "traffic": None, "kernel": "gemm_kernel (3 launches per Newton-Schulz iteration, all 42 matrices batched)",
                      "flops_per_step": r["flops"]},
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_muon(),
     }

@@ -1,13 +1,15 @@
-// Batched bf16 "NT" GEMM on gfx950 MFMA, the building block of the Muon
+// Batched bf16 GEMM on gfx950 MFMA, the building block of the Muon
 // Newton-Schulz iteration (streamtrain/optimizer.py:19-21):
 //
 //   C[b] = alpha * P[b] . Q[b]^T + beta * D[b]      (bf16 in, fp32 accumulate, bf16 out)
 //   Ct[b] = C[b]^T                                   (optional second output)
 //
-// P is [M, K] and Q is [N, K], both row-major with K contiguous, so every MFMA
-// operand fragment is 16 contiguous bytes of one row.  One NS iteration is three
-// such products: A = X X^T; B = b A + c A A^T (A is symmetric); X' = a X + B Xt^T
-// (B is symmetric, Xt = X^T), which is why only this one layout is needed.
+// P is [M, K] row-major with K contiguous, so every P fragment is 16
+// contiguous bytes of one row.  Q is [N, K] likewise ("NT"), or [K, N] with N
+// contiguous (MORPH_GEMM_Q_KN): then its fragments come from LDS through
+// gfx950's transposing reads (ds_read_b64_tr_b16) and the product is P . Q.
+// One NS iteration is three products: A = X X^T and B = b A + c A A^T (A is
+// symmetric) in the NT form, and X' = a X + B X with X as the [K, N] operand.
 //
 // Tiling.  A workgroup (256 lanes, 4 wave64) owns a 256 x 256 tile of C; wave w
 // owns the 128 x 128 quarter (w / 2, w % 2) as 4 x 4 tiles of
