@@ -99,6 +99,8 @@ __device__ __forceinline__ double block_sum(double x, double* lds) {
 // kElemsPerBlock consecutive elements; a lane moves 4 consecutive elements per
 // 128-bit access when the matrix's buffers are 16-byte aligned (one
 // contiguous 4 KiB segment per wave access), else one element per access.
+// Every stream is touched once here (u is re-read only after the whole
+// batch, gigabytes later), so the accesses are non-temporal.
 template <bool kMomentum>
 __device__ __forceinline__ void momentum_one(float gi, float& m, float& ui, float mom_w,
                                              float nest_w, bool large_m, bool large_n) {
@@ -128,9 +130,9 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u
 #pragma unroll
     for (int k = 0; k < kElemsPerBlock / (4 * kBlock); ++k) {
       const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
-      const f32x4 gv = *reinterpret_cast<const f32x4*>(g + i);
+      const f32x4 gv = load_stream<true>(reinterpret_cast<const f32x4*>(g + i));
       f32x4 mv = f32x4{0.f, 0.f, 0.f, 0.f}, uv;
-      if constexpr (kMomentum) mv = *reinterpret_cast<const f32x4*>(mom + i);
+      if constexpr (kMomentum) mv = load_stream<true>(reinterpret_cast<const f32x4*>(mom + i));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float m = mv[e], ui;
@@ -139,8 +141,8 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u
         uv[e] = ui;
         ss += (double)ui * (double)ui;
       }
-      if constexpr (kMomentum) *reinterpret_cast<f32x4*>(mom + i) = mv;
-      *reinterpret_cast<f32x4*>(u + i) = uv;
+      if constexpr (kMomentum) store_stream<true>(reinterpret_cast<f32x4*>(mom + i), mv);
+      store_stream<true>(reinterpret_cast<f32x4*>(u + i), uv);
     }
   } else {
     for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
@@ -209,7 +211,7 @@ __global__ __launch_bounds__(kBlock) void scale_kernel(MatPtrs mats, const float
     const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
     uint32_t h[4] = {0, 0, 0, 0};
     if (t.vec) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(u + r * t.pc + c);
+      const f32x4 v = load_stream<true>(reinterpret_cast<const f32x4*>(u + r * t.pc + c));
 #pragma unroll
       for (int e = 0; e < 4; ++e) h[e] = float_to_bf16_bits(v[e] / d);
     } else {
@@ -310,10 +312,10 @@ __global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint1
     float* pr_ = p + r * t.pc + c;
     if (vec) {
       f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (!kExtract) pv = *reinterpret_cast<const f32x4*>(pr_);
+      if constexpr (!kExtract) pv = load_stream<true>(reinterpret_cast<const f32x4*>(pr_));
 #pragma unroll
       for (int e = 0; e < 4; ++e) pv[e] = apply_one<kExtract>(pv[e], h[e], scale, decay, neg_lr);
-      *reinterpret_cast<f32x4*>(pr_) = pv;
+      store_stream<true>(reinterpret_cast<f32x4*>(pr_), pv);
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
