@@ -565,6 +565,25 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
       (Ct && ldct > kMaxLd))
     return MORPH_ERANGE;
   if (M == 0 || N == 0 || batch == 0) return MORPH_OK;
+  // Outputs are written while other tiles still read P and Q: the address
+  // ranges of C and Ct may not meet those of P and Q (D may alias C).
+  auto span = [&](const uint16_t* base, int64_t stride, int64_t rows, int64_t ld,
+                  int64_t cols) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(base);
+    return std::pair<uintptr_t, uintptr_t>(
+        lo, lo + 2 * (uintptr_t)((batch - 1) * stride + (rows - 1) * ld + cols));
+  };
+  auto meet = [](std::pair<uintptr_t, uintptr_t> a, std::pair<uintptr_t, uintptr_t> b) {
+    return a.first < b.second && b.first < a.second;
+  };
+  const auto sp = span(P, stride_p, M, ldp, K);
+  const auto sq = qkn ? span(Q, stride_q, K, ldq, N) : span(Q, stride_q, N, ldq, K);
+  const auto sc = span(C, stride_c, M, ldc, N);
+  if (meet(sc, sp) || meet(sc, sq)) return MORPH_EINVAL;
+  if (Ct) {
+    const auto st = span(Ct, stride_ct, N, ldct, M);
+    if (meet(st, sp) || meet(st, sq) || meet(st, sc)) return MORPH_EINVAL;
+  }
   const int64_t tm = M / BM, tn = N / BN;
   const int64_t per = symmetric ? tm * (tm + 1) / 2 : tm * tn;
   const int64_t total = batch * per;

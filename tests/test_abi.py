@@ -64,6 +64,13 @@ def test_argument_validation_happens_before_any_launch():
     assert gemm(256, 256, 64, _lib.GEMM_SYMMETRIC, Ct=p) == -1
     assert gemm(100, 256, 64, 0) == -4                    # not a tile multiple
     assert gemm(256, 256, 0, 0) == -1
+    # the output may not overlap an operand (other tiles still read it); D may alias C
+    q, c = ctypes.c_void_p(0x100000), ctypes.c_void_p(0x200000)
+    ok = lambda C, flags=0, D=None: lib.morph_gemm_nt_bf16(
+        p, q, D, C, None, 256, 256, 64, 1, 64, 256 if flags else 64, 256, 256, 0, 0, 0, 0, 0, 0,
+        1.0, 0.0, flags, None)
+    assert ok(p) == -1 and ok(q) == -1 and ok(q, _lib.GEMM_Q_KN) == -1
+    assert ok(ctypes.c_void_p(0x100000 + 2 * 64 * 256 - 16), _lib.GEMM_Q_KN) == -1  # last Q bytes
 
 
 def test_muon_matrix_flags_are_validated():
