@@ -53,7 +53,7 @@ constexpr int kUnroll = MORPH_ADAMW_UNROLL;
 constexpr bool kNT = MORPH_ADAMW_NT != 0;
 constexpr bool kGradNT = MORPH_ADAMW_GRAD_NT != 0;
 constexpr int kPerBlock = kBlock * 4 * kUnroll;
-constexpr int kMaxTensors = 24;
+constexpr int kMaxTensors = 48;
 constexpr int kMaxHp = 8;
 // A tensor is cut into segments of at most this many elements so block
 // counts stay far inside the 32-bit grid limits.
@@ -80,6 +80,7 @@ struct LaunchArgs {
   const morph_step_state* state;    // device form only
   int32_t count;
 };
+static_assert(sizeof(LaunchArgs) + 64 <= kMaxKernargBytes, "launch table fits the kernel arguments");
 
 // Power of two (normal double): zero fraction field, finite, positive.
 __device__ __forceinline__ bool pow2_double(double x) {
@@ -215,9 +216,7 @@ __global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const LaunchArgs a,
     if (skip != nullptr && *skip != 0u) return;
   }
   const int b = blockIdx.x;
-  int ti = 0;
-  while (ti + 1 < a.count && a.t[ti + 1].first_block <= b) ++ti;
-  const TensorArg& T = a.t[ti];
+  const TensorArg& T = a.t[segment_of(a.t, a.count, b)];
   morph_adamw_hp hp = a.hp[T.hp];
   if constexpr (kDev) {
     // Step-dependent constants from device state, in the host's double arithmetic.

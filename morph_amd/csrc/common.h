@@ -88,6 +88,23 @@ __device__ __forceinline__ bool nonfinite_bf16x2(uint32_t x) {
   return ((x & 0x7F80u) == 0x7F80u) | ((x & 0x7F800000u) == 0x7F800000u);
 }
 
+// Multi-tensor launches: segment i owns blocks [t[i].first_block,
+// t[i + 1].first_block).  The segment of block b, by binary search over the
+// kernel-argument table (first_block ascending, t[0].first_block == 0).
+template <typename Seg>
+__device__ __forceinline__ int segment_of(const Seg* t, int count, int b) {
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t[mid].first_block <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Kernel arguments travel in the 4 KiB kernel-argument segment.
+constexpr size_t kMaxKernargBytes = 4096;
+
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline int launch_status() {

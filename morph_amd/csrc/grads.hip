@@ -49,6 +49,7 @@ struct LaunchArgs {
   float scale, inv_scale;
   int64_t partial_base;  // index of this launch's first partial
 };
+static_assert(sizeof(LaunchArgs) + 64 <= kMaxKernargBytes, "launch table fits the kernel arguments");
 
 template <typename GT>
 __device__ __forceinline__ void load8(const void* g, int64_t e, float (&x)[8]) {
@@ -95,9 +96,7 @@ __global__ __launch_bounds__(kBlock) void accumulate_kernel(const LaunchArgs a,
                                                             double* __restrict__ partials) {
   __shared__ double lds[kBlock / 64];
   const int b = blockIdx.x;
-  int ti = 0;
-  while (ti + 1 < a.count && a.t[ti + 1].first_block <= b) ++ti;
-  const TensorArg& T = a.t[ti];
+  const TensorArg& T = a.t[segment_of(a.t, a.count, b)];
   const int64_t base = (int64_t)(b - T.first_block) * kPerBlock;
   const int tid = threadIdx.x;
   bool bad = false;

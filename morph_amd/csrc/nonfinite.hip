@@ -30,7 +30,7 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kUnroll = MORPH_NONFINITE_UNROLL;
 constexpr int kBytesPerBlock = kBlock * 16 * kUnroll;
-constexpr int kMaxTensors = 64;
+constexpr int kMaxTensors = 160;
 constexpr int64_t kMaxSegmentBytes = int64_t(1) << 32;
 
 struct TensorArg {
@@ -44,6 +44,7 @@ struct LaunchArgs {
   TensorArg t[kMaxTensors];
   int32_t count;
 };
+static_assert(sizeof(LaunchArgs) + 64 <= kMaxKernargBytes, "launch table fits the kernel arguments");
 
 template <typename GT>
 __device__ __forceinline__ bool word_nonfinite(uint32_t x) {
@@ -66,9 +67,7 @@ __global__ __launch_bounds__(kBlock) void nonfinite_kernel(const LaunchArgs a,
   constexpr int kElemBytes = Fmt<GT>::bytes;
   constexpr int kPerBlock = kBytesPerBlock / kElemBytes;
   const int b = blockIdx.x;
-  int ti = 0;
-  while (ti + 1 < a.count && a.t[ti + 1].first_block <= b) ++ti;
-  const TensorArg& T = a.t[ti];
+  const TensorArg& T = a.t[segment_of(a.t, a.count, b)];
   const int64_t base = (int64_t)(b - T.first_block) * kPerBlock;
   bool bad = false;
   if (T.vector_ok && base + kPerBlock <= T.n) {

@@ -75,7 +75,9 @@ def test_random_poison_matches_oracle():
 
 def test_many_tensors_beyond_one_launch():
     """More tensors than one launch descriptor holds; the poison is in the last one."""
-    grads = [torch.ones(17 + i, dtype=torch.float16) for i in range(150)]
+    grads = [torch.ones(17 + i, dtype=torch.float16) for i in range(400)]
     assert not detect(grads)
-    grads[-1][-1] = float("inf")
-    assert detect(grads)
+    for k in (0, 159, 160, 399):  # first, last of a launch, first of the next, last
+        h = [g.clone() for g in grads]
+        h[k][-1] = float("inf")
+        assert detect(h), k
