@@ -332,6 +332,9 @@ typedef struct morph_muon_matrix {
   float* param;    /* FP32 master, updated in place (the output of morph_muon_orthogonalize) */
   int32_t transposed; /* 0 or 1 */
   int32_t reserved;   /* 0 */
+  /* NULL, or a separate buffer of the momentum's shape: the updated momentum
+   * is written there and `momentum` is only read (see morph_muon_prepare) */
+  float* momentum_out;
 } morph_muon_matrix;
 
 /*
@@ -384,13 +387,19 @@ int morph_muon_orthogonalize(const morph_muon_matrix* mats, int count, int64_t r
  * The three phases morph_muon_step / morph_muon_orthogonalize run, for callers
  * that interleave other work or time the Newton-Schulz GEMM chain on its own:
  * prepare (momentum + Nesterov, or u = grad when orthogonalize_only; norm;
- * bf16 X and X^T into the workspace), newton_schulz (hp->ns_steps iterations,
- * 3 GEMMs each, on the workspace only), finish (master update, or U into
- * param when orthogonalize_only).  Same arguments and workspace throughout.
+ * bf16 X into the workspace), newton_schulz (hp->ns_steps iterations, 3 GEMMs
+ * each, on the workspace only), finish (master update, or U into param when
+ * orthogonalize_only).  Same arguments and workspace throughout.
+ * prepare with d_found_inf != NULL also tests every gradient for +-inf/NaN
+ * in the same pass and stores 1 there if one is found (the gate of
+ * optimizer.py:49-51); with each matrix's momentum_out set it then mutates
+ * nothing the caller keeps, so the caller can read the flag and drop the
+ * step before newton_schulz and finish (the updated momentum is in
+ * momentum_out: swap the buffers after finish).
  */
 int morph_muon_prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
                        const morph_muon_hp* hp, int orthogonalize_only, void* workspace,
-                       size_t workspace_bytes, void* stream);
+                       size_t workspace_bytes, uint32_t* d_found_inf, void* stream);
 int morph_muon_newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp,
                              void* workspace, size_t workspace_bytes, void* stream);
 int morph_muon_finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,

@@ -80,7 +80,7 @@ class MuonMatrix(ctypes.Structure):
     """morph_muon_matrix."""
     _fields_ = [("grad", ctypes.c_void_p), ("momentum", ctypes.c_void_p),
                 ("param", ctypes.c_void_p), ("transposed", ctypes.c_int32),
-                ("reserved", ctypes.c_int32)]
+                ("reserved", ctypes.c_int32), ("momentum_out", ctypes.c_void_p)]
 
 
 class MuonHP(ctypes.Structure):
@@ -132,7 +132,7 @@ def lib():
             "morph_muon_orthogonalize": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
                                           ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
             "morph_muon_prepare": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
-                                    ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp], i32),
+                                    ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp, vp], i32),
             "morph_muon_newton_schulz": ([i32, i64, i64, ctypes.POINTER(MuonHP), vp,
                                           ctypes.c_size_t, vp], i32),
             "morph_muon_finish": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,

@@ -39,7 +39,8 @@ constexpr int64_t kRowPad = 64;                 // bf16 elements appended to eve
 
 struct MatPtrs {
   const float* grad[kMaxMats];
-  float* mom[kMaxMats];
+  const float* mom[kMaxMats];
+  float* mom_out[kMaxMats];  // the updated momentum (== mom when updated in place)
   float* param[kMaxMats];
   int32_t transposed[kMaxMats];  // stored [cols, rows] instead of [rows, cols]
 };
@@ -100,7 +101,11 @@ __device__ __forceinline__ double block_sum(double x, double* lds) {
 // 128-bit access when the matrix's buffers are 16-byte aligned (one
 // contiguous 4 KiB segment per wave access), else one element per access.
 // Every stream is touched once here (u is re-read only after the whole
-// batch, gigabytes later), so the accesses are non-temporal.
+// batch, gigabytes later), so the accesses are non-temporal.  With a flag
+// the gradients are also tested for +-inf/NaN (the gate of
+// optimizer.py:49-51) in the same pass: a wave with a non-finite element
+// stores 1; the caller then discards this pass's outputs (u, and a
+// momentum written to a separate buffer) without anything being mutated.
 template <bool kMomentum>
 __device__ __forceinline__ void momentum_one(float gi, float& m, float& ui, float mom_w,
                                              float nest_w, bool large_m, bool large_n) {
@@ -115,22 +120,28 @@ template <bool kMomentum>
 __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u_all,
                                                           double* part_all, int64_t numel,
                                                           int64_t blocks, float mom_w,
-                                                          float nest_w) {
+                                                          float nest_w, uint32_t* found_inf) {
   __shared__ double lds[kBlock / 64];
   const int mat = blockIdx.y;
   const float* g = mats.grad[mat];
-  float* mom = mats.mom[mat];
+  const float* mom = mats.mom[mat];
+  float* mom_out = mats.mom_out[mat];
   float* u = u_all + (int64_t)mat * numel;
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
   const bool large_m = mom_w >= 0.5f, large_n = nest_w >= 0.5f;
-  const bool vec = ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(mom)) & 15) == 0 &&
+  const bool vec = ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(mom) |
+                     reinterpret_cast<uintptr_t>(mom_out)) & 15) == 0 &&
                    base + kElemsPerBlock <= numel;  // u is 256-byte aligned, numel * 4 per matrix
   double ss = 0.0;
+  bool bad = false;
   if (vec && (numel & 3) == 0) {
 #pragma unroll
     for (int k = 0; k < kElemsPerBlock / (4 * kBlock); ++k) {
       const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
       const f32x4 gv = load_stream<true>(reinterpret_cast<const f32x4*>(g + i));
+      const u32x4 gb = __builtin_bit_cast(u32x4, gv);
+      bad |= nonfinite_f32_bits(gb.x) | nonfinite_f32_bits(gb.y) | nonfinite_f32_bits(gb.z) |
+             nonfinite_f32_bits(gb.w);
       f32x4 mv = f32x4{0.f, 0.f, 0.f, 0.f}, uv;
       if constexpr (kMomentum) mv = load_stream<true>(reinterpret_cast<const f32x4*>(mom + i));
 #pragma unroll
@@ -141,18 +152,21 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u
         uv[e] = ui;
         ss += (double)ui * (double)ui;
       }
-      if constexpr (kMomentum) store_stream<true>(reinterpret_cast<f32x4*>(mom + i), mv);
+      if constexpr (kMomentum) store_stream<true>(reinterpret_cast<f32x4*>(mom_out + i), mv);
       store_stream<true>(reinterpret_cast<f32x4*>(u + i), uv);
     }
   } else {
     for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
       float m = kMomentum ? mom[i] : 0.f, ui;
+      bad |= nonfinite_f32_bits(__builtin_bit_cast(uint32_t, g[i]));
       momentum_one<kMomentum>(g[i], m, ui, mom_w, nest_w, large_m, large_n);
-      if constexpr (kMomentum) mom[i] = m;
+      if constexpr (kMomentum) mom_out[i] = m;
       u[i] = ui;
       ss += (double)ui * (double)ui;
     }
   }
+  if (found_inf != nullptr && __any(bad) && (threadIdx.x & 63) == 0)
+    *reinterpret_cast<volatile uint32_t*>(found_inf) = 1u;
   const double s = block_sum(ss, lds);
   if (threadIdx.x == 0) part_all[(int64_t)mat * blocks + blockIdx.x] = s;
 }
@@ -390,6 +404,7 @@ MatPtrs pointers(const morph_muon_matrix* mats, int count) {
   for (int i = 0; i < count; ++i) {
     m.grad[i] = mats[i].grad;
     m.mom[i] = mats[i].momentum;
+    m.mom_out[i] = mats[i].momentum_out != nullptr ? mats[i].momentum_out : mats[i].momentum;
     m.param[i] = mats[i].param;
     m.transposed[i] = mats[i].transposed;
   }
@@ -398,7 +413,7 @@ MatPtrs pointers(const morph_muon_matrix* mats, int count) {
 
 int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
             const morph_muon_hp* hp, void* workspace, size_t workspace_bytes, bool orth_only,
-            void* stream) {
+            uint32_t* found_inf, void* stream) {
   Bufs W;
   int rc = setup(mats, count, rows, cols, hp, workspace, workspace_bytes, true, !orth_only, &W);
   if (rc || count == 0) return rc;
@@ -408,10 +423,10 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
   const dim3 ew((unsigned)L.blocks, count);
   if (orth_only)
     hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.u, W.part, L.numel,
-                       L.blocks, hp->momentum_weight, hp->nesterov_weight);
+                       L.blocks, hp->momentum_weight, hp->nesterov_weight, found_inf);
   else
     hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.u, W.part, L.numel,
-                       L.blocks, hp->momentum_weight, hp->nesterov_weight);
+                       L.blocks, hp->momentum_weight, hp->nesterov_weight, found_inf);
   if ((rc = launch_status())) return rc;
   hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, W.part, W.den, L.blocks);
   if ((rc = launch_status())) return rc;
@@ -474,9 +489,10 @@ int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
 
 extern "C" int morph_muon_prepare(const morph_muon_matrix* mats, int count, int64_t rows,
                                   int64_t cols, const morph_muon_hp* hp, int orthogonalize_only,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
+                                  void* workspace, size_t workspace_bytes, uint32_t* d_found_inf,
+                                  void* stream) {
   return prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, orthogonalize_only != 0,
-                 stream);
+                 d_found_inf, stream);
 }
 
 extern "C" int morph_muon_newton_schulz(int count, int64_t rows, int64_t cols,
@@ -495,7 +511,7 @@ extern "C" int morph_muon_finish(const morph_muon_matrix* mats, int count, int64
 extern "C" int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t rows,
                                int64_t cols, const morph_muon_hp* hp, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  int rc = prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
+  int rc = prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, false, nullptr, stream);
   if (!rc) rc = newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream);
   if (!rc) rc = finish(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
   return rc;
@@ -504,7 +520,7 @@ extern "C" int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t
 extern "C" int morph_muon_orthogonalize(const morph_muon_matrix* mats, int count, int64_t rows,
                                         int64_t cols, const morph_muon_hp* hp, void* workspace,
                                         size_t workspace_bytes, void* stream) {
-  int rc = prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, true, stream);
+  int rc = prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, true, nullptr, stream);
   if (!rc) rc = newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream);
   if (!rc) rc = finish(mats, count, rows, cols, hp, workspace, workspace_bytes, true, stream);
   return rc;

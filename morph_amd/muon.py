@@ -65,13 +65,13 @@ def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, symmetric=F
 
 
 class _Workspaces:
-    """Zero-filled device workspaces, one per (shape, count, device), kept for reuse."""
+    """Zero-filled device workspaces, one per (shape, count, device, batch index), kept for reuse."""
 
     def __init__(self):
         self._ws = {}
 
-    def get(self, rows, cols, count, device):
-        key = (rows, cols, count, device)
+    def get(self, rows, cols, count, device, index=0):
+        key = (rows, cols, count, device, index)
         if key not in self._ws:
             nbytes = lib().morph_muon_workspace_bytes(rows, cols, count)
             if nbytes == 0:
@@ -112,34 +112,52 @@ def ns_flops(rows, cols, count, steps=NS_STEPS):
     return count * steps * (4 * m * m * n + 2 * m ** 3)
 
 
-def _run(mats, rows, cols, hp, orth_only, stream, workspaces, timer=None):
-    """prepare -> Newton-Schulz -> finish for up to 64 matrices per batch.
+def _prepare(mats, rows, cols, hp, orth_only, stream, workspaces, found_inf=None, first=0):
+    """Enqueue prepare for up to 64 matrices per batch; returns the batches for _complete.
 
-    mats: [((param, grad, momentum), transposed)], each stored [rows, cols], or
-    [cols, rows] when transposed.  timer: optional list; (start_event,
-    end_event, flops) around each NS chain.
+    mats: [((param, grad, momentum, momentum_out), transposed)], each stored
+    [rows, cols], or [cols, rows] when transposed.  found_inf: optional device
+    flag that prepare sets when a gradient is non-finite.  first: index of the
+    first batch (each batch of one step gets its own workspace).
     """
     L = lib()
-    for start in range(0, len(mats), 64):
+    batches = []
+    for k, start in enumerate(range(0, len(mats), 64)):
         chunk = mats[start:start + 64]
-        ws = workspaces.get(rows, cols, len(chunk), chunk[0][0][0].device)
+        ws = workspaces.get(rows, cols, len(chunk), chunk[0][0][0].device, first + k)
         arr = (MuonMatrix * len(chunk))()
-        for i, ((p, g, m), transposed) in enumerate(chunk):
+        for i, ((p, g, m, m_out), transposed) in enumerate(chunk):
             arr[i].grad, arr[i].param = g.data_ptr(), p.data_ptr()
             arr[i].momentum = m.data_ptr() if m is not None else None
+            arr[i].momentum_out = m_out.data_ptr() if m_out is not None else None
             arr[i].transposed = transposed
-        args = (ctypes.byref(hp),)
-        wsp, wsn, sh = ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream_handle(stream)
-        check(L.morph_muon_prepare(arr, len(chunk), rows, cols, *args, int(orth_only), wsp, wsn, sh))
+        flag = ctypes.c_void_p(found_inf.data_ptr()) if found_inf is not None else None
+        check(L.morph_muon_prepare(arr, len(chunk), rows, cols, ctypes.byref(hp), int(orth_only),
+                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), flag,
+                                   stream_handle(stream)))
+        batches.append((arr, len(chunk), rows, cols, hp, orth_only, ws))
+    return batches
+
+
+def _complete(batches, stream, timer=None):
+    """Newton-Schulz chain and finish for the batches _prepare enqueued.
+
+    timer: optional list; (start_event, end_event, flops) around each NS chain.
+    """
+    L = lib()
+    sh = stream_handle(stream)
+    for arr, count, rows, cols, hp, orth_only, ws in batches:
+        wsp, wsn = ctypes.c_void_p(ws.data_ptr()), ws.numel()
         if timer is not None:
             s = stream or torch.cuda.current_stream()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-        check(L.morph_muon_newton_schulz(len(chunk), rows, cols, *args, wsp, wsn, sh))
+        check(L.morph_muon_newton_schulz(count, rows, cols, ctypes.byref(hp), wsp, wsn, sh))
         if timer is not None:
             e1.record(s)
-            timer.append((e0, e1, ns_flops(rows, cols, len(chunk), hp.ns_steps)))
-        check(L.morph_muon_finish(arr, len(chunk), rows, cols, *args, int(orth_only), wsp, wsn, sh))
+            timer.append((e0, e1, ns_flops(rows, cols, count, hp.ns_steps)))
+        check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), int(orth_only), wsp,
+                                  wsn, sh))
 
 
 def _check_matrix(t, name):
@@ -160,30 +178,48 @@ def orthogonalize(gradients, steps=NS_STEPS, stream=None, workspaces=_WORKSPACES
     for g in gs:
         _check_matrix(g, "gradient")
         outs.append(torch.empty_like(g))
-    items = [(o, g, None) for o, g in zip(outs, gs)]
+    items = [(o, g, None, None) for o, g in zip(outs, gs)]
+    batches = []
     for (rows, cols), group in _by_shape(items).items():
-        _run(group, rows, cols, _hp(steps=steps), True, stream, workspaces)
+        batches += _prepare(group, rows, cols, _hp(steps=steps), True, stream, workspaces,
+                            first=len(batches))
+    _complete(batches, stream)
     return outs[0] if single else outs
 
 
 def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=None,
-              workspaces=_WORKSPACES, timer=None):
+              workspaces=_WORKSPACES, timer=None, momenta_out=None, found_inf=None, gate=None):
     """The Muon loop body of optimizer.py:55-61 for every (param, grad, momentum) triple.
 
     In place on params and momenta.  Scalars follow the reference: decay
     1 - lr * weight_decay, update scale sqrt(max(1, rows / cols)), alpha -lr.
+    momenta_out: optional separate buffers that receive the updated momenta
+    (momenta are then only read).  found_inf: optional device flag set when a
+    gradient is non-finite, tested in the momentum pass.  gate: optional
+    callable run after that pass and before anything the caller keeps is
+    mutated (with momenta_out); it may raise to drop the step.
     """
     items = []
-    for p, g, m in zip(params, grads, momenta):
+    outs = momenta_out if momenta_out is not None else [None] * len(params)
+    for p, g, m, mo in zip(params, grads, momenta, outs):
         for t, name in ((p, "param"), (g, "grad"), (m, "momentum")):
             _check_matrix(t, name)
         if not (p.shape == g.shape == m.shape):
             raise ValueError("param, grad and momentum shapes differ")
-        items.append((p, g, m))
+        if mo is not None:
+            _check_matrix(mo, "momentum_out")
+            if mo.shape != m.shape or mo.data_ptr() == m.data_ptr():
+                raise ValueError("momentum_out must be a separate buffer of the momentum's shape")
+        items.append((p, g, m, mo))
+    batches = []
     for (rows, cols), group in _by_shape(items).items():
         hp = _hp(update_scale=max(1, rows / cols) ** .5, decay=1 - lr * weight_decay,
                  neg_lr=-lr, steps=steps, update_scale_transposed=max(1, cols / rows) ** .5)
-        _run(group, rows, cols, hp, False, stream, workspaces, timer)
+        batches += _prepare(group, rows, cols, hp, False, stream, workspaces, found_inf,
+                            first=len(batches))
+    if gate is not None:
+        gate()
+    _complete(batches, stream, timer)
 
 
 def partition(model):
@@ -212,6 +248,9 @@ class HybridMuonAdamW:
         self.lr = lr if muon_lr is None else muon_lr
         self.weight_decay = weight_decay
         self.momentum = {}
+        # the momentum pass writes into these and they swap with `momentum`
+        # once the non-finite gate has passed, so a raise mutates nothing
+        self._momentum_next = {}
         self.adam = FusedAdamW(adam, lr=lr, weight_decay=weight_decay, betas=(.9, .95),
                                sync=True) if adam else None
         self._flag = None
@@ -222,38 +261,54 @@ class HybridMuonAdamW:
         if self.adam is not None:
             self.adam.zero_grad(set_to_none=set_to_none)
 
-    def _all_params(self):
-        adam = [p for g in self.adam.param_groups for p in g["params"]] if self.adam else []
-        return self.muon + adam
-
     @torch.no_grad()
     def step(self):
-        grads = [p.grad for p in self._all_params() if p.grad is not None]
-        if grads:
-            if self._flag is None:
-                self._flag = kernels.new_flag(grads[0].device)
-            kernels.flag_clear(self._flag)
-            kernels.nonfinite_or(grads, self._flag)
+        """The gate of optimizer.py:49-51 covers every gradient: the AdamW group's
+        by the detector, the Muon matrices' inside their momentum pass (which
+        writes only scratch buffers until the gate has passed)."""
+        live = [(i, p) for i, p in enumerate(self.muon) if p.grad is not None]
+        adam_grads = [p.grad for g in (self.adam.param_groups if self.adam else [])
+                      for p in g["params"] if p.grad is not None]
+        if not live and not adam_grads:
+            return
+        if self._flag is None:
+            self._flag = kernels.new_flag((live[0][1] if live else adam_grads[0]).device)
+        kernels.flag_clear(self._flag)
+        if adam_grads:
+            kernels.nonfinite_or(adam_grads, self._flag)
+
+        def gate():
             if self._flag.item():
                 raise FloatingPointError('nonfinite gradient; optimizer not updated')
-        live = [(i, p) for i, p in enumerate(self.muon) if p.grad is not None]
-        for i, p in live:
-            if i not in self.momentum:
-                self.momentum[i] = torch.zeros_like(p)
+
         if live:
+            for i, p in live:
+                if i not in self.momentum:
+                    self.momentum[i] = torch.zeros_like(p)
+                if i not in self._momentum_next:
+                    self._momentum_next[i] = torch.empty_like(p)
             muon_step([p for _, p in live], [p.grad for _, p in live],
                       [self.momentum[i] for i, _ in live], self.lr, self.weight_decay,
-                      timer=self.ns_timer)
+                      timer=self.ns_timer, momenta_out=[self._momentum_next[i] for i, _ in live],
+                      found_inf=self._flag, gate=gate)
+            for i, _ in live:
+                self.momentum[i], self._momentum_next[i] = self._momentum_next[i], self.momentum[i]
+        else:
+            gate()
         if self.adam is not None:
             self.adam.step()
 
     def state_dict(self):
+        """{momentum, adam, lr, weight_decay} as optimizer.py:64-65.  The momentum
+        tensors are the current ones; a later step writes its update into a
+        second buffer and swaps, so they are not updated in place afterwards."""
         return dict(momentum=self.momentum,
                     adam=self.adam.state_dict() if self.adam else None,
                     lr=self.lr, weight_decay=self.weight_decay)
 
     def load_state_dict(self, state):
         self.momentum = {i: value.to(self.muon[i].device) for i, value in state['momentum'].items()}
+        self._momentum_next = {}
         if self.adam is not None:
             self.adam.load_state_dict(state['adam'])
         self.lr, self.weight_decay = state['lr'], state['weight_decay']

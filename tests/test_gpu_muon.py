@@ -223,19 +223,38 @@ def test_hybrid_partition_and_adam_group_match_torch():
         assert (p.detach().cpu() - q.detach()).abs().max() <= 1e-6 * q.detach().abs().max()
 
 
-def test_hybrid_nonfinite_raises_before_any_mutation():
-    """optimizer.py:49-51 / tests/test_training.py:22-27."""
+@pytest.mark.parametrize("poisoned,bad", [("norm.weight", float("nan")),
+                                          ("up.weight", float("inf")),
+                                          ("down.weight", float("nan"))])
+def test_hybrid_nonfinite_raises_before_any_mutation(poisoned, bad):
+    """optimizer.py:49-51 / tests/test_training.py:22-27: an AdamW-group gradient (caught by
+    the detector) or a Muon gradient (caught in the momentum pass) raises with parameters,
+    momenta and AdamW state untouched; the next finite step then equals the step of an
+    optimizer that never saw the poisoned one."""
+    torch.manual_seed(1)
     gpu = Tiny().to(DEV)
-    opt = muon.HybridMuonAdamW(gpu, lr=.003)
-    _grads(gpu, 1)
-    opt.step()
+    twin = copy.deepcopy(gpu)
+    opt, opt2 = muon.HybridMuonAdamW(gpu, lr=.003), muon.HybridMuonAdamW(twin, lr=.003)
+    for o, m in ((opt, gpu), (opt2, twin)):
+        _grads(m, 1)
+        o.step()
     before = copy.deepcopy(gpu.state_dict())
+    mom = {i: t.clone() for i, t in opt.momentum.items()}
     _grads(gpu, 2)
-    gpu.norm.weight.grad.fill_(float("nan"))
+    dict(gpu.named_parameters())[poisoned].grad.view(-1)[5] = bad
     with pytest.raises(FloatingPointError):
         opt.step()
     for k, v in gpu.state_dict().items():
         assert torch.equal(v, before[k]), k
+    for i, t in opt.momentum.items():
+        assert torch.equal(t, mom[i]), i
+    for o, m in ((opt, gpu), (opt2, twin)):
+        _grads(m, 3)
+        o.step()
+    for (k, v), (k2, v2) in zip(gpu.state_dict().items(), twin.state_dict().items()):
+        assert torch.equal(v, v2), k
+    for i in opt.momentum:
+        assert torch.equal(opt.momentum[i], opt2.momentum[i]), i
 
 
 def test_hybrid_muon_diagonal_matches_scalar_newton_schulz():
