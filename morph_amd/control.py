@@ -71,6 +71,11 @@ class StepControl:
     def found_inf_ptr(self):
         return self.state.data_ptr() + FOUND_INF_OFFSET
 
+    @property
+    def found_inf_view(self):
+        """found_inf as a 1-element int32 view of the state block."""
+        return self.state[FOUND_INF_OFFSET:FOUND_INF_OFFSET + 4].view(torch.int32)
+
     def _scale_fields(self):
         s = self.loss_scale
         if isinstance(s, DynamicLossScale) or (hasattr(s, "overflow") and hasattr(s, "success")):

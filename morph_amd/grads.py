@@ -103,11 +103,14 @@ class StageGradients:
             self.seen[i] = True
         return arr, dtype_code(dtype if dtype is not None else torch.float32), keep
 
-    def accumulate(self, grads, loss_scale=1.0, final=False, stream=None):
+    def accumulate(self, grads, loss_scale=1.0, final=False, stream=None, found_inf=None):
         """views[i] += float(grads[i]) / loss_scale for every non-None gradient.
 
         final=True also computes the window's non-finite flag and FP64 sum of
-        squares (read with found_inf() / norm_squared()).
+        squares (read with found_inf() / norm_squared()).  found_inf: a device
+        int32 flag to receive that flag instead of the window's own, e.g. a
+        FusedAdamW's `found_inf`, whose step(..., checked=True) then needs no
+        detector pass.
         """
         if self._finalized:
             raise RuntimeError("window already finalized; call zero_() to start again")
@@ -119,10 +122,18 @@ class StageGradients:
         if final and (self._partials is None or self._partials.numel() < max(n_part, 1)):
             self._partials = torch.empty(max(n_part, 1), dtype=torch.float64, device=self.device)
         if final:
-            kernels.flag_clear(self._flag, stream)  # on the same stream as the pass
+            if found_inf is not None:
+                kernels.require_device_tensor(found_inf, "found_inf")
+                if found_inf.dtype != torch.int32 or found_inf.numel() < 1:
+                    raise TypeError("found_inf must be a device int32 flag")
+                self._flag_target = found_inf
+            else:
+                self._flag_target = self._flag
+            kernels.flag_clear(self._flag_target, stream)  # on the same stream as the pass
         sh = stream_handle(stream)
+        flag = (self._flag_target if final else self._flag)
         check(L.morph_grad_accumulate(arr, len(self.views), code, float(loss_scale), flags,
-                                      _ptr(self._flag), _ptr(self._partials),
+                                      _ptr(flag), _ptr(self._partials),
                                       self._partials.numel() if self._partials is not None else 0, sh))
         if final:
             check(L.morph_sumsq_total(_ptr(self._partials), n_part, _ptr(self._sumsq), 0, sh))
@@ -133,7 +144,7 @@ class StageGradients:
     def found_inf(self):
         """True when the finished window holds an inf or NaN (synchronizes)."""
         self._require_final()
-        return bool(self._flag.item())
+        return bool(self._flag_target.item())
 
     def norm_squared(self):
         """FP64 sum of squares of the finished window (synchronizes)."""

@@ -99,6 +99,14 @@ class FusedAdamW:
     def loss_scale(self):
         return self._ctl.loss_scale
 
+    @property
+    def found_inf(self):
+        """The step's non-finite flag in the device step state, as a 1-element int32
+        tensor.  A producer that already tests every gradient (the final pass of
+        StageGradients.accumulate(..., found_inf=opt.found_inf)) can set it and
+        call step(..., checked=True), which then skips the detector pass."""
+        return self._ctl.found_inf_view
+
     # -- helpers -----------------------------------------------------------
     def _flat(self):
         return [(gi, p) for gi, group in enumerate(self.param_groups) for p in group["params"]]
@@ -163,11 +171,14 @@ class FusedAdamW:
 
     # -- the step ----------------------------------------------------------
     @torch.no_grad()
-    def step(self, grads=None, stream=None):
+    def step(self, grads=None, stream=None, checked=False):
         """Enqueue one optimizer step (detector, fused AdamW, step close).
 
         grads: one tensor (or None) per parameter in param-group order; by
-        default p.grad.  Returns None, or with sync the applied/skipped outcome.
+        default p.grad.  checked=True: every gradient's non-finite test is
+        already in `found_inf` (set on this stream since the last step), so
+        the detector pass is skipped.  Returns None, or with sync the
+        applied/skipped outcome.
         """
         flat = self._flat()
         if grads is None:
@@ -183,7 +194,8 @@ class FusedAdamW:
             self._ctl.push_scale()
         batch, clock_list, hps, scheds = self._prepare(grads, present)
         ctl = self._ctl
-        kernels.nonfinite_or([grads[i] for i in present], ctl.found_inf_ptr, stream)
+        if not checked:
+            kernels.nonfinite_or([grads[i] for i in present], ctl.found_inf_ptr, stream)
         if self.kernel_timer is not None:
             s = stream or torch.cuda.current_stream()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

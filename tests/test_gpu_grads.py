@@ -149,3 +149,40 @@ def test_clip_coefficient_matches_reference_expression():
     for n2 in (0.0, 0.25, 1.0, 4.0, 1e6):
         norm = math.sqrt(n2)
         assert G.clip_coefficient(n2, 1.0) == min(1., 1.0 / (norm + 1e-6))
+
+
+@pytest.mark.parametrize("poison", [False, True])
+def test_window_flag_into_the_optimizer_replaces_the_detector(poison):
+    """The final accumulate pass writes its non-finite flag into FusedAdamW's step state
+    and step(..., checked=True) skips the detector: the same masters, moments, exports,
+    skip decision and loss scale as the ordinary step on the same window."""
+    from morph_amd import DynamicLossScale, FusedAdamW
+    shapes = [(300, 200), (4097,), (64, 64)]
+    gen = torch.Generator().manual_seed(11)
+    masters = [torch.randn(s, generator=gen) * .02 for s in shapes]
+    micro = [[(torch.randn(s, generator=gen) * 1e-4 * 1024).half() for s in shapes]
+             for _ in range(3)]
+    if poison:
+        micro[1][1][17] = float("inf")
+    results = []
+    for checked in (False, True):
+        opt = FusedAdamW([m.to(DEV) for m in masters], lr=3e-4, betas=(.9, .95),
+                         weight_decay=.1, loss_scale=DynamicLossScale(1024., 2000),
+                         export_dtype=torch.float16, sync=True)
+        window = G.StageGradients(shapes, DEV).zero_()
+        for k, grads in enumerate(micro):
+            window.accumulate([g.to(DEV) for g in grads], 1.0, final=(k == 2),
+                              found_inf=opt.found_inf if checked else None)
+        assert window.found_inf() == poison
+        applied = opt.step(window.views, checked=checked)
+        assert applied == (not poison)
+        results.append(opt)
+    a, b = results
+    assert a.loss_scale.scale == b.loss_scale.scale == (512. if poison else 1024.)
+    for p, q in zip([p for g in a.param_groups for p in g["params"]],
+                    [p for g in b.param_groups for p in g["params"]]):
+        assert torch.equal(p, q)
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(a.state[p][key], b.state[q][key])
+    for x, y in zip(a.exports, b.exports):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
