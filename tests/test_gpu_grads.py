@@ -186,3 +186,39 @@ def test_window_flag_into_the_optimizer_replaces_the_detector(poison):
             assert torch.equal(a.state[p][key], b.state[q][key])
     for x, y in zip(a.exports, b.exports):
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+
+
+def test_tied_embedding_sum_through_the_windows():
+    """disk.py:455-462 / sparse_disk.py:126-130: the head stage holds its embedding gradient,
+    stage 0 adds it (one FP32 add) before the update; the norm counts the sum once.  Here the
+    head stage accumulates into its own window and stage 0's final pass takes that FP32 view
+    with scale 1 (x * 1 is exact, so the add is the reference's): views bit-exact, norm over
+    stage 0 only."""
+    gen = torch.Generator().manual_seed(13)
+    emb, other = (96, 64), (64, 128)
+    scale = 1024.0
+    head_micro = [(torch.randn(emb, generator=gen) * 1e-3 * scale).half() for _ in range(2)]
+    stage0_micro = [[(torch.randn(s, generator=gen) * 1e-3 * scale).half() for s in (emb, other)]
+                    for _ in range(3)]
+    tied = G.StageGradients([emb], DEV).zero_()
+    for k, g in enumerate(head_micro):
+        tied.accumulate([g.to(DEV)], scale, final=(k == 1))
+    window = G.StageGradients([emb, other], DEV).zero_()
+    for grads in stage0_micro:
+        window.accumulate([g.to(DEV) for g in grads], scale)
+    window.accumulate([tied.views[0], None], 1.0, final=True)
+    # the reference's ops on the CPU
+    held = torch.zeros(emb)
+    for g in head_micro:
+        held.add_(g.float() / scale)
+    ref = [torch.zeros(emb), torch.zeros(other)]
+    for grads in stage0_micro:
+        for d, g in zip(ref, grads):
+            d.add_(g.float() / scale)
+    ref[0].add_(held)
+    for got, exp in zip(window.views, ref):
+        assert torch.equal(got.cpu().view(torch.int32), exp.view(torch.int32))
+    ref_norm = sum(float(piece.double().square().sum()) for t in ref
+                   for piece in t.flatten().split(1048576))
+    assert abs(window.norm_squared() - ref_norm) <= 1e-12 * ref_norm
+    assert not window.found_inf()
