@@ -62,6 +62,10 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
     compute = torch.cuda.current_stream(device)
     copy_in = torch.cuda.Stream(device)
     slots = [_Staging(chunk, device) for _ in range(2)]
+    # The staging tensors come from the caching allocator on the compute stream, which may hand
+    # out memory whose last reader is still queued there, and a device gradient may still be in
+    # production on it: the copy stream starts after everything queued so far.
+    copy_in.wait_stream(compute)
     starts = list(range(0, size, chunk_elements))
 
     def stage_in(k):

@@ -95,6 +95,8 @@ class ResidentWindow:
         for name in (self.names if names is None else names):
             size = int(self.store.entries[name]["size"])
             dev = torch.empty((3, size), dtype=torch.float32, device=self.device)
+            # allocated on the compute stream, which may still have work queued on this memory
+            self._copy.wait_stream(compute)
             fd = os.open(self._path(name), os.O_RDONLY)
             try:
                 for k, start in enumerate(range(0, size, self.chunk)):
