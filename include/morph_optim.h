@@ -386,10 +386,13 @@ int morph_muon_orthogonalize(const morph_muon_matrix* mats, int count, int64_t r
 /*
  * The three phases morph_muon_step / morph_muon_orthogonalize run, for callers
  * that interleave other work or time the Newton-Schulz GEMM chain on its own:
- * prepare (momentum + Nesterov, or u = grad when orthogonalize_only; norm;
- * bf16 X into the workspace), newton_schulz (hp->ns_steps iterations, 3 GEMMs
- * each, on the workspace only), finish (master update, or U into param when
- * orthogonalize_only).  Same arguments and workspace throughout.
+ * prepare (momentum + Nesterov, or u = grad when orthogonalize_only; X0 =
+ * bf16(u) in the Newton-Schulz orientation and den = |u|_F + 1e-7 into the
+ * workspace), newton_schulz (hp->ns_steps iterations, 3 GEMMs each, on the
+ * workspace only; the first iteration's products apply 1 / den), finish
+ * (master update, or U into param when orthogonalize_only).  Same arguments
+ * and workspace throughout (with hp->ns_steps == 0 prepare itself writes
+ * X = bf16(X0 / den), so the phases must see the same hp).
  * prepare with d_found_inf != NULL also tests every gradient for +-inf/NaN
  * in the same pass and stores 1 there if one is found (the gate of
  * optimizer.py:49-51); with each matrix's momentum_out set it then mutates

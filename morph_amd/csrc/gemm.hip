@@ -61,6 +61,7 @@
 // Dimensions must be multiples of the tile (M, N of 256, K of 64): callers pad
 // with zeros, which is exact for Newton-Schulz (zero rows stay zero).
 #include "common.h"
+#include "gemm.h"
 
 namespace morph {
 namespace {
@@ -101,6 +102,7 @@ struct GemmArgs {
   int64_t ldp, ldq, ldd, ldc, ldct;
   int64_t sp, sq, sd, sc, sct;
   float alpha, beta;
+  const float* bscale;       // optional per-matrix factor of alpha and beta (device)
   int32_t tiles_m, tiles_n;
   int32_t tiles_per_matrix;  // tiles_m * tiles_n, or the upper triangle when symmetric
   int32_t flags;             // MORPH_GEMM_SYMMETRIC
@@ -157,9 +159,9 @@ __device__ __forceinline__ void store_tile(const uint16_t* E, uint16_t* dst, uin
 // and the alpha multiply are template parameters so that each variant is
 // straight-line code.
 template <int kDMode, bool kScaled>
-__device__ __forceinline__ void epilogue(const GemmArgs& g, f32x16 (&acc)[4][4],
-                                         uint16_t* smem, const uint16_t* D, uint16_t* C,
-                                         uint16_t* T, int64_t ldt) {
+__device__ __forceinline__ void epilogue(const GemmArgs& g, float alpha, float beta,
+                                         f32x16 (&acc)[4][4], uint16_t* smem, const uint16_t* D,
+                                         uint16_t* C, uint16_t* T, int64_t ldt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
   const int fr = lane & 31, fh = lane >> 5;
@@ -204,8 +206,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, f32x16 (&acc)[4][4],
       float x[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        x[r] = kScaled ? g.alpha * acc[i][j][r] : acc[i][j][r];
-        if (kDMode != kNoD) x[r] = __fmaf_rn(g.beta, dval[r], x[r]);
+        x[r] = kScaled ? alpha * acc[i][j][r] : acc[i][j][r];
+        if (kDMode != kNoD) x[r] = __fmaf_rn(beta, dval[r], x[r]);
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
@@ -514,31 +516,36 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
     ldt = g.ldct;
   }
   uint16_t* C = g.C + b * g.sc + row0 * g.ldc + col0;
+  float alpha = g.alpha, beta = g.beta;
+  if (g.bscale != nullptr) {
+    const float s = g.bscale[b];
+    alpha *= s;
+    beta *= s;
+  }
   // alpha == 1 (A = X X^T, X' = a X + B X) skips the multiply, which is exact then
-  if (g.alpha == 1.0f) {
+  if (alpha == 1.0f) {
     if (D == nullptr)
-      epilogue<kNoD, false>(g, acc, smem, nullptr, C, T, ldt);
+      epilogue<kNoD, false>(g, alpha, beta, acc, smem, nullptr, C, T, ldt);
     else
-      epilogue<kDRowMajor, false>(g, acc, smem, D, C, T, ldt);
+      epilogue<kDRowMajor, false>(g, alpha, beta, acc, smem, D, C, T, ldt);
   } else {
     if (D == nullptr)
-      epilogue<kNoD, true>(g, acc, smem, nullptr, C, T, ldt);
+      epilogue<kNoD, true>(g, alpha, beta, acc, smem, nullptr, C, T, ldt);
     else
-      epilogue<kDRowMajor, true>(g, acc, smem, D, C, T, ldt);
+      epilogue<kDRowMajor, true>(g, alpha, beta, acc, smem, D, C, T, ldt);
   }
 }
 
 }  // namespace
 }  // namespace morph
 
-using namespace morph;
-
-extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D,
-                                  uint16_t* C, uint16_t* Ct, int64_t M, int64_t N, int64_t K,
-                                  int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
-                                  int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
-                                  int64_t stride_d, int64_t stride_c, int64_t stride_ct,
-                                  float alpha, float beta, int flags, void* stream) {
+int morph::gemm_nt_bf16_scaled(const uint16_t* P, const uint16_t* Q, const uint16_t* D,
+                               uint16_t* C, uint16_t* Ct, int64_t M, int64_t N, int64_t K,
+                               int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
+                               int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
+                               int64_t stride_d, int64_t stride_c, int64_t stride_ct,
+                               float alpha, float beta, const float* bscale, int flags,
+                               void* stream) {
   if (P == nullptr || Q == nullptr || C == nullptr || M < 0 || N < 0 || K <= 0 || batch < 0)
     return MORPH_EINVAL;
   auto misaligned = [](const void* p, uintptr_t a) {
@@ -590,7 +597,7 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
   const int64_t grid = (total + 7) / 8 * 8;
   if (per > (int64_t(1) << 31) - 1 || grid > (int64_t(1) << 31) - 1) return MORPH_ERANGE;
   GemmArgs g{P, Q, D, C, Ct, K, ldp, ldq, ldd, ldc, ldct,
-             stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta,
+             stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta, bscale,
              (int32_t)tm, (int32_t)tn, (int32_t)per, flags, total};
   if (qkn)
     hipLaunchKernelGGL(gemm_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0,
@@ -599,4 +606,17 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
     hipLaunchKernelGGL(gemm_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0,
                        as_stream(stream), g);
   return launch_status();
+}
+
+using namespace morph;
+
+extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const uint16_t* D,
+                                  uint16_t* C, uint16_t* Ct, int64_t M, int64_t N, int64_t K,
+                                  int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
+                                  int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
+                                  int64_t stride_d, int64_t stride_c, int64_t stride_ct,
+                                  float alpha, float beta, int flags, void* stream) {
+  return gemm_nt_bf16_scaled(P, Q, D, C, Ct, M, N, K, batch, ldp, ldq, ldd, ldc, ldct, stride_p,
+                             stride_q, stride_d, stride_c, stride_ct, alpha, beta, nullptr, flags,
+                             stream);
 }

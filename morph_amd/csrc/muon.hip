@@ -11,13 +11,16 @@
 //   p = p * decay + (U * scale) * neg_lr        U = X in p's layout           (60-61)
 //
 // The reference computes orthogonalize in FP32; here X, A and B are bf16 (the
-// BASELINE's Newton-Schulz precision) with fp32 accumulation and one rounding
-// per product, so parity with the reference is a tolerance, not bit equality.
-// The elementwise steps round exactly like torch (explicit fmaf where its CPU
-// kernels fuse, plain multiplies elsewhere).
+// precision this path specifies for Newton-Schulz) with fp32 accumulation and
+// one rounding per product, so parity with the reference is a tolerance, not
+// bit equality.  The momentum pass writes X0 = bf16(u) (transposed when
+// rows > cols) and the FP64 sum of u^2; the first iteration's products apply
+// the normalisation per matrix, A = X0 X0^T / den^2 and X' = (a X0 + B X0) /
+// den, so u never goes to memory.  The elementwise steps round exactly like
+// torch (explicit fmaf where its CPU kernels fuse, plain multiplies elsewhere).
 //
 // Workspace (caller-allocated, zero-filled once; morph_muon_workspace_bytes):
-// u fp32 [count][rows*cols]; per-block partial sums f64; denominators f32;
+// per-block partial sums f64; per-matrix 1/den, 1/den^2, den f32;
 // X0/X1 [count][Mp][Np] (iterations alternate: X' = a X + B X reads all of X
 // as its [K, N] operand, so it cannot overwrite it), A and B [count][Mp][Mp],
 // bf16, with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.
@@ -26,7 +29,10 @@
 // Rows are stored kRowPad elements longer than Mp / Np (never read): with
 // rows a multiple of 4 KiB apart, the 256 rows of a GEMM operand tile fall
 // on few L2 channels; the pad spreads them (about 6% on the K = Mp products).
+#include <algorithm>
+
 #include "common.h"
+#include "gemm.h"
 
 namespace morph {
 namespace {
@@ -48,9 +54,12 @@ struct MatPtrs {
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct Layout {
-  int64_t rows, cols, m, n, mp, np, count, numel, blocks;
+  int64_t rows, cols, m, n, mp, np, count, numel;
+  int64_t blocks;  // flat blocks per matrix (momentum_kernel)
+  int64_t tiles;   // 64 x 64 tiles per matrix (momentum_t_kernel, apply_kernel)
+  int64_t parts;   // partial sums per matrix: max(blocks, tiles)
   int64_t ldn, ldm;  // row lengths of X ([Mp][ldn]) and of A, B ([Mp][ldm])
-  size_t off_u, off_part, off_den, off_x0, off_x1, off_a, off_b, total;
+  size_t off_part, off_scale, off_x0, off_x1, off_a, off_b, total;
 };
 
 Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
@@ -66,15 +75,16 @@ Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
   L.ldm = L.mp + kRowPad;
   L.numel = rows * cols;
   L.blocks = (L.numel + kElemsPerBlock - 1) / kElemsPerBlock;
+  L.tiles = ((rows + kTile - 1) / kTile) * ((cols + kTile - 1) / kTile);
+  L.parts = L.blocks > L.tiles ? L.blocks : L.tiles;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t at = off;
     off = (off + bytes + 255) / 256 * 256;
     return at;
   };
-  L.off_u = take((size_t)count * L.numel * 4);
-  L.off_part = take((size_t)count * L.blocks * 8);
-  L.off_den = take((size_t)count * 4);
+  L.off_part = take((size_t)count * L.parts * 8);
+  L.off_scale = take((size_t)count * 3 * 4);
   L.off_x0 = take((size_t)count * L.mp * L.ldn * 2);
   L.off_x1 = take((size_t)count * L.mp * L.ldn * 2);
   L.off_a = take((size_t)count * L.mp * L.ldm * 2);
@@ -95,17 +105,23 @@ __device__ __forceinline__ double block_sum(double x, double* lds) {
   return s;  // valid in thread 0
 }
 
-// momentum + Nesterov blend + partial sums of u^2 (one partial per block).
-// kMomentum = false: u = grad (orthogonalize alone).  A block covers
-// kElemsPerBlock consecutive elements; a lane moves 4 consecutive elements per
-// 128-bit access when the matrix's buffers are 16-byte aligned (one
-// contiguous 4 KiB segment per wave access), else one element per access.
-// Every stream is touched once here (u is re-read only after the whole
-// batch, gigabytes later), so the accesses are non-temporal.  With a flag
-// the gradients are also tested for +-inf/NaN (the gate of
-// optimizer.py:49-51) in the same pass: a wave with a non-finite element
-// stores 1; the caller then discards this pass's outputs (u, and a
-// momentum written to a separate buffer) without anything being mutated.
+// Stored layout of a matrix: [pr, pc] = [rows, cols], or [cols, rows] when
+// transposed.  X is [m, n] with m = min: it has the stored layout when
+// pr <= pc, else it is the transpose.
+__device__ __forceinline__ bool x_is_stored(const MatPtrs& mats, int mat, int64_t rows,
+                                            int64_t cols) {
+  const bool tr = mats.transposed[mat] != 0;
+  return (tr ? cols : rows) <= (tr ? rows : cols);
+}
+
+// Momentum + Nesterov blend, with u = the blend written straight into the
+// Newton-Schulz operand as X0 = bf16(u) (the Frobenius scale 1 / (|u| + 1e-7)
+// is applied by the first iteration's products, so u itself never goes to
+// memory), partial sums of u^2 in FP64 (one per block), and, with a flag,
+// the non-finite test of the gradients (the gate of optimizer.py:49-51): a
+// wave with a non-finite element stores 1; the caller then discards this
+// pass's outputs (X0, and a momentum written to a separate buffer) without
+// anything being mutated.  kMomentum = false: u = grad (orthogonalize alone).
 template <bool kMomentum>
 __device__ __forceinline__ void momentum_one(float gi, float& m, float& ui, float mom_w,
                                              float nest_w, bool large_m, bool large_n) {
@@ -116,25 +132,40 @@ __device__ __forceinline__ void momentum_one(float gi, float& m, float& ui, floa
   }
 }
 
+__device__ __forceinline__ void flag_nonfinite(uint32_t* found_inf, bool bad) {
+  if (found_inf != nullptr && __any(bad) && (threadIdx.x & 63) == 0)
+    *reinterpret_cast<volatile uint32_t*>(found_inf) = 1u;
+}
+
+// Matrices whose X has the stored layout: a flat pass.  A block covers
+// kElemsPerBlock consecutive elements; a lane moves 4 consecutive elements
+// (one row, pc a multiple of 4) per 128-bit access when the matrix's buffers
+// are 16-byte aligned, else one element per access.  Gradient and momentum
+// are touched once here, so their accesses are non-temporal.
 template <bool kMomentum>
-__global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u_all,
-                                                          double* part_all, int64_t numel,
-                                                          int64_t blocks, float mom_w,
+__global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, uint16_t* x_all,
+                                                          double* part_all, int64_t rows,
+                                                          int64_t cols, int64_t mp, int64_t ldn,
+                                                          int64_t parts, float mom_w,
                                                           float nest_w, uint32_t* found_inf) {
   __shared__ double lds[kBlock / 64];
   const int mat = blockIdx.y;
+  if (!x_is_stored(mats, mat, rows, cols)) return;  // block-uniform: momentum_t_kernel's matrix
+  const int64_t pc = mats.transposed[mat] ? rows : cols, numel = rows * cols;
   const float* g = mats.grad[mat];
   const float* mom = mats.mom[mat];
   float* mom_out = mats.mom_out[mat];
-  float* u = u_all + (int64_t)mat * numel;
+  uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
   const bool large_m = mom_w >= 0.5f, large_n = nest_w >= 0.5f;
-  const bool vec = ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(mom) |
-                     reinterpret_cast<uintptr_t>(mom_out)) & 15) == 0 &&
-                   base + kElemsPerBlock <= numel;  // u is 256-byte aligned, numel * 4 per matrix
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(g) |
+                         (kMomentum ? reinterpret_cast<uintptr_t>(mom) |
+                                          reinterpret_cast<uintptr_t>(mom_out)
+                                    : 0);
+  const bool vec = (addr & 15) == 0 && (pc & 3) == 0 && base + kElemsPerBlock <= numel;
   double ss = 0.0;
   bool bad = false;
-  if (vec && (numel & 3) == 0) {
+  if (vec) {
 #pragma unroll
     for (int k = 0; k < kElemsPerBlock / (4 * kBlock); ++k) {
       const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
@@ -142,18 +173,20 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u
       const u32x4 gb = __builtin_bit_cast(u32x4, gv);
       bad |= nonfinite_f32_bits(gb.x) | nonfinite_f32_bits(gb.y) | nonfinite_f32_bits(gb.z) |
              nonfinite_f32_bits(gb.w);
-      f32x4 mv = f32x4{0.f, 0.f, 0.f, 0.f}, uv;
+      f32x4 mv = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (kMomentum) mv = load_stream<true>(reinterpret_cast<const f32x4*>(mom + i));
+      uint32_t h[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float m = mv[e], ui;
         momentum_one<kMomentum>(gv[e], m, ui, mom_w, nest_w, large_m, large_n);
         mv[e] = m;
-        uv[e] = ui;
+        h[e] = float_to_bf16_bits(ui);
         ss += (double)ui * (double)ui;
       }
       if constexpr (kMomentum) store_stream<true>(reinterpret_cast<f32x4*>(mom_out + i), mv);
-      store_stream<true>(reinterpret_cast<f32x4*>(u + i), uv);
+      const int64_t r = i / pc, c = i - r * pc;
+      *reinterpret_cast<u32x2*>(xm + r * ldn + c) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     }
   } else {
     for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
@@ -161,34 +194,21 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, float* u
       bad |= nonfinite_f32_bits(__builtin_bit_cast(uint32_t, g[i]));
       momentum_one<kMomentum>(g[i], m, ui, mom_w, nest_w, large_m, large_n);
       if constexpr (kMomentum) mom_out[i] = m;
-      u[i] = ui;
+      const int64_t r = i / pc, c = i - r * pc;
+      xm[r * ldn + c] = (uint16_t)float_to_bf16_bits(ui);
       ss += (double)ui * (double)ui;
     }
   }
-  if (found_inf != nullptr && __any(bad) && (threadIdx.x & 63) == 0)
-    *reinterpret_cast<volatile uint32_t*>(found_inf) = 1u;
+  flag_nonfinite(found_inf, bad);
   const double s = block_sum(ss, lds);
-  if (threadIdx.x == 0) part_all[(int64_t)mat * blocks + blockIdx.x] = s;
+  if (threadIdx.x == 0) part_all[(int64_t)mat * parts + blockIdx.x] = s;
 }
 
-// den = fp32(sqrt(sum)) + fp32(1e-7): x / (x.norm() + 1e-7) of optimizer.py:18.
-__global__ __launch_bounds__(kBlock) void norm_kernel(const double* part_all, float* den,
-                                                      int64_t blocks) {
-  __shared__ double lds[kBlock / 64];
-  const int mat = blockIdx.x;
-  double s = 0.0;
-  for (int64_t i = threadIdx.x; i < blocks; i += kBlock) s += part_all[(int64_t)mat * blocks + i];
-  const double t = block_sum(s, lds);
-  if (threadIdx.x == 0) den[mat] = (float)sqrt(t) + 1e-7f;
-}
-
-// Tile geometry shared by scale_kernel and apply_kernel.  A matrix's stored
-// layout is [pr, pc] = [rows, cols], or [cols, rows] when transposed; X is
-// [m, n] with m = min.  When pr <= pc X has the stored layout, otherwise it is
-// the transpose.  One 64 x 64 tile of the stored layout per block; the grid
-// covers [rows, cols] in 64-tiles and a transposed matrix reads block (x, y)
-// as its tile (y, x).  `vec`: a whole tile with rows a multiple of 4, moved 4
-// consecutive elements per lane access.
+// Tile geometry shared by momentum_t_kernel and apply_kernel.  One 64 x 64
+// tile of the stored layout per block; the grid covers [rows, cols] in
+// 64-tiles and a transposed matrix reads block (x, y) as its tile (y, x).
+// `vec`: a whole tile with rows a multiple of 4, moved 4 consecutive elements
+// per lane access.
 struct TileGeo {
   int64_t pr, pc, r0, c0;
   bool same_is_x, vec;
@@ -207,45 +227,72 @@ __device__ __forceinline__ TileGeo tile_geo(const MatPtrs& mats, int mat, int64_
   return t;
 }
 
-// X (bf16, padded [Mp][ldn]) from u / den.  X in the stored layout is
-// written straight from the tile; otherwise the tile is transposed through
-// LDS so both the u reads and the X writes are coalesced.
-__global__ __launch_bounds__(kBlock) void scale_kernel(MatPtrs mats, const float* u_all,
-                                                       const float* den, uint16_t* x_all,
-                                                       int64_t rows, int64_t cols, int64_t mp,
-                                                       int64_t ldn, int64_t numel) {
+// Matrices whose X is the transpose of the stored layout: the momentum pass
+// per 64 x 64 tile, bf16(u) transposed through LDS so that both the stored
+// reads and the X writes are coalesced.  One partial sum per tile, indexed by
+// the tile's place in the stored layout (row-major over tiles), so a matrix
+// sums in the same order whichever way the batch describes it.
+template <bool kMomentum>
+__global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16_t* x_all,
+                                                            double* part_all, int64_t rows,
+                                                            int64_t cols, int64_t mp, int64_t ldn,
+                                                            int64_t parts, float mom_w,
+                                                            float nest_w, uint32_t* found_inf) {
   __shared__ __attribute__((aligned(8))) uint16_t tile[kTile][kTile + 4];
+  __shared__ double lds[kBlock / 64];
   const int mat = blockIdx.z;
   const TileGeo t = tile_geo(mats, mat, rows, cols);
-  const float d = den[mat];
-  const float* u = u_all + (int64_t)mat * numel;  // 16-byte aligned when pc % 4 == 0
+  if (t.same_is_x) return;  // block-uniform: momentum_kernel's matrix
+  const float* g = mats.grad[mat];
+  const float* mom = mats.mom[mat];
+  float* mom_out = mats.mom_out[mat];
   uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
+  const bool large_m = mom_w >= 0.5f, large_n = nest_w >= 0.5f;
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(g) |
+                         (kMomentum ? reinterpret_cast<uintptr_t>(mom) |
+                                          reinterpret_cast<uintptr_t>(mom_out)
+                                    : 0);
+  const bool vec = t.vec && (addr & 15) == 0;
   const int q = threadIdx.x & 15, w = threadIdx.x >> 4;  // 4-element group, row of a pass
+  double ss = 0.0;
+  bool bad = false;
   for (int rr = w; rr < kTile; rr += kBlock / 16) {
     const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
     uint32_t h[4] = {0, 0, 0, 0};
-    if (t.vec) {
-      const f32x4 v = load_stream<true>(reinterpret_cast<const f32x4*>(u + r * t.pc + c));
+    if (vec) {
+      const int64_t i = r * t.pc + c;
+      const f32x4 gv = load_stream<true>(reinterpret_cast<const f32x4*>(g + i));
+      const u32x4 gb = __builtin_bit_cast(u32x4, gv);
+      bad |= nonfinite_f32_bits(gb.x) | nonfinite_f32_bits(gb.y) | nonfinite_f32_bits(gb.z) |
+             nonfinite_f32_bits(gb.w);
+      f32x4 mv = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kMomentum) mv = load_stream<true>(reinterpret_cast<const f32x4*>(mom + i));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) h[e] = float_to_bf16_bits(v[e] / d);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (r < t.pr && c + e < t.pc) h[e] = float_to_bf16_bits(u[r * t.pc + c + e] / d);
-    }
-    if (t.same_is_x) {
-      if (t.vec) {
-        *reinterpret_cast<u32x2*>(xm + r * ldn + c) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (r < t.pr && c + e < t.pc) xm[r * ldn + c + e] = (uint16_t)h[e];
+      for (int e = 0; e < 4; ++e) {
+        float m = mv[e], ui;
+        momentum_one<kMomentum>(gv[e], m, ui, mom_w, nest_w, large_m, large_n);
+        mv[e] = m;
+        h[e] = float_to_bf16_bits(ui);
+        ss += (double)ui * (double)ui;
       }
+      if constexpr (kMomentum) store_stream<true>(reinterpret_cast<f32x4*>(mom_out + i), mv);
     } else {
-      *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (r < t.pr && c + e < t.pc) {
+          const int64_t i = r * t.pc + c + e;
+          float m = kMomentum ? mom[i] : 0.f, ui;
+          bad |= nonfinite_f32_bits(__builtin_bit_cast(uint32_t, g[i]));
+          momentum_one<kMomentum>(g[i], m, ui, mom_w, nest_w, large_m, large_n);
+          if constexpr (kMomentum) mom_out[i] = m;
+          h[e] = float_to_bf16_bits(ui);
+          ss += (double)ui * (double)ui;
+        }
+      }
     }
+    *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
   }
-  if (t.same_is_x) return;  // block-uniform
+  flag_nonfinite(found_inf, bad);
   __syncthreads();
   for (int cc = w; cc < kTile; cc += kBlock / 16) {
     const int64_t c = t.c0 + cc, r = t.r0 + 4 * q;  // X row c, columns r .. r + 3
@@ -260,11 +307,47 @@ __global__ __launch_bounds__(kBlock) void scale_kernel(MatPtrs mats, const float
         if (c < t.pc && r + e < t.pr) xm[c * ldn + r + e] = (uint16_t)h[e];
     }
   }
+  const double s = block_sum(ss, lds);
+  if (threadIdx.x == 0)
+    part_all[(int64_t)mat * parts + (t.r0 / kTile) * ((t.pc + kTile - 1) / kTile) + t.c0 / kTile] = s;
+}
+
+// den = fp32(sqrt(sum)) + fp32(1e-7): x / (x.norm() + 1e-7) of optimizer.py:18.
+// scale[mat] = 1 / den and scale[count + mat] = 1 / den^2 scale the first
+// Newton-Schulz products of X0 = bf16(u); scale[2 count + mat] = den.
+__global__ __launch_bounds__(kBlock) void norm_kernel(MatPtrs mats, const double* part_all,
+                                                      float* scale, int64_t rows, int64_t cols,
+                                                      int64_t blocks, int64_t tiles,
+                                                      int64_t parts, int count) {
+  __shared__ double lds[kBlock / 64];
+  const int mat = blockIdx.x;
+  const int64_t n = x_is_stored(mats, mat, rows, cols) ? blocks : tiles;
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += kBlock) s += part_all[(int64_t)mat * parts + i];
+  const double t = block_sum(s, lds);
+  if (threadIdx.x == 0) {
+    const float den = (float)sqrt(t) + 1e-7f;
+    scale[mat] = 1.0f / den;
+    scale[count + mat] = (float)(1.0 / ((double)den * (double)den));
+    scale[2 * count + mat] = den;
+  }
+}
+
+// Without Newton-Schulz iterations X itself is the result: X = bf16(X0 / den)
+// over the whole padded buffer (zero padding stays zero).
+__global__ __launch_bounds__(kBlock) void rescale_kernel(uint16_t* x_all, const float* den,
+                                                         int64_t per_matrix) {
+  const int mat = blockIdx.y;
+  const float d = den[mat];
+  uint16_t* xm = x_all + (int64_t)mat * per_matrix;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < per_matrix;
+       i += (int64_t)gridDim.x * kBlock)
+    xm[i] = (uint16_t)float_to_bf16_bits(bf16_bits_to_float(xm[i]) / d);
 }
 
 // p = p * decay + (U * scale) * neg_lr with U = X in p's layout; scale is
 // scale_t for a transposed matrix.  kExtract: p = U instead (orthogonalize
-// alone returns the fp32 value of U).  Same tiles as scale_kernel: when X is
+// alone returns the fp32 value of U).  Same tiles as momentum_t_kernel: when X is
 // the transpose of p's layout the tile of X is staged through LDS first.
 template <bool kExtract>
 __device__ __forceinline__ float apply_one(float p, uint32_t u16, float scale, float decay,
@@ -354,9 +437,8 @@ namespace {
 
 struct Bufs {
   Layout L;
-  float* u;
   double* part;
-  float* den;
+  float* scale;  // [3][count]: 1 / den, 1 / den^2, den
   uint16_t* X[2];
   uint16_t* A;
   uint16_t* B;
@@ -383,9 +465,8 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   if ((rows + kTile - 1) / kTile > 65535) return MORPH_ERANGE;  // grid y of scale/apply
   char* ws = static_cast<char*>(workspace);
   out->L = L;
-  out->u = reinterpret_cast<float*>(ws + L.off_u);
   out->part = reinterpret_cast<double*>(ws + L.off_part);
-  out->den = reinterpret_cast<float*>(ws + L.off_den);
+  out->scale = reinterpret_cast<float*>(ws + L.off_scale);
   out->X[0] = reinterpret_cast<uint16_t*>(ws + L.off_x0);
   out->X[1] = reinterpret_cast<uint16_t*>(ws + L.off_x1);
   out->A = reinterpret_cast<uint16_t*>(ws + L.off_a);
@@ -393,7 +474,7 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   return MORPH_OK;
 }
 
-// 64 x 64 tiles of [rows, cols] per matrix (scale_kernel, apply_kernel).
+// 64 x 64 tiles of [rows, cols] per matrix (momentum_t_kernel, apply_kernel).
 dim3 tile_grid(int64_t rows, int64_t cols, int count) {
   return dim3((unsigned)((cols + kTile - 1) / kTile), (unsigned)((rows + kTile - 1) / kTile),
               (unsigned)count);
@@ -420,19 +501,44 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
   const Layout& L = W.L;
   hipStream_t s = as_stream(stream);
   const MatPtrs mp_ = pointers(mats, count);
-  const dim3 ew((unsigned)L.blocks, count);
-  if (orth_only)
-    hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.u, W.part, L.numel,
-                       L.blocks, hp->momentum_weight, hp->nesterov_weight, found_inf);
-  else
-    hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.u, W.part, L.numel,
-                       L.blocks, hp->momentum_weight, hp->nesterov_weight, found_inf);
+  // X0 has the stored layout of a matrix when its stored rows are the shorter side
+  bool flat = false, tiled = false;
+  for (int i = 0; i < count; ++i) {
+    const bool tr = mats[i].transposed != 0;
+    ((tr ? cols : rows) <= (tr ? rows : cols) ? flat : tiled) = true;
+  }
+  const float mw = hp->momentum_weight, nw = hp->nesterov_weight;
+  if (flat) {
+    const dim3 ew((unsigned)L.blocks, count);
+    if (orth_only)
+      hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
+                         rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
+    else
+      hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
+                         rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
+    if ((rc = launch_status())) return rc;
+  }
+  if (tiled) {
+    const dim3 tg = tile_grid(rows, cols, count);
+    if (orth_only)
+      hipLaunchKernelGGL(momentum_t_kernel<false>, tg, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
+                         rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
+    else
+      hipLaunchKernelGGL(momentum_t_kernel<true>, tg, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
+                         rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
+    if ((rc = launch_status())) return rc;
+  }
+  hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, mp_, W.part, W.scale, rows,
+                     cols, L.blocks, L.tiles, L.parts, count);
   if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, W.part, W.den, L.blocks);
-  if ((rc = launch_status())) return rc;
-  hipLaunchKernelGGL(scale_kernel, tile_grid(rows, cols, count), dim3(kBlock), 0, s, mp_, W.u,
-                     W.den, W.X[0], rows, cols, L.mp, L.ldn, L.numel);
-  return launch_status();
+  if (hp->ns_steps == 0) {
+    const int64_t per = L.mp * L.ldn;
+    const int64_t bx = std::min<int64_t>((per + kBlock - 1) / kBlock, 4096);
+    hipLaunchKernelGGL(rescale_kernel, dim3((unsigned)bx, count), dim3(kBlock), 0, s, W.X[0],
+                       W.scale + 2 * count, per);
+    rc = launch_status();
+  }
+  return rc;
 }
 
 int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp,
@@ -446,17 +552,22 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
   int cur = 0;
   for (int it = 0; it < hp->ns_steps; ++it) {
     uint16_t* X = W.X[cur];
+    // X0 = bf16(u) is not normalised yet: the first iteration's products take
+    // the per-matrix factors, A = (X0 X0^T) / den^2 and X' = (B X0 + a X0) / den
+    const float* inv_den = it == 0 ? W.scale : nullptr;
+    const float* inv_den2 = it == 0 ? W.scale + count : nullptr;
     // A = X X^T (symmetric: upper triangle of tiles, mirrored)
-    rc = morph_gemm_nt_bf16(X, X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, n, n, 0, m, 0,
-                            sx, sx, 0, ss, 0, 1.0f, 0.0f, MORPH_GEMM_SYMMETRIC, stream);
+    rc = gemm_nt_bf16_scaled(X, X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, n, n, 0, m, 0,
+                             sx, sx, 0, ss, 0, 1.0f, 0.0f, inv_den2, MORPH_GEMM_SYMMETRIC, stream);
     if (rc) return rc;
     // B = c (A A^T) + b A (symmetric)
     rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, m, m, m, m, 0,
                             ss, ss, ss, ss, 0, hp->c, hp->b, MORPH_GEMM_SYMMETRIC, stream);
     if (rc) return rc;
     // X' = B X + a X: X as the [K, N] operand (transposing LDS reads), into the other buffer
-    rc = morph_gemm_nt_bf16(W.B, X, X, W.X[cur ^ 1], nullptr, L.mp, L.np, L.mp, count, m, n, n, n,
-                            0, ss, sx, sx, sx, 0, 1.0f, hp->a, MORPH_GEMM_Q_KN, stream);
+    rc = gemm_nt_bf16_scaled(W.B, X, X, W.X[cur ^ 1], nullptr, L.mp, L.np, L.mp, count, m, n, n,
+                             n, 0, ss, sx, sx, sx, 0, 1.0f, hp->a, inv_den, MORPH_GEMM_Q_KN,
+                             stream);
     if (rc) return rc;
     cur ^= 1;
   }

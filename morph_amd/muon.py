@@ -251,8 +251,12 @@ class HybridMuonAdamW:
         # the momentum pass writes into these and they swap with `momentum`
         # once the non-finite gate has passed, so a raise mutates nothing
         self._momentum_next = {}
+        # The gate below has already seen every AdamW gradient finite when the group
+        # steps (and it has no loss scale), so its step needs no host round trip of its
+        # own: the one wait per step is the gate's.  Host mirrors of its step counts
+        # refresh on resolve(), which state_dict() and load_state_dict() call.
         self.adam = FusedAdamW(adam, lr=lr, weight_decay=weight_decay, betas=(.9, .95),
-                               sync=True) if adam else None
+                               sync=False) if adam else None
         self._flag = None
 
     def zero_grad(self, set_to_none=True):

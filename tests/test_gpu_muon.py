@@ -143,6 +143,17 @@ def test_orthogonalize_batches_same_shape_matrices():
         assert torch.equal(muon.orthogonalize(g.to(DEV)), b)
 
 
+@pytest.mark.parametrize("shape", [(96, 160), (160, 96), (70, 45)])
+def test_orthogonalize_without_iterations_is_the_normalised_input(shape):
+    """steps=0: X = G / (|G| + 1e-7) (optimizer.py:18), here bf16(bf16(G) / den): two bf16
+    roundings of the FP32 value, so within 2^-7 of it elementwise, in both orientations."""
+    G = torch.randn(shape, generator=torch.Generator().manual_seed(sum(shape))) * 1e-3
+    out = muon.orthogonalize(G.to(DEV), steps=0).cpu()
+    ref = G / (G.norm() + 1e-7)
+    assert out.shape == ref.shape
+    assert bool(((out - ref).abs() <= ref.abs() * 2 ** -7).all())
+
+
 @pytest.mark.parametrize("shape", [(128, 256), (300, 100), (70, 45), (4100, 1024)])
 def test_muon_step_elementwise_bitexact(shape):
     """momentum/Nesterov and the master update match the oracle bit for bit (128-bit
