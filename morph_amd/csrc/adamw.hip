@@ -17,7 +17,10 @@
 // issued before any arithmetic.  Measured on MI355X (config 2 window), small
 // workgroups with one access per lane (128 x 1) stream best: many short-lived
 // workgroups keep every CU's memory pipeline full, while longer per-lane
-// chains (unroll 4/8) or 1024-lane groups lose 3-7%.  Chunks map to workgroups
+// chains (unroll 4/8) or 1024-lane groups lose 3-7%; and fewer of them per CU
+// at a time (8, set by the launch's LDS reservation), with each lane's stream
+// loads issued before the step's control words are read, are 0-6% faster
+// than the hardware's own limit.  Chunks map to workgroups
 // in address order; the dispatcher spreads consecutive workgroups round-robin
 // over the 8 XCDs, which is what a pure stream with no reuse wants.
 //
@@ -55,6 +58,15 @@ constexpr bool kGradNT = MORPH_ADAMW_GRAD_NT != 0;
 constexpr int kPerBlock = kBlock * 4 * kUnroll;
 constexpr int kMaxTensors = 48;
 constexpr int kMaxHp = 8;
+// Residency cap: every workgroup reserves this much LDS, which it does not
+// use, so at most 160 KiB / 20 KiB = 8 workgroups (16 waves) share a CU.  The
+// stream runs faster with fewer workgroups in flight per CU, by an amount that
+// depends on where the buffers sit in physical memory: config-2 window,
+// round-robin against the uncapped kernel in one process, 0-15 us faster in
+// most placements and up to 3 us slower in a few; a cap of 7 is as fast, 6 is
+// slower and 5 far slower (277 us).  The cap pays off with the loads issued
+// before the control words (adamw_multi_kernel).
+constexpr unsigned kOccupancyLds = 20 * 1024;
 // A tensor is cut into segments of at most this many elements so block
 // counts stay far inside the 32-bit grid limits.
 constexpr int64_t kMaxSegment = int64_t(1) << 30;
@@ -160,36 +172,45 @@ __device__ __forceinline__ void store_out1(void* out, int64_t i, float p) {
   }
 }
 
-template <typename GT, typename OT>
-__device__ __forceinline__ void chunk_vector(const TensorArg& T, const morph_adamw_hp& hp,
-                                             int64_t base) {
-  const int tid = threadIdx.x;
+// One lane's share of a vector chunk, held between the loads and the update.
+struct VecRegs {
   f32x4 P[kUnroll], M[kUnroll], V[kUnroll];
   float G[kUnroll][4];
+};
+
+template <typename GT>
+__device__ __forceinline__ void load_vector(const TensorArg& T, int64_t base, VecRegs& r) {
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t e = base + (int64_t)(u * kBlock + tid) * 4;
-    load_grad4<GT>(T.grad, e, G[u]);
-    P[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.p + e));
-    M[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.m + e));
-    V[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.v + e));
+    load_grad4<GT>(T.grad, e, r.G[u]);
+    r.P[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.p + e));
+    r.M[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.m + e));
+    r.V[u] = load_stream<kNT>(reinterpret_cast<const f32x4*>(T.v + e));
   }
+}
+
+template <typename OT>
+__device__ __forceinline__ void update_vector(const TensorArg& T, const morph_adamw_hp& hp,
+                                              int64_t base, VecRegs& r) {
+  const int tid = threadIdx.x;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      float p = P[u][k], m = M[u][k], v = V[u][k];
-      adamw_update(G[u][k], p, m, v, hp);
-      P[u][k] = p; M[u][k] = m; V[u][k] = v;
+      float p = r.P[u][k], m = r.M[u][k], v = r.V[u][k];
+      adamw_update(r.G[u][k], p, m, v, hp);
+      r.P[u][k] = p; r.M[u][k] = m; r.V[u][k] = v;
     }
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t e = base + (int64_t)(u * kBlock + tid) * 4;
-    store_stream<kNT>(reinterpret_cast<f32x4*>(T.p + e), P[u]);
-    store_stream<kNT>(reinterpret_cast<f32x4*>(T.m + e), M[u]);
-    store_stream<kNT>(reinterpret_cast<f32x4*>(T.v + e), V[u]);
-    if (T.out != nullptr) store_out4<OT>(T.out, e, P[u]);
+    store_stream<kNT>(reinterpret_cast<f32x4*>(T.p + e), r.P[u]);
+    store_stream<kNT>(reinterpret_cast<f32x4*>(T.m + e), r.M[u]);
+    store_stream<kNT>(reinterpret_cast<f32x4*>(T.v + e), r.V[u]);
+    if (T.out != nullptr) store_out4<OT>(T.out, e, r.P[u]);
   }
 }
 
@@ -206,44 +227,60 @@ __device__ __forceinline__ void chunk_scalar(const TensorArg& T, const morph_ada
   }
 }
 
-template <typename GT, typename OT, bool kDev>
-__global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const LaunchArgs a,
-                                                             const uint32_t* __restrict__ skip) {
-  // Conditional skip: a flagged (overflowed) step leaves every byte untouched.
+// The step's constants for this workgroup's tensor, or false when the step
+// must leave memory untouched (overflow flagged, fatal state, or a clock
+// outside the tables).
+template <bool kDev>
+__device__ __forceinline__ bool control(const LaunchArgs& a, const TensorArg& T,
+                                        const uint32_t* skip, morph_adamw_hp& hp) {
+  hp = a.hp[T.hp];
   if constexpr (kDev) {
-    if ((a.state->found_inf | a.state->fatal) != 0u) return;
-  } else {
-    if (skip != nullptr && *skip != 0u) return;
-  }
-  const int b = blockIdx.x;
-  const TensorArg& T = a.t[segment_of(a.t, a.count, b)];
-  morph_adamw_hp hp = a.hp[T.hp];
-  if constexpr (kDev) {
+    if ((a.state->found_inf | a.state->fatal) != 0u) return false;
     // Step-dependent constants from device state, in the host's double arithmetic.
     const morph_adamw_sched& S = a.sched[T.hp];
     const int64_t t = a.clocks[T.clock] + 1;
-    if (t < 1 || t > S.table_len) return;  // host keeps clocks inside the tables
+    if (t < 1 || t > S.table_len) return false;  // host keeps clocks inside the tables
     const double scale = a.state->scale;
     hp.scale = (float)scale;
     hp.inv_scale = (float)(1.0 / scale);
     hp.flags = (hp.flags & ~MORPH_HP_DIVIDE_SCALE) | (pow2_double(scale) ? 0u : MORPH_HP_DIVIDE_SCALE);
     hp.bias_correction2_sqrt = S.bias_correction2_sqrt[t - 1];
     hp.neg_step_size = (float)(-(S.lr / S.bias_correction1[t - 1]));
+  } else {
+    if (skip != nullptr && *skip != 0u) return false;
   }
+  return true;
+}
+
+template <typename GT, typename OT, bool kDev>
+__global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const LaunchArgs a,
+                                                             const uint32_t* __restrict__ skip) {
+  const int b = blockIdx.x;
+  const TensorArg& T = a.t[segment_of(a.t, a.count, b)];
   const int64_t base = (int64_t)(b - T.first_block) * kPerBlock;
-  if (T.vector_ok && base + kPerBlock <= T.n)
-    chunk_vector<GT, OT>(T, hp, base);
-  else
+  morph_adamw_hp hp;
+  if (T.vector_ok && base + kPerBlock <= T.n) {
+    // The streams are requested before the control words, so their latency
+    // overlaps; a skipped step (control false) still writes nothing.
+    VecRegs r;
+    load_vector<GT>(T, base, r);
+    if (!control<kDev>(a, T, skip, hp)) return;
+    update_vector<OT>(T, hp, base, r);
+  } else {
+    if (!control<kDev>(a, T, skip, hp)) return;
     chunk_scalar<GT, OT>(T, hp, base, base + kPerBlock < T.n ? base + kPerBlock : T.n);
+  }
 }
 
 template <typename GT, typename OT>
 int launch(bool dev, const LaunchArgs& a, int blocks, const uint32_t* skip, hipStream_t s) {
   if (dev)
-    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, true>), dim3(blocks), dim3(kBlock), 0, s, a,
+    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, true>), dim3(blocks), dim3(kBlock),
+                       kOccupancyLds, s, a,
                        skip);
   else
-    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, false>), dim3(blocks), dim3(kBlock), 0, s, a,
+    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, false>), dim3(blocks), dim3(kBlock),
+                       kOccupancyLds, s, a,
                        skip);
   return launch_status();
 }
