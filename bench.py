@@ -158,7 +158,32 @@ def cpu_baseline(seconds=10.0):
         pass
     return dict(value=round(n / med / 1e9, 4), unit="Gparams/s", cores=threads, kind="port",
                 sample=f"config 2 window (N={n}), {len(times)} whole steps, median; "
-                       f"torch.optim.AdamW(foreach=False) after FP16 unscale; CPU: {cpu}")
+                       f"torch.optim.AdamW(foreach=False) after FP16 unscale; CPU: {cpu}",
+                disk_ops=cpu_baseline_disk(masters, grads16, seconds / 2))
+
+
+def cpu_baseline_disk(masters, grads16, seconds):
+    """The second CPU form: DiskState.update's chunked op sequence (streamtrain/disk.py:207-216,
+    1,048,576-element chunks, torch CPU ops, stacked write-back) on the config-2 window's three
+    [3, N] states held in RAM (no file I/O, no fsync), gradients unscaled from FP16."""
+    import numpy as np
+    from oracle import reference as R
+    states = [np.stack([m.numpy().reshape(-1), np.zeros(m.numel(), np.float32),
+                        np.zeros(m.numel(), np.float32)]) for m in masters]
+    grads = [(g.float() / LOSS_SCALE).reshape(-1) for g in grads16]
+    times = []
+    start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - start < seconds and len(times) < 20):
+        t0 = time.perf_counter()
+        for st, g in zip(states, grads):
+            R.disk_update_torch(st, g, len(times) + 1, HYPER["lr"], 1.0)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    n = sum(m.numel() for m in masters)
+    return dict(value=round(n / med / 1e9, 4), unit="Gparams/s",
+                sample=f"config 2 window, {len(times)} whole steps, median; DiskState.update's "
+                       "chunked torch op sequence on [3, N] states in RAM")
 
 
 def time_muon(steps, warmup):
