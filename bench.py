@@ -1,14 +1,16 @@
 """Benchmark of the MI355X optimizer step (BASELINE config 2 on one GPU).
 
-python bench.py [--gpus 1] [--steps K] [--warmup W]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
 A step is one optimizer step over the 5B-preset SwiGLU stage window
 (W_gate, W_up [6144, 3072] and W_down [3072, 6144]; N = 56,623,104 FP32
-masters): the non-finite detector over the FP16 gradients, the fused unscale +
-AdamW + FP16 export kernel, and the step close that applies the skip decision
-and advances the loss scale and the clocks -- all on the device, with no host
-round trip between steps.  Inputs are synthetic (seeded), resident in HBM
-before the timed region.
+masters, held with their moments and export copy in one arena): the
+non-finite detector over the FP16 gradients, the fused unscale + AdamW + FP16
+export kernel, and the step close that applies the skip decision and advances
+the loss scale and the clocks -- all on the device, with no host round trip
+between steps.  Inputs are synthetic (seeded), resident in HBM before the
+timed region.  Other workloads: embedding (config 3), overflow (config 4),
+muon (config 5), grads, window, fp8.
 
 Prints one JSON line.  `value` is whole-step throughput in Gparams/s;
 `roofline` is the fused AdamW kernel's algorithmic bandwidth (28 bytes per
@@ -92,7 +94,8 @@ def time_gpu(steps, warmup):
 
     The K timed steps carry no instrumentation (HIP events around a launch add
     about 6 us per step on the GPU); the AdamW launch duration comes from HIP
-    events around each launch of K further steps, run right after.
+    events around each launch of K further steps, run right after.  K more
+    steps with checked=True time the step without the detector pass.
     """
     from morph_amd import DynamicLossScale, FusedAdamW
 
@@ -101,7 +104,7 @@ def time_gpu(steps, warmup):
     grads = config2_grads(device, 1000)
     n = sum(p.numel() for p in masters)
     scaler = DynamicLossScale(LOSS_SCALE, growth_interval=2000)
-    opt = FusedAdamW(masters, **HYPER, loss_scale=scaler, export_dtype=torch.float16)
+    opt = FusedAdamW(masters, **HYPER, loss_scale=scaler, export_dtype=torch.float16, arena=True)
     for _ in range(warmup):
         opt.step(grads)
     opt.resolve()
@@ -111,16 +114,25 @@ def time_gpu(steps, warmup):
         opt.step(grads)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    opt.kernel_timer = []
+    timer = opt.kernel_timer = []
     for _ in range(steps):
         opt.step(grads)
     torch.cuda.synchronize()
+    opt.kernel_timer = None
+    kernel_ms = [a.elapsed_time(b) for a, b in timer]
+    # The same step when the gradients' producer has already set the step's
+    # non-finite flag (StageGradients.accumulate(..., final=True,
+    # found_inf=opt.found_inf)): fused AdamW + step close, no detector pass.
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step(grads, checked=True)
+    torch.cuda.synchronize()
+    elapsed_checked = time.perf_counter() - t0
     opt.resolve()
     if opt.skipped_steps:
         raise RuntimeError(f"{opt.skipped_steps} steps skipped on synthetic finite gradients")
-    kernel_ms = [a.elapsed_time(b) for a, b in opt.kernel_timer]
-    avg_kernel_s = sum(kernel_ms) / len(kernel_ms) / 1e3
-    return dict(n=n, elapsed=elapsed, avg_kernel_s=avg_kernel_s, kernel_ms=kernel_ms,
+    return dict(n=n, elapsed=elapsed, elapsed_checked=elapsed_checked,
+                avg_kernel_s=sum(kernel_ms) / len(kernel_ms) / 1e3, kernel_ms=kernel_ms,
                 scale=scaler.scale, applied=opt.applied_steps)
 
 
@@ -553,6 +565,232 @@ def fp8_main(args):
     print(json.dumps(line), flush=True)
 
 
+
+EMBED_SHAPE = (65536, 3072)
+EMBED_GRAD_SETS = 4  # distinct sparse-row gradients, cycled over the steps
+
+
+def time_embedding(steps, warmup):
+    """Config 3: the tied [65536, 3072] embedding, one tensor of 201,326,592 FP32 masters.
+    Each step's BF16 gradient is nonzero only on rows drawn Zipf(1.1) from 4 x 1024 token IDs
+    (N(0, 1e-3) there); every row still gets the dense update; wd 0, BF16 export.  A step is
+    detector + fused AdamW + step close, as in the config-2 workload."""
+    from morph_amd import FusedAdamW
+    device = torch.device("cuda", 0)
+    w = torch.randn(EMBED_SHAPE, generator=torch.Generator(device=device).manual_seed(3),
+                    device=device) * .02
+    sets, rows = [], []
+    for k in range(EMBED_GRAD_SETS):
+        g, active = config3_embedding_grad(3000 + k, device=device)
+        sets.append([g])
+        rows.append(active.numel())
+    opt = FusedAdamW([w], lr=3e-4, betas=(.9, .95), eps=1e-8, weight_decay=0.0,
+                     export_dtype=torch.bfloat16)
+    for t in range(warmup):
+        opt.step(sets[t % EMBED_GRAD_SETS])
+    opt.resolve()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(steps):
+        opt.step(sets[t % EMBED_GRAD_SETS])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer = opt.kernel_timer = []
+    for t in range(steps):
+        opt.step(sets[t % EMBED_GRAD_SETS])
+    torch.cuda.synchronize()
+    opt.kernel_timer = None
+    kernel_ms = [a.elapsed_time(b) for a, b in timer]
+    opt.resolve()
+    if opt.skipped_steps:
+        raise RuntimeError(f"{opt.skipped_steps} steps skipped on synthetic finite gradients")
+    return dict(n=w.numel(), elapsed=elapsed, avg_kernel_s=sum(kernel_ms) / len(kernel_ms) / 1e3,
+                rows=rows)
+
+
+def cpu_baseline_embedding(seconds=20.0):
+    """torch.optim.AdamW(foreach=False) on the [65536, 3072] embedding on the host cores
+    (BF16 gradient widened to FP32, wd 0): whole steps until `seconds` have passed (at
+    least 2), median."""
+    from oracle import reference as R
+    threads = min(16, R.cpu_threads())
+    torch.set_num_threads(threads)
+    w = torch.nn.Parameter(torch.randn(EMBED_SHAPE, generator=torch.Generator().manual_seed(3)) * .02)
+    g16, _ = config3_embedding_grad(3000)
+    opt = torch.optim.AdamW([w], lr=3e-4, betas=(.9, .95), eps=1e-8, weight_decay=0.0,
+                            foreach=False)
+    times = []
+    start = time.perf_counter()
+    while len(times) < 2 or (time.perf_counter() - start < seconds and len(times) < 10):
+        t0 = time.perf_counter()
+        w.grad = g16.float()
+        opt.step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return dict(value=round(w.numel() / med / 1e9, 4), unit="Gparams/s", cores=threads,
+                kind="port", sample=f"[65536, 3072] embedding, {len(times)} whole steps, median; "
+                                    "torch.optim.AdamW(foreach=False), BF16 grad widened to FP32")
+
+
+def embedding_main(args):
+    r = time_embedding(args.steps, args.warmup)
+    n = r["n"]
+    achieved = BYTES_PER_PARAM * n / r["avg_kernel_s"] / 1e9
+    line = {
+        "metric": "AdamW Gparams/s + achieved HBM GB/s vs peak, tied 65536x3072 embedding, 1 MI355X",
+        "value": round(n * args.steps / r["elapsed"] / 1e9, 3), "unit": "Gparams/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(r["elapsed"] / args.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "config 3: tied [65536, 3072] embedding, FP32 masters, BF16 "
+                               "sparse-row grads (Zipf(1.1) rows of 4x1024 tokens, N(0, 1e-3)), "
+                               "dense update of every row, wd 0, BF16 export; detector + fused "
+                               "AdamW + step close",
+                   "params": n, "shape": list(EMBED_SHAPE), "grad_dtype": "bf16",
+                   "export_dtype": "bf16", "lr": 3e-4, "betas": [0.9, 0.95], "eps": 1e-8,
+                   "weight_decay": 0.0, "gradient_rows_per_step": r["rows"]},
+        "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "adamw_multi_kernel<BF16,BF16,dev>",
+                     "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
+                     "bytes_per_launch": BYTES_PER_PARAM * n},
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_embedding(),
+    }
+    print(json.dumps(line), flush=True)
+
+
+CONFIG4_STEPS = 16
+CONFIG4_OVERFLOW = (3, 7, 12)
+
+
+def config4_sequence(device, seed=44):
+    """Config 4's 16 gradient sets: config-2 FP16 gradients x 2^16, with +inf/-inf/NaN written
+    at 1-8 seeded positions in steps 3, 7 and 12 (numpy RandomState(seed) picks the count,
+    tensor, position and value, in that order)."""
+    import numpy as np
+    rng = np.random.RandomState(seed)
+    sets = []
+    for t in range(1, CONFIG4_STEPS + 1):
+        grads = config2_grads(device, 4000 + t)
+        if t in CONFIG4_OVERFLOW:
+            for _ in range(int(rng.randint(1, 9))):
+                k = int(rng.randint(len(grads)))
+                flat = grads[k].view(-1)
+                flat[int(rng.randint(flat.numel()))] = float(rng.choice([np.inf, -np.inf, np.nan]))
+        sets.append(grads)
+    return sets
+
+
+def expected_config4_scales():
+    """Loss scale before each of the 16 steps by DynamicLossScale's rule (precision.py:6-17):
+    halve on overflow, grow x2 after 2000 good steps (not reached), cap 65536."""
+    from morph_amd import DynamicLossScale
+    s = DynamicLossScale(LOSS_SCALE, growth_interval=2000)
+    out = []
+    for t in range(1, CONFIG4_STEPS + 1):
+        out.append(s.scale)
+        s.overflow() if t in CONFIG4_OVERFLOW else s.success()
+    return out, s.state_dict()
+
+
+def time_overflow(reps):
+    """Config 4 on the config-2 window: the 16-step sequence enqueued back to back (skip
+    decisions, loss scale and clocks stay on the device).  One optimizer runs it once
+    untimed (its launch tables and bias tables are built there), then `reps` more times
+    timed; every repetition overflows three more times, so the scale keeps halving
+    (2^16 -> 2^4 after four).  Fresh optimizers then give per-launch times and, step by
+    step (sync=True), every decision and scale of the config's own 16 steps."""
+    from morph_amd import DynamicLossScale, FusedAdamW
+    device = torch.device("cuda", 0)
+    sets = config4_sequence(device)
+    masters0 = config2_window(device)
+    n = sum(m.numel() for m in masters0)
+
+    def fresh(sync=False):
+        scaler = DynamicLossScale(LOSS_SCALE, growth_interval=2000)
+        opt = FusedAdamW([m.clone() for m in masters0], **HYPER, loss_scale=scaler,
+                         export_dtype=torch.float16, arena=True, sync=sync)
+        return opt, scaler
+
+    opt, scaler = fresh()
+    for grads in sets:
+        opt.step(grads)
+    opt.resolve()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for grads in sets:
+            opt.step(grads)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    opt.resolve()
+    if opt.skipped_steps != 3 * (reps + 1):
+        raise RuntimeError(f"{opt.skipped_steps} skipped steps in {reps + 1} sequences")
+    del opt
+    # per-launch AdamW times, applied vs skipped steps (HIP events around each launch)
+    opt, _ = fresh()
+    timer = opt.kernel_timer = []
+    for grads in sets:
+        opt.step(grads)
+    torch.cuda.synchronize()
+    opt.kernel_timer = None
+    kernel_us = [a.elapsed_time(b) * 1e3 for a, b in timer]
+    opt.resolve()
+    # step by step: every decision and the scale before each step
+    sopt, sscaler = fresh(sync=True)
+    scales, applied = [], []
+    for grads in sets:
+        scales.append(sscaler.scale)
+        applied.append(bool(sopt.step(grads)))
+    clocks = [sopt.state[p]["step"] for p in sopt.param_groups[0]["params"]]
+    return dict(n=n, elapsed=elapsed, kernel_us=kernel_us, scales=scales, applied=applied,
+                scaler_state=sscaler.state_dict(), clocks=clocks,
+                async_skipped=opt.skipped_steps, async_applied=opt.applied_steps)
+
+
+def overflow_main(args):
+    reps = min(4, max(1, args.steps // CONFIG4_STEPS))  # 3 halvings per sequence: stay > 1
+    r = time_overflow(reps)
+    n = r["n"]
+    want_scales, want_state = expected_config4_scales()
+    skipped = [t for t, a in enumerate(r["applied"], 1) if not a]
+    ok = (r["scales"] == want_scales and r["scaler_state"] == want_state
+          and skipped == list(CONFIG4_OVERFLOW) and r["async_skipped"] == len(CONFIG4_OVERFLOW)
+          and r["clocks"] == [CONFIG4_STEPS - len(CONFIG4_OVERFLOW)] * 3)
+    k_app = [u for u, a in zip(r["kernel_us"], r["applied"]) if a]
+    k_skip = [u for u, a in zip(r["kernel_us"], r["applied"]) if not a]
+    avg_app = sum(k_app) / len(k_app)
+    achieved = BYTES_PER_PARAM * n / avg_app / 1e3
+    steps_run = reps * CONFIG4_STEPS
+    line = {
+        "metric": "Conditional-skip AdamW Gparams/s over config 4's 16 steps (3 skipped), 5B SwiGLU window, 1 MI355X",
+        "value": round(n * steps_run / r["elapsed"] / 1e9, 3), "unit": "Gparams/s",
+        "n_gpus": 1, "steps": steps_run, "warmup": CONFIG4_STEPS,
+        "ms_per_step": round(r["elapsed"] / steps_run * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "config 4: config-2 window, 16 steps from loss scale 2^16, "
+                               "+inf/-inf/NaN at 1-8 seeded positions in steps 3, 7, 12; "
+                               "detector + fused AdamW + step close, enqueued back to back; "
+                               "timed: the sequence repeated on one warmed optimizer",
+                   "params": n, "shapes": CONFIG2_SHAPES, "overflow_steps": list(CONFIG4_OVERFLOW),
+                   "repetitions": reps},
+        "sequence_ok": ok,
+        "skipped_steps": skipped,
+        "scale_before_step": r["scales"],
+        "adamw_us_applied": round(avg_app, 2),
+        "adamw_us_skipped": round(sum(k_skip) / len(k_skip), 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "adamw_multi_kernel<F16,F16,dev> (applied steps)",
+                     "avg_launch_us": round(avg_app, 2), "bytes_per_launch": BYTES_PER_PARAM * n},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    if not ok:
+        raise SystemExit("config-4 sequence differs from DynamicLossScale's rule")
+
 def measured_traffic():
     """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
     try:
@@ -567,9 +805,11 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("adamw", "muon", "grads", "window", "fp8"),
+    ap.add_argument("--workload", choices=("adamw", "embedding", "overflow", "muon", "grads",
+                                           "window", "fp8"),
                     default="adamw",
-                    help="adamw: the headline config-2 step (default); muon: config 5; "
+                    help="adamw: the headline config-2 step (default); embedding: config 3; "
+                         "overflow: config 4's skip sequence; muon: config 5; "
                          "grads: the stage-gradient window; window: the HBM-resident [3, N] "
                          "state; fp8: block-scaled FP8 transport encoding")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
@@ -591,6 +831,10 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "embedding":
+        return embedding_main(args)
+    if args.workload == "overflow":
+        return overflow_main(args)
     if args.workload == "muon":
         return muon_main(args)
     if args.workload == "grads":
@@ -620,8 +864,14 @@ def main():
                                "FP16 grads x 2^16 loss scale, detector + fused AdamW + FP16 export",
                    "params": n, "shapes": CONFIG2_SHAPES, "grad_dtype": "f16",
                    "export_dtype": "f16", **{k: v for k, v in HYPER.items()},
-                   "loss_scale": LOSS_SCALE},
+                   "loss_scale": LOSS_SCALE,
+                   "state_layout": "one arena: masters, moments, export (FusedAdamW(arena=True))"},
         "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
+        "step_checked": {
+            "gparams_per_s": round(n * args.steps / r["elapsed_checked"] / 1e9, 3),
+            "ms_per_step": round(r["elapsed_checked"] / args.steps * 1e3, 4),
+            "what": "fused AdamW + step close with the non-finite flag already set by the "
+                    "gradients' producer (step(checked=True)); no detector pass"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),

@@ -100,6 +100,28 @@ class AdamwBatch:
             d.clock_index = clock_index[i]
             keep.append((p, m, v, g, o))
         self._keep = keep  # the tensors must outlive the descriptors
+        self._grad_dtype = grads[0].dtype if n else None
+        self._numels = [p.numel() for p in params]
+        self._device = params[0].device if n else None
+
+    def rebind_grads(self, grads):
+        """Point the descriptors at new gradient tensors of the same sizes and dtype.
+
+        A training loop hands a new gradient buffer every step (autograd with
+        zero_grad(set_to_none=True), a rotating stage window); this swaps the
+        pointers without rebuilding and re-validating the whole table.
+        """
+        grads = list(grads)
+        if len(grads) != self.count:
+            raise ValueError(f"expected {self.count} gradients, got {len(grads)}")
+        for i, g in enumerate(grads):
+            require_device_tensor(g, f"grad[{i}]")
+            if g.dtype != self._grad_dtype or g.numel() != self._numels[i] or g.device != self._device:
+                raise ValueError(f"grad[{i}] does not match the batch (dtype, size or device)")
+        for i, g in enumerate(grads):
+            self.array[i].grad = g.data_ptr()
+            p, m, v, _, o = self._keep[i]
+            self._keep[i] = (p, m, v, g, o)
 
     def launch(self, hps, skip_flag=None, stream=None):
         """Enqueue the step.  hps: sequence of AdamwHP, indexed by hp_index."""

@@ -53,10 +53,16 @@ class FusedAdamW:
       from step() like HybridMuonAdamW (optimizer.py:50-51); implies sync.
     sync: resolve after every step; step() then returns True (applied) or
       False (skipped).  Otherwise step() returns None and enqueues only.
+    arena: place every master, both moments and the export copy in one device
+      allocation laid out for the fused pass (morph_amd.arena), the way a stage
+      window holds its state; each parameter's `.data` is moved there (its
+      values copied), so views of a parameter taken before construction stop
+      aliasing it.  Parameters must be distinct, non-overlapping tensors.
     """
 
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2, *,
-                 loss_scale=None, export_dtype=None, on_overflow="skip", sync=False):
+                 loss_scale=None, export_dtype=None, on_overflow="skip", sync=False,
+                 arena=False):
         if on_overflow not in _OVERFLOW_POLICIES:
             raise ValueError(f"on_overflow must be one of {_OVERFLOW_POLICIES}")
         if not 0.0 <= lr:
@@ -81,10 +87,15 @@ class FusedAdamW:
             if device is not None and p.device != device:
                 raise ValueError("all parameters must be on one device")
             device = p.device
-            self.state[p] = {"step": 0, "exp_avg": torch.zeros_like(p),
-                             "exp_avg_sq": torch.zeros_like(p)}
-            if export_dtype is not None:
-                self.exports.append(p.detach().to(export_dtype))
+        self.arena = None
+        if arena:
+            self._place_in_arena([p for _, p in flat], device, export_dtype)
+        else:
+            for _, p in flat:
+                self.state[p] = {"step": 0, "exp_avg": torch.zeros_like(p),
+                                 "exp_avg_sq": torch.zeros_like(p)}
+                if export_dtype is not None:
+                    self.exports.append(p.detach().to(export_dtype))
         self.device = device
         self._ctl = StepControl(device, len(flat), loss_scale)
         self._tables = {}
@@ -108,6 +119,24 @@ class FusedAdamW:
         return self._ctl.found_inf_view
 
     # -- helpers -----------------------------------------------------------
+    @torch.no_grad()
+    def _place_in_arena(self, params, device, export_dtype):
+        """Masters, moments and export copies in one Arena; p.data moves to its master view."""
+        from .arena import Arena
+        streams = [[(p.numel(), torch.float32)] * 3
+                   + ([(p.numel(), export_dtype)] if export_dtype is not None else [])
+                   for p in params]
+        self.arena = Arena(streams, device)
+        for p, views in zip(params, self.arena.views):
+            w, m, v = (t.view(p.shape) for t in views[:3])
+            w.copy_(p.detach())
+            m.zero_()
+            v.zero_()
+            p.data = w
+            self.state[p] = {"step": 0, "exp_avg": m, "exp_avg_sq": v}
+            if export_dtype is not None:
+                self.exports.append(views[3].view(p.shape).copy_(w))
+
     def _flat(self):
         return [(gi, p) for gi, group in enumerate(self.param_groups) for p in group["params"]]
 
@@ -144,8 +173,9 @@ class FusedAdamW:
         flat = self._flat()
         groups = sorted({flat[i][0] for i in present})
         hp_of = {gi: k for k, gi in enumerate(groups)}
-        key = (tuple(present), tuple(grads[i].data_ptr() for i in present),
+        key = (tuple(present), tuple(grads[i].dtype for i in present),
                tuple(e.data_ptr() for e in self.exports) if self.exports else None)
+        ptrs = tuple(grads[i].data_ptr() for i in present)
         if key != self._cache_key:
             ps = [flat[i][1] for i in present]
             batch = kernels.AdamwBatch(
@@ -154,9 +184,14 @@ class FusedAdamW:
                 [self.exports[i] for i in present] if self.exports else None,
                 hp_index=[hp_of[flat[i][0]] for i in present], clock_index=list(present))
             clock_list = torch.tensor(present, dtype=torch.int32).to(self.device)
-            self._cache = (batch, clock_list)
+            self._cache = [batch, clock_list, ptrs]
             self._cache_key = key
-        batch, clock_list = self._cache
+        elif ptrs != self._cache[2]:
+            # same tensors, new gradient buffers: swap pointers only (no table rebuild,
+            # no host-to-device copy that would wait for the queued steps)
+            self._cache[0].rebind_grads([grads[i] for i in present])
+            self._cache[2] = ptrs
+        batch, clock_list, _ = self._cache
         hps, scheds = [], []
         for gi in groups:
             group = self.param_groups[gi]

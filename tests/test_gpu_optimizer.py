@@ -259,6 +259,73 @@ def test_state_dict_interchanges_with_torch_adamw():
     assert float(back["state"][0]["step"]) == 4.0
 
 
+
+def test_arena_layout_gives_identical_steps():
+    """arena=True moves masters, moments and exports into one allocation: the steps,
+    the exports and the state dict are bit-identical to separate allocations, and each
+    parameter object keeps its identity with its data in the arena."""
+    shapes = [(1024, 1024), (3072,), (768, 384), (2048, 1024), (5,)]
+    gen = torch.Generator().manual_seed(70)
+    masters = [torch.randn(s, generator=gen) * .02 for s in shapes]
+    grads = [[(torch.randn(s, generator=gen) * 1e-4 * 1024).half() for s in shapes]
+             for _ in range(3)]
+    runs = []
+    for arena in (False, True):
+        params = [torch.nn.Parameter(m.to(DEV)) for m in masters]
+        groups = [{"params": params[:2], "weight_decay": .1}, {"params": params[2:]}]
+        opt = FusedAdamW(groups, lr=3e-4, betas=(.9, .95), eps=1e-8, weight_decay=0.0,
+                         loss_scale=1024.0, export_dtype=torch.float16, arena=arena)
+        for p, m in zip(params, masters):
+            assert torch.equal(p.detach().cpu(), m)
+        if arena:
+            base, end = opt.arena.storage.data_ptr(), opt.arena.storage.data_ptr() + opt.arena.nbytes
+            for p in params:
+                for t in (p, opt.state[p]["exp_avg"], opt.state[p]["exp_avg_sq"]):
+                    assert base <= t.data_ptr() < end
+        for gs in grads:
+            opt.step([g.to(DEV) for g in gs])
+        opt.resolve()
+        runs.append((params, opt))
+    (pa, a), (pb, b) = runs
+    for p, q in zip(pa, pb):
+        assert torch.equal(p, q)
+        for k in ("exp_avg", "exp_avg_sq"):
+            assert torch.equal(a.state[p][k], b.state[q][k])
+        assert a.state[p]["step"] == b.state[q]["step"] == 3
+    for e, f in zip(a.exports, b.exports):
+        assert torch.equal(e, f)
+    sa, sb = a.state_dict(), b.state_dict()
+    for i in sa["state"]:
+        assert torch.equal(sa["state"][i]["exp_avg_sq"], sb["state"][i]["exp_avg_sq"])
+
+
+def test_new_gradient_buffers_swap_pointers_only():
+    """A new gradient buffer every step (autograd with set_to_none) reuses the launch
+    table with swapped pointers and gives the same bytes as one reused buffer; a size
+    mismatch is rejected before anything is enqueued."""
+    shapes = [(300, 70), (4099,)]
+    gen = torch.Generator().manual_seed(71)
+    masters = [torch.randn(s, generator=gen) * .02 for s in shapes]
+    grads = [[torch.randn(s, generator=gen).half() for s in shapes] for _ in range(4)]
+    a = FusedAdamW([m.to(DEV) for m in masters], lr=1e-3, loss_scale=8.0)
+    b = FusedAdamW([m.to(DEV) for m in masters], lr=1e-3, loss_scale=8.0)
+    held = [g.to(DEV) for g in grads[0]]
+    tables = set()
+    for gs in grads:
+        a.step([g.to(DEV) for g in gs])
+        tables.add(id(a._cache[0]))
+        for h, g in zip(held, gs):
+            h.copy_(g.to(DEV))
+        b.step(held)
+    a.resolve()
+    b.resolve()
+    assert len(tables) == 1
+    for p, q in zip(a.param_groups[0]["params"], b.param_groups[0]["params"]):
+        assert torch.equal(p, q)
+        assert torch.equal(a.state[p]["exp_avg_sq"], b.state[q]["exp_avg_sq"])
+    with pytest.raises(ValueError):
+        a._cache[0].rebind_grads([torch.zeros(10, dtype=torch.half, device=DEV), held[1]])
+
 def _config4_grads(shapes, rng, t, scale, overflow_steps):
     grads = bench.config2_grads("cpu", 2000 + t, shapes, scale=scale)
     if t in overflow_steps:
