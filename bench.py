@@ -29,6 +29,7 @@ import torch
 
 ROOT = Path(__file__).resolve().parent
 TRAFFIC_PROFILE = ROOT / "profiles" / "adamw_config2_traffic.json"
+TRAFFIC_PROFILE_C3 = ROOT / "profiles" / "adamw_config3_traffic.json"
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_PARAM = 28  # read g16 2 + w 4 + m 4 + v 4; write w 4 + m 4 + v 4 + export 2
 CONFIG2_SHAPES = [(6144, 3072), (6144, 3072), (3072, 6144)]  # W_gate, W_up, W_down (nn.Linear storage)
@@ -89,34 +90,40 @@ class Config5(torch.nn.Module):
 
 
 # --------------------------------------------------------------- timing --
+GRAD_SETS = 3  # gradient sets cycled over the steps: 3 x 113 MB exceeds the 256 MB Infinity Cache
+
+
 def time_gpu(steps, warmup):
     """Steps are enqueued back to back (device-resident skip/scale/clock control).
 
-    The K timed steps carry no instrumentation (HIP events around a launch add
-    about 6 us per step on the GPU); the AdamW launch duration comes from HIP
-    events around each launch of K further steps, run right after.  K more
-    steps with checked=True time the step without the detector pass.
+    Each step takes the next of GRAD_SETS gradient sets, so no step finds its
+    gradients left in the Infinity Cache by an earlier one (one reused buffer
+    would flatter the step without a detector pass by about 10 us).  The K
+    timed steps carry no instrumentation (HIP events around a launch add about
+    6 us per step on the GPU); the AdamW launch duration comes from HIP events
+    around each launch of K further steps, run right after.  K more steps with
+    checked=True time the step without the detector pass.
     """
     from morph_amd import DynamicLossScale, FusedAdamW
 
     device = torch.device("cuda", 0)
     masters = config2_window(device)
-    grads = config2_grads(device, 1000)
+    sets = [config2_grads(device, 1000 + k) for k in range(GRAD_SETS)]
     n = sum(p.numel() for p in masters)
     scaler = DynamicLossScale(LOSS_SCALE, growth_interval=2000)
     opt = FusedAdamW(masters, **HYPER, loss_scale=scaler, export_dtype=torch.float16, arena=True)
-    for _ in range(warmup):
-        opt.step(grads)
+    for t in range(max(warmup, GRAD_SETS)):
+        opt.step(sets[t % GRAD_SETS])
     opt.resolve()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        opt.step(grads)
+    for t in range(steps):
+        opt.step(sets[t % GRAD_SETS])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     timer = opt.kernel_timer = []
-    for _ in range(steps):
-        opt.step(grads)
+    for t in range(steps):
+        opt.step(sets[t % GRAD_SETS])
     torch.cuda.synchronize()
     opt.kernel_timer = None
     kernel_ms = [a.elapsed_time(b) for a, b in timer]
@@ -124,8 +131,8 @@ def time_gpu(steps, warmup):
     # non-finite flag (StageGradients.accumulate(..., final=True,
     # found_inf=opt.found_inf)): fused AdamW + step close, no detector pass.
     t0 = time.perf_counter()
-    for _ in range(steps):
-        opt.step(grads, checked=True)
+    for t in range(steps):
+        opt.step(sets[t % GRAD_SETS], checked=True)
     torch.cuda.synchronize()
     elapsed_checked = time.perf_counter() - t0
     opt.resolve()
@@ -652,7 +659,8 @@ def embedding_main(args):
                    "weight_decay": 0.0, "gradient_rows_per_step": r["rows"]},
         "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(TRAFFIC_PROFILE_C3),
                      "kernel": "adamw_multi_kernel<BF16,BF16,dev>",
                      "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
                      "bytes_per_launch": BYTES_PER_PARAM * n},
@@ -791,10 +799,10 @@ def overflow_main(args):
     if not ok:
         raise SystemExit("config-4 sequence differs from DynamicLossScale's rule")
 
-def measured_traffic():
+def measured_traffic(path=TRAFFIC_PROFILE):
     """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
     try:
-        return json.loads(TRAFFIC_PROFILE.read_text())["traffic_bytes_per_launch"]
+        return json.loads(path.read_text())["traffic_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
 
@@ -865,7 +873,8 @@ def main():
                    "params": n, "shapes": CONFIG2_SHAPES, "grad_dtype": "f16",
                    "export_dtype": "f16", **{k: v for k, v in HYPER.items()},
                    "loss_scale": LOSS_SCALE,
-                   "state_layout": "one arena: masters, moments, export (FusedAdamW(arena=True))"},
+                   "state_layout": "one arena: masters, moments, export (FusedAdamW(arena=True))",
+                   "gradient_sets": GRAD_SETS},
         "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
         "step_checked": {
             "gparams_per_s": round(n * args.steps / r["elapsed_checked"] / 1e9, 3),
