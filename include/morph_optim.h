@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 2
+#define MORPH_ABI_VERSION 3
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -116,11 +116,14 @@ typedef struct morph_adamw_tensor {
  *
  * scale/good_steps/growth_interval/scale_cap are DynamicLossScale's state
  * (streamtrain/precision.py:6-17) kept in double precision, so the device
- * sequence of scales is bit-identical to the host one.  found_inf is the
- * detector's output for the step in flight.  fatal is sticky: bit 0 = an
- * overflow happened at scale <= 1 (the reference raises FloatingPointError
- * there).  While fatal is set every later step is a no-op, so the state the
- * host finds equals the reference's state at the point it would have raised.
+ * sequence of scales is bit-identical to the host one.  found_inf[slot] is
+ * the detector's output for a step in flight: steps alternate slots (the
+ * host's step count & 1), so the close of step s can run inside step s+1's
+ * detector launch (morph_nonfinite_or_close) while that launch ORs step
+ * s+1's flag into the other word.  fatal is sticky: bit 0 = an overflow
+ * happened at scale <= 1 (the reference raises FloatingPointError there).
+ * While fatal is set every later step is a no-op, so the state the host
+ * finds equals the reference's state at the point it would have raised.
  */
 typedef struct morph_step_state {
   double scale;
@@ -129,10 +132,11 @@ typedef struct morph_step_state {
   int64_t growth_interval;
   int64_t applied;        /* steps applied */
   int64_t skipped;        /* steps skipped on overflow */
-  uint32_t found_inf;     /* written by the detector, consumed by morph_step_end */
+  uint32_t found_inf[2];  /* per slot: written by the detector, consumed by the step's close */
   uint32_t fatal;
   uint32_t last_found_inf;
   uint32_t dynamic;       /* 1: DynamicLossScale state machine; 0: fixed scale */
+  uint32_t reserved;
 } morph_step_state;
 
 #define MORPH_FATAL_MIN_SCALE 1u
@@ -201,7 +205,7 @@ int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dty
 /*
  * Device-resident form of morph_adamw_multi.  Each tensor's step t is
  * d_clocks[clock_index] + 1; the unscale factor comes from d_state->scale; the
- * step is skipped when d_state->found_inf or d_state->fatal is set.  From
+ * step is skipped when d_state->found_inf[slot] or d_state->fatal is set.  From
  * hps[] only the step-independent fields are used (clip, decay, lerp_weight,
  * beta2, one_minus_beta2, eps, flags minus MORPH_HP_DIVIDE_SCALE); scheds[]
  * parallels hps[].  Clocks are NOT advanced here: morph_step_end does that.
@@ -209,18 +213,31 @@ int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dty
 int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad_dtype,
                           int out_dtype, const morph_adamw_hp* hps,
                           const morph_adamw_sched* scheds, int n_hp, const int64_t* d_clocks,
-                          const morph_step_state* d_state, void* stream);
+                          const morph_step_state* d_state, int slot, void* stream);
 
 /*
- * Closes a device-resident step (one workgroup): on overflow counts a skip and,
- * when `dynamic`, applies DynamicLossScale.overflow (or sets fatal bit 0 at
- * scale <= 1); else counts the step, applies success() when `dynamic`, and
- * advances the clocks d_clocks[d_clock_list[0..n)] (indices must be distinct).
- * Then records found_inf in last_found_inf and clears found_inf.  No-op while
- * fatal is set.
+ * Closes a device-resident step (one workgroup): on overflow (found_inf[slot])
+ * counts a skip and, when `dynamic`, applies DynamicLossScale.overflow (or sets
+ * fatal bit 0 at scale <= 1); else counts the step, applies success() when
+ * `dynamic`, and advances the clocks d_clocks[d_clock_list[0..n)] (indices must
+ * be distinct).  Then records found_inf[slot] in last_found_inf and clears it.
+ * No-op while fatal is set.  Must run after the step's AdamW launch and before
+ * the next step's (stream order).
  */
 int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* d_clock_list,
-                   int n, void* stream);
+                   int n, int slot, void* stream);
+
+/*
+ * One launch that closes the previous step and runs this step's detector:
+ * morph_nonfinite_or_multi over `grads` into d_state->found_inf[slot], and in
+ * one extra workgroup morph_step_end(d_state, d_clocks, d_prev_clock_list,
+ * n_prev, slot ^ 1).  The two touch disjoint words (the close reads and clears
+ * only found_inf[slot ^ 1]), so their workgroups may run in any order.  This
+ * saves the close's own launch on every step that runs the detector.
+ */
+int morph_nonfinite_or_close(const void* const* grads, const int64_t* numels, int count,
+                             int dtype, morph_step_state* d_state, int slot, int64_t* d_clocks,
+                             const int32_t* d_prev_clock_list, int n_prev, void* stream);
 
 /* ---- Stage-gradient accumulation ------------------------------------------
  * Replaces the reference's per-micro-batch

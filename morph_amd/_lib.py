@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmorph_optim.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_NONE, DTYPE_F32, DTYPE_F16, DTYPE_BF16 = -1, 0, 1, 2
 HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
@@ -22,7 +22,8 @@ HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
 EXPORTS = (
     "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
-    "morph_adamw_multi_dev", "morph_step_end", "morph_grad_partials", "morph_grad_accumulate",
+    "morph_adamw_multi_dev", "morph_step_end", "morph_nonfinite_or_close",
+    "morph_grad_partials", "morph_grad_accumulate",
     "morph_sumsq_total", "morph_convert_f32", "morph_fp8_pack", "morph_fp8_unpack",
     "morph_gemm_nt_bf16",
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
@@ -57,12 +58,13 @@ class AdamwTensor(ctypes.Structure):
 
 
 class StepState(ctypes.Structure):
-    """morph_step_state (device-resident step control, 64 bytes)."""
+    """morph_step_state (device-resident step control, 72 bytes)."""
     _fields_ = [("scale", ctypes.c_double), ("scale_cap", ctypes.c_double),
                 ("good_steps", ctypes.c_int64), ("growth_interval", ctypes.c_int64),
                 ("applied", ctypes.c_int64), ("skipped", ctypes.c_int64),
-                ("found_inf", ctypes.c_uint32), ("fatal", ctypes.c_uint32),
-                ("last_found_inf", ctypes.c_uint32), ("dynamic", ctypes.c_uint32)]
+                ("found_inf", ctypes.c_uint32 * 2), ("fatal", ctypes.c_uint32),
+                ("last_found_inf", ctypes.c_uint32), ("dynamic", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32)]
 
 
 class AdamwSched(ctypes.Structure):
@@ -115,8 +117,9 @@ def lib():
                                    ctypes.POINTER(AdamwHP), i32, vp, vp], i32),
             "morph_adamw_multi_dev": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
                                        ctypes.POINTER(AdamwHP), ctypes.POINTER(AdamwSched), i32,
-                                       vp, vp, vp], i32),
-            "morph_step_end": ([vp, vp, vp, i32, vp], i32),
+                                       vp, vp, i32, vp], i32),
+            "morph_step_end": ([vp, vp, vp, i32, i32, vp], i32),
+            "morph_nonfinite_or_close": ([vp, vp, i32, i32, vp, i32, vp, vp, i32, vp], i32),
             "morph_grad_partials": ([ctypes.POINTER(AccumTensor), i32], i64),
             "morph_grad_accumulate": ([ctypes.POINTER(AccumTensor), i32, i32, ctypes.c_double, i32,
                                        vp, vp, i64, vp], i32),

@@ -1,10 +1,12 @@
 """Device-resident step control: loss-scale state, step clocks, bias-correction tables.
 
 With these in HBM the optimizer step needs no host round trip: the detector
-writes found_inf into the state block, the AdamW kernel reads the scale, the
-skip decision and each tensor's clock from it, and morph_step_end advances the
-loss scale and the clocks.  The host mirrors (DynamicLossScale, per-tensor
-step counts) are refreshed only when the caller asks (resolve()).
+writes found_inf[slot] into the state block, the AdamW kernel reads the scale,
+the skip decision and each tensor's clock from it, and the step's close
+advances the loss scale and the clocks.  Steps alternate between the two flag
+slots, so a step's close can ride in the next step's detector launch.  The
+host mirrors (DynamicLossScale, per-tensor step counts) are refreshed only
+when the caller asks (resolve()).
 """
 import ctypes
 import math
@@ -17,7 +19,7 @@ from .hyper import to_f32
 from .precision import DynamicLossScale
 
 STATE_BYTES = ctypes.sizeof(StepState)
-FOUND_INF_OFFSET = StepState.found_inf.offset
+FOUND_INF_OFFSET = StepState.found_inf.offset  # two uint32 words, one per slot
 
 
 class BiasTables:
@@ -67,14 +69,17 @@ class StepControl:
         self._initialized = False
         self.push_scale()
 
-    @property
-    def found_inf_ptr(self):
-        return self.state.data_ptr() + FOUND_INF_OFFSET
+    def found_inf_ptr(self, slot):
+        if slot not in (0, 1):
+            raise ValueError("slot must be 0 or 1")
+        return self.state.data_ptr() + FOUND_INF_OFFSET + 4 * slot
 
-    @property
-    def found_inf_view(self):
-        """found_inf as a 1-element int32 view of the state block."""
-        return self.state[FOUND_INF_OFFSET:FOUND_INF_OFFSET + 4].view(torch.int32)
+    def found_inf_view(self, slot):
+        """found_inf[slot] as a 1-element int32 view of the state block."""
+        if slot not in (0, 1):
+            raise ValueError("slot must be 0 or 1")
+        at = FOUND_INF_OFFSET + 4 * slot
+        return self.state[at:at + 4].view(torch.int32)
 
     def _scale_fields(self):
         s = self.loss_scale

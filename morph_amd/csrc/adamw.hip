@@ -235,7 +235,8 @@ __device__ __forceinline__ bool control(const LaunchArgs& a, const TensorArg& T,
                                         const uint32_t* skip, morph_adamw_hp& hp) {
   hp = a.hp[T.hp];
   if constexpr (kDev) {
-    if ((a.state->found_inf | a.state->fatal) != 0u) return false;
+    // skip = &state->found_inf[slot], this step's flag word
+    if ((*skip | a.state->fatal) != 0u) return false;
     // Step-dependent constants from device state, in the host's double arithmetic.
     const morph_adamw_sched& S = a.sched[T.hp];
     const int64_t t = a.clocks[T.clock] + 1;
@@ -415,10 +416,10 @@ extern "C" int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int coun
                                      int out_dtype, const morph_adamw_hp* hps,
                                      const morph_adamw_sched* scheds, int n_hp,
                                      const int64_t* d_clocks, const morph_step_state* d_state,
-                                     void* stream) {
-  if (d_state == nullptr) return MORPH_EINVAL;
+                                     int slot, void* stream) {
+  if (d_state == nullptr || (slot != 0 && slot != 1)) return MORPH_EINVAL;
   return enqueue(tensors, count, grad_dtype, out_dtype, hps, scheds, n_hp, d_clocks, d_state,
-                 nullptr, stream);
+                 &d_state->found_inf[slot], stream);
 }
 
 extern "C" int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp_avg,

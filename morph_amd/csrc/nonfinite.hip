@@ -12,7 +12,13 @@
 // writes 1 to the flag with a plain vector store (every writer writes the
 // same value, so the race is benign).  Nothing is ever written on a clean
 // pass, so detector calls over several tensors OR into one flag.
+//
+// morph_nonfinite_or_close adds one workgroup past the detector's blocks that
+// closes the previous optimizer step (close_step), which saves that close its
+// own launch.  It reads and clears only the other step's flag word, so the
+// detector workgroups and the close may run in any order.
 #include "common.h"
+#include "step_close.h"
 
 #ifndef MORPH_NONFINITE_UNROLL
 #define MORPH_NONFINITE_UNROLL 4
@@ -61,12 +67,28 @@ __device__ __forceinline__ bool elem_nonfinite(const void* g, int64_t i) {
     return word_nonfinite<GT>(static_cast<const uint16_t*>(g)[i]);
 }
 
-template <typename GT>
+// The previous step's close, carried by the detector launch of the next one.
+struct CloseArgs {
+  morph_step_state* state;
+  int64_t* clocks;
+  const int32_t* list;
+  int32_t n;
+  int32_t slot;
+};
+
+template <typename GT, bool kClose>
 __global__ __launch_bounds__(kBlock) void nonfinite_kernel(const LaunchArgs a,
-                                                           uint32_t* __restrict__ flag) {
+                                                           uint32_t* __restrict__ flag,
+                                                           const CloseArgs c) {
   constexpr int kElemBytes = Fmt<GT>::bytes;
   constexpr int kPerBlock = kBytesPerBlock / kElemBytes;
   const int b = blockIdx.x;
+  if constexpr (kClose) {
+    if (b == (int)gridDim.x - 1) {  // one workgroup past the detector's blocks
+      close_step(c.state, c.clocks, c.list, c.n, c.slot, kBlock);
+      return;
+    }
+  }
   const TensorArg& T = a.t[segment_of(a.t, a.count, b)];
   const int64_t base = (int64_t)(b - T.first_block) * kPerBlock;
   bool bad = false;
@@ -89,16 +111,24 @@ __global__ __launch_bounds__(kBlock) void nonfinite_kernel(const LaunchArgs a,
 }
 
 template <typename GT>
-int launch(const LaunchArgs& a, int blocks, uint32_t* flag, hipStream_t s) {
-  hipLaunchKernelGGL((nonfinite_kernel<GT>), dim3(blocks), dim3(kBlock), 0, s, a, flag);
+int launch(const LaunchArgs& a, int blocks, uint32_t* flag, const CloseArgs* close,
+           hipStream_t s) {
+  if (close != nullptr)
+    hipLaunchKernelGGL((nonfinite_kernel<GT, true>), dim3(blocks + 1), dim3(kBlock), 0, s, a,
+                       flag, *close);
+  else
+    hipLaunchKernelGGL((nonfinite_kernel<GT, false>), dim3(blocks), dim3(kBlock), 0, s, a, flag,
+                       CloseArgs{});
   return launch_status();
 }
 
-int dispatch(int dtype, const LaunchArgs& a, int blocks, uint32_t* flag, hipStream_t s) {
+// `close` (nullable) rides in this launch as one extra workgroup.
+int dispatch(int dtype, const LaunchArgs& a, int blocks, uint32_t* flag, const CloseArgs* close,
+             hipStream_t s) {
   switch (dtype) {
-    case MORPH_DTYPE_F32: return launch<F32>(a, blocks, flag, s);
-    case MORPH_DTYPE_F16: return launch<F16>(a, blocks, flag, s);
-    case MORPH_DTYPE_BF16: return launch<BF16>(a, blocks, flag, s);
+    case MORPH_DTYPE_F32: return launch<F32>(a, blocks, flag, close, s);
+    case MORPH_DTYPE_F16: return launch<F16>(a, blocks, flag, close, s);
+    case MORPH_DTYPE_BF16: return launch<BF16>(a, blocks, flag, close, s);
     default: return MORPH_EDTYPE;
   }
 }
@@ -118,10 +148,12 @@ extern "C" int morph_flag_clear(uint32_t* d_flag, void* stream) {
   return launch_status();
 }
 
-extern "C" int morph_nonfinite_or_multi(const void* const* grads, const int64_t* numels, int count,
-                                        int dtype, uint32_t* d_flag, void* stream) {
-  if (d_flag == nullptr || count < 0 || (count > 0 && (grads == nullptr || numels == nullptr)))
-    return MORPH_EINVAL;
+namespace {
+
+// Detector over `count` tensors into d_flag; `close` (nullable) rides in the
+// first launch (or in a launch of its own when there is nothing to scan).
+int nonfinite_impl(const void* const* grads, const int64_t* numels, int count, int dtype,
+                   uint32_t* d_flag, const CloseArgs* close, hipStream_t s) {
   int eb;
   switch (dtype) {
     case MORPH_DTYPE_F32: eb = 4; break;
@@ -133,15 +165,15 @@ extern "C" int morph_nonfinite_or_multi(const void* const* grads, const int64_t*
     if (numels[i] < 0 || (numels[i] > 0 && grads[i] == nullptr)) return MORPH_EINVAL;
   const int per_block = kBytesPerBlock / eb;
   const int64_t max_seg = kMaxSegmentBytes / eb;
-  hipStream_t s = as_stream(stream);
   LaunchArgs a;
   a.count = 0;
   int blocks = 0;
   for (int i = 0; i < count; ++i) {
     for (int64_t off = 0; off < numels[i]; off += max_seg) {
       if (a.count == kMaxTensors) {
-        const int rc = dispatch(dtype, a, blocks, d_flag, s);
+        const int rc = dispatch(dtype, a, blocks, d_flag, close, s);
         if (rc != MORPH_OK) return rc;
+        close = nullptr;
         a.count = 0;
         blocks = 0;
       }
@@ -154,8 +186,30 @@ extern "C" int morph_nonfinite_or_multi(const void* const* grads, const int64_t*
       blocks += (int)((n + per_block - 1) / per_block);
     }
   }
-  if (a.count == 0) return MORPH_OK;
-  return dispatch(dtype, a, blocks, d_flag, s);
+  if (a.count == 0 && close == nullptr) return MORPH_OK;
+  return dispatch(dtype, a, blocks, d_flag, close, s);
+}
+
+}  // namespace
+
+extern "C" int morph_nonfinite_or_multi(const void* const* grads, const int64_t* numels, int count,
+                                        int dtype, uint32_t* d_flag, void* stream) {
+  if (d_flag == nullptr || count < 0 || (count > 0 && (grads == nullptr || numels == nullptr)))
+    return MORPH_EINVAL;
+  return nonfinite_impl(grads, numels, count, dtype, d_flag, nullptr, as_stream(stream));
+}
+
+extern "C" int morph_nonfinite_or_close(const void* const* grads, const int64_t* numels, int count,
+                                        int dtype, morph_step_state* d_state, int slot,
+                                        int64_t* d_clocks, const int32_t* d_prev_clock_list,
+                                        int n_prev, void* stream) {
+  if (d_state == nullptr || count < 0 || (count > 0 && (grads == nullptr || numels == nullptr)) ||
+      (slot != 0 && slot != 1) || n_prev < 0 ||
+      (n_prev > 0 && (d_clocks == nullptr || d_prev_clock_list == nullptr)))
+    return MORPH_EINVAL;
+  const CloseArgs close{d_state, d_clocks, d_prev_clock_list, n_prev, slot ^ 1};
+  return nonfinite_impl(grads, numels, count, dtype, &d_state->found_inf[slot], &close,
+                        as_stream(stream));
 }
 
 extern "C" int morph_nonfinite_or(const void* grad, int dtype, int64_t n, uint32_t* d_flag,

@@ -1,16 +1,10 @@
-// Device-resident close of an optimizer step: DynamicLossScale's state machine
-// (streamtrain/precision.py:6-17) and the per-tensor step clocks, evaluated on
-// the GPU so a training loop never waits for the skip decision.
-//
-// One workgroup.  Every lane reads the step's found_inf / fatal before lane 0
-// changes the scalar state (a barrier separates the two); the clocks of the
-// tensors stepped in this step advance only when the step was applied.  The
-// arithmetic is the reference's, in double: overflow -> raise at scale <= 1
-// (here: set fatal bit 0, change nothing), else scale = max(1, scale / 2),
-// good_steps = 0; success -> good_steps += 1, and at growth_interval
-// scale = min(scale * 2, cap), good_steps = 0.  Halving and doubling are exact
-// in double, so the device sequence equals the host one bit for bit.
+// Device-resident close of an optimizer step as a launch of its own (one
+// workgroup), for steps whose close does not ride in the next step's
+// detector launch (morph_nonfinite_or_close): the last step before the host
+// reads the state, and steps whose non-finite flag came from the gradients'
+// producer.  The state machine is close_step (step_close.h).
 #include "common.h"
+#include "step_close.h"
 
 namespace morph {
 namespace {
@@ -18,42 +12,8 @@ namespace {
 constexpr int kBlock = 256;
 
 __global__ __launch_bounds__(kBlock) void step_end_kernel(morph_step_state* st, int64_t* clocks,
-                                                          const int32_t* list, int n) {
-  volatile morph_step_state* vs = st;
-  const uint32_t fatal = vs->fatal;
-  const uint32_t inf = vs->found_inf;
-  __syncthreads();
-  if (fatal != 0u) return;  // sticky: nothing advances after a fatal overflow
-  if (threadIdx.x == 0) {
-    const bool dynamic = vs->dynamic != 0u;
-    if (inf != 0u) {
-      vs->skipped = vs->skipped + 1;
-      const double scale = vs->scale;
-      if (!dynamic) {
-        // fixed scale: the step is skipped and nothing else changes
-      } else if (scale <= 1.0) {
-        vs->fatal = fatal | MORPH_FATAL_MIN_SCALE;
-      } else {
-        vs->scale = fmax(1.0, scale / 2.0);
-        vs->good_steps = 0;
-      }
-    } else if (!dynamic) {
-      vs->applied = vs->applied + 1;
-    } else {
-      vs->applied = vs->applied + 1;
-      const int64_t good = vs->good_steps + 1;
-      if (good >= vs->growth_interval) {
-        vs->scale = fmin(vs->scale * 2.0, vs->scale_cap);
-        vs->good_steps = 0;
-      } else {
-        vs->good_steps = good;
-      }
-    }
-    vs->last_found_inf = inf;
-    vs->found_inf = 0u;
-  }
-  if (inf == 0u)
-    for (int i = threadIdx.x; i < n; i += kBlock) clocks[list[i]] += 1;
+                                                          const int32_t* list, int n, int slot) {
+  close_step(st, clocks, list, n, slot, kBlock);
 }
 
 }  // namespace
@@ -62,10 +22,11 @@ __global__ __launch_bounds__(kBlock) void step_end_kernel(morph_step_state* st, 
 using namespace morph;
 
 extern "C" int morph_step_end(morph_step_state* d_state, int64_t* d_clocks,
-                              const int32_t* d_clock_list, int n, void* stream) {
-  if (d_state == nullptr || n < 0 || (n > 0 && (d_clocks == nullptr || d_clock_list == nullptr)))
+                              const int32_t* d_clock_list, int n, int slot, void* stream) {
+  if (d_state == nullptr || n < 0 || (n > 0 && (d_clocks == nullptr || d_clock_list == nullptr)) ||
+      (slot != 0 && slot != 1))
     return MORPH_EINVAL;
   hipLaunchKernelGGL(step_end_kernel, dim3(1), dim3(kBlock), 0, as_stream(stream), d_state,
-                     d_clocks, d_clock_list, n);
+                     d_clocks, d_clock_list, n, slot);
   return launch_status();
 }

@@ -136,11 +136,12 @@ class AdamwBatch:
                                       arr, len(hps), _ptr(skip_flag), stream_handle(stream)))
 
 
-    def launch_dev(self, hps, scheds, clocks, state, stream=None):
+    def launch_dev(self, hps, scheds, clocks, state, slot=0, stream=None):
         """Enqueue the device-resident form (morph_adamw_multi_dev).
 
         scheds: AdamwSched per constant set; clocks: device int64 tensor;
-        state: device tensor holding a morph_step_state.
+        state: device tensor holding a morph_step_state; slot: the step's
+        found_inf word (0 or 1).
         """
         if self.count == 0:
             return
@@ -154,18 +155,41 @@ class AdamwBatch:
         sarr = (_lib.AdamwSched * len(scheds))(*scheds)
         check(lib().morph_adamw_multi_dev(self.array, self.count, self.grad_dtype,
                                           self.out_dtype, harr, sarr, len(hps), _ptr(clocks),
-                                          _ptr(state), stream_handle(stream)))
+                                          _ptr(state), slot, stream_handle(stream)))
 
 
-def step_end(state, clocks, clock_list, stream=None):
-    """Enqueue morph_step_end (clock_list: device int32 tensor of distinct indices)."""
+def _check_close_args(state, clocks, clock_list):
     require_device_tensor(state, "state")
     require_device_tensor(clocks, "clocks")
     require_device_tensor(clock_list, "clock_list")
     if clock_list.dtype != torch.int32 or clocks.dtype != torch.int64:
         raise TypeError("clock_list must be int32 and clocks int64")
+
+
+def step_end(state, clocks, clock_list, slot=0, stream=None):
+    """Enqueue morph_step_end (clock_list: device int32 tensor of distinct indices)."""
+    _check_close_args(state, clocks, clock_list)
     check(lib().morph_step_end(_ptr(state), _ptr(clocks), _ptr(clock_list), clock_list.numel(),
-                               stream_handle(stream)))
+                               slot, stream_handle(stream)))
+
+
+def nonfinite_or_close(grads, state, slot, clocks, prev_clock_list, stream=None):
+    """One launch: the detector over `grads` into found_inf[slot] of `state`, and the
+    close of the previous step (slot ^ 1, clocks prev_clock_list) in one extra workgroup
+    (morph_nonfinite_or_close).  All gradients must share one dtype."""
+    _check_close_args(state, clocks, prev_clock_list)
+    dtypes = {g.dtype for g in grads}
+    if len(dtypes) > 1:
+        raise ValueError(f"one launch takes one gradient dtype, got {dtypes}")
+    for i, g in enumerate(grads):
+        require_device_tensor(g, f"grads[{i}]")
+    n = len(grads)
+    ptrs = (ctypes.c_void_p * max(n, 1))(*[g.data_ptr() for g in grads])
+    sizes = (ctypes.c_int64 * max(n, 1))(*[g.numel() for g in grads])
+    dtype = dtype_code(next(iter(dtypes))) if n else _lib.DTYPE_F32
+    check(lib().morph_nonfinite_or_close(ptrs, sizes, n, dtype, _ptr(state), slot, _ptr(clocks),
+                                         _ptr(prev_clock_list), prev_clock_list.numel(),
+                                         stream_handle(stream)))
 
 
 def adamw_step(param, exp_avg, exp_avg_sq, grad, hp, out=None, skip_flag=None, stream=None):

@@ -10,9 +10,11 @@ optimizer.py:49-51 driving a conditional skip and DynamicLossScale
 (precision.py:6-17).  Parameters whose gradient is None are not touched and
 their step clock does not advance (sparse_disk.py:1-5, torch's own rule).
 
-A step is three kernels on the caller's stream -- detector, fused AdamW,
-step close -- driven by device-resident state (morph_amd.control), so no step
-waits for the host.  The host copies of the clocks and of the loss scale are
+A step is two launches on the caller's stream -- the detector (which also
+closes the previous step: loss scale, clocks) and the fused AdamW pass --
+driven by device-resident state (morph_amd.control), so no step waits for the
+host.  The last step's close is enqueued when the host next needs the state
+(resolve()) or when the next step has no detector pass of its own.  The host copies of the clocks and of the loss scale are
 refreshed by resolve(); with sync=True (or on_overflow="raise") every step
 resolves and reports its outcome like the reference does.
 """
@@ -102,6 +104,8 @@ class FusedAdamW:
         self._bound = [0] * len(flat)  # upper bound of each device clock
         self._cache_key = None
         self._cache = None
+        self._slot = 0          # found_inf word of the next step (steps alternate)
+        self._pending = None    # (slot, clock_list, stream) of a step whose close is not enqueued
         self.kernel_timer = None  # optional list: (start, end) events around each AdamW launch
         self.skipped_steps = 0
         self.applied_steps = 0
@@ -112,11 +116,12 @@ class FusedAdamW:
 
     @property
     def found_inf(self):
-        """The step's non-finite flag in the device step state, as a 1-element int32
-        tensor.  A producer that already tests every gradient (the final pass of
-        StageGradients.accumulate(..., found_inf=opt.found_inf)) can set it and
-        call step(..., checked=True), which then skips the detector pass."""
-        return self._ctl.found_inf_view
+        """The next step's non-finite flag in the device step state, as a 1-element
+        int32 tensor.  A producer that already tests every gradient (the final pass of
+        StageGradients.accumulate(..., found_inf=opt.found_inf)) can set it and call
+        step(..., checked=True), which then skips the detector pass.  Steps alternate
+        between two flag words: read this property anew before every step."""
+        return self._ctl.found_inf_view(self._slot)
 
     # -- helpers -----------------------------------------------------------
     @torch.no_grad()
@@ -207,7 +212,9 @@ class FusedAdamW:
     # -- the step ----------------------------------------------------------
     @torch.no_grad()
     def step(self, grads=None, stream=None, checked=False):
-        """Enqueue one optimizer step (detector, fused AdamW, step close).
+        """Enqueue one optimizer step: the detector (carrying the previous step's
+        close), then the fused AdamW pass.  This step's close follows with the next
+        step's detector, or on its own at resolve() or before a checked step.
 
         grads: one tensor (or None) per parameter in param-group order; by
         default p.grad.  checked=True: every gradient's non-finite test is
@@ -229,18 +236,32 @@ class FusedAdamW:
             self._ctl.push_scale()
         batch, clock_list, hps, scheds = self._prepare(grads, present)
         ctl = self._ctl
-        if not checked:
-            kernels.nonfinite_or([grads[i] for i in present], ctl.found_inf_ptr, stream)
+        slot = self._slot
+        s = stream or torch.cuda.current_stream(self.device)
+        if self._pending is not None and self._pending[2] != s:
+            # the previous step ran on another stream: close it there, and order
+            # this step after that close
+            prev = self._pending[2]
+            self._flush_close()
+            s.wait_stream(prev)
+        if checked:
+            self._flush_close()
+        elif self._pending is not None:
+            kernels.nonfinite_or_close([grads[i] for i in present], ctl.state, slot, ctl.clocks,
+                                       self._pending[1], s)
+            self._pending = None
+        else:
+            kernels.nonfinite_or([grads[i] for i in present], ctl.found_inf_ptr(slot), s)
         if self.kernel_timer is not None:
-            s = stream or torch.cuda.current_stream()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, stream)
+            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s)
             e1.record(s)
             self.kernel_timer.append((e0, e1))
         else:
-            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, stream)
-        kernels.step_end(ctl.state, ctl.clocks, clock_list, stream)
+            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s)
+        self._pending = (slot, clock_list, s)
+        self._slot = slot ^ 1
         for i in present:
             self._bound[i] += 1
         if not self.sync:
@@ -250,6 +271,14 @@ class FusedAdamW:
             raise FloatingPointError("nonfinite gradient; optimizer not updated")
         return not st.last_found_inf
 
+    def _flush_close(self):
+        """Enqueue the pending step's close on that step's stream, on its own."""
+        if self._pending is None:
+            return
+        slot, clock_list, s = self._pending
+        self._pending = None
+        kernels.step_end(self._ctl.state, self._ctl.clocks, clock_list, slot, s)
+
     def resolve(self):
         """Wait for enqueued steps; refresh clocks, counters and the host loss scale.
 
@@ -257,6 +286,11 @@ class FusedAdamW:
         reference raises there; on the device that step and every later one
         changed nothing).
         """
+        if self._pending is not None:
+            s = self._pending[2]
+            self._flush_close()
+            if s != torch.cuda.current_stream(self.device):
+                s.synchronize()
         st = self._ctl.read()
         clocks = self._ctl.clocks.cpu().tolist()
         for i, (_, p) in enumerate(self._flat()):

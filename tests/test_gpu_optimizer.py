@@ -326,6 +326,126 @@ def test_new_gradient_buffers_swap_pointers_only():
     with pytest.raises(ValueError):
         a._cache[0].rebind_grads([torch.zeros(10, dtype=torch.half, device=DEV), held[1]])
 
+
+@pytest.mark.parametrize("prev_inf,now_inf,scale,count", [
+    (0, 0, 1024.0, 2), (1, 0, 1024.0, 2), (0, 1, 1024.0, 2), (1, 1, 1024.0, 2),
+    (1, 0, 1.0, 2), (0, 0, 2.0 ** 15, 0), (1, 0, 512.0, 0)],
+    ids=["clean", "prev-overflow", "now-overflow", "both", "fatal", "close-only", "close-only-inf"])
+def test_fused_detector_close_equals_separate_launches(prev_inf, now_inf, scale, count):
+    """morph_nonfinite_or_close(slot) leaves the state block and the clocks byte-identical
+    to morph_step_end(slot ^ 1) followed by the detector into found_inf[slot]."""
+    from morph_amd import kernels
+    from morph_amd.control import StepControl
+    gen = torch.Generator().manual_seed(80)
+    grads = [torch.randn(1000 + 37 * k, generator=gen).half() for k in range(count)]
+    if now_inf:
+        grads[0][17] = float("inf")
+    grads = [g.to(DEV) for g in grads]
+    blocks = []
+    for fused in (False, True):
+        ctl = StepControl(DEV, 4, DynamicLossScale(scale, growth_interval=3))
+        st = ctl.read()
+        st.good_steps = 2  # the next success grows the scale
+        st.found_inf[1] = prev_inf
+        ctl.state.copy_(torch.frombuffer(bytearray(bytes(st)), dtype=torch.uint8))
+        ctl.clocks.copy_(torch.tensor([5, 6, 7, 8]))
+        clock_list = torch.tensor([0, 2, 3], dtype=torch.int32, device=DEV)
+        if fused:
+            kernels.nonfinite_or_close(grads, ctl.state, 0, ctl.clocks, clock_list)
+        else:
+            kernels.step_end(ctl.state, ctl.clocks, clock_list, slot=1)
+            kernels.nonfinite_or(grads, ctl.found_inf_ptr(0))
+        torch.cuda.synchronize()
+        blocks.append((ctl.state.cpu(), ctl.clocks.cpu(), ctl.read()))
+    (sa, ca, a), (sb, cb, b) = blocks
+    assert torch.equal(sa, sb) and torch.equal(ca, cb)
+    assert b.found_inf[0] == now_inf and b.found_inf[1] == 0
+    assert b.last_found_inf == prev_inf
+    if prev_inf and scale <= 1.0:
+        assert b.fatal == 1 and cb.tolist() == [5, 6, 7, 8]
+    elif prev_inf:
+        assert b.scale == scale / 2 and b.skipped == 1 and cb.tolist() == [5, 6, 7, 8]
+    else:
+        assert b.scale == min(2 * scale, 65536.0) and b.applied == 1
+        assert cb.tolist() == [6, 6, 8, 9]
+
+
+def test_steps_on_alternating_streams_equal_one_stream(golden_dir):
+    """A pending step close is enqueued on the stream of its own step when the next step
+    runs on another stream: 16 config-4 steps alternating between two streams (each
+    waiting for the other) end where the step-by-step run ends."""
+    cfg = json.loads((golden_dir / "loss_scale.json").read_text())["config4"]
+    shapes = [(512, 256), (1000,)]
+    masters = [torch.randn(s, generator=torch.Generator().manual_seed(90 + i)) * .02
+               for i, s in enumerate(shapes)]
+    streams = [torch.cuda.Stream(DEV), torch.cuda.Stream(DEV)]
+    runs = []
+    for alternate in (False, True):
+        scaler = DynamicLossScale(cfg["initial"], cfg["growth_interval"])
+        opt = FusedAdamW([m.to(DEV) for m in masters], lr=3e-4, betas=(.9, .95),
+                         weight_decay=.1, loss_scale=scaler, export_dtype=torch.float16,
+                         sync=not alternate)
+        rng = np.random.RandomState(46)
+        for t in range(1, cfg["steps"] + 1):
+            grads = [g.to(DEV) for g in _config4_grads(shapes, rng, t, cfg["scale_before_step"][t - 1],
+                                                       cfg["overflow_steps"])]
+            if alternate:
+                s = streams[t % 2]
+                s.wait_stream(torch.cuda.current_stream(DEV))
+                s.wait_stream(streams[(t + 1) % 2])
+                opt.step(grads, stream=s)
+                for g in grads:
+                    g.record_stream(s)
+            else:
+                opt.step(grads)
+        torch.cuda.current_stream(DEV).wait_stream(streams[0])
+        torch.cuda.current_stream(DEV).wait_stream(streams[1])
+        opt.resolve()
+        runs.append((opt, scaler))
+    (a, sa), (b, sb) = runs
+    assert sa.state_dict() == sb.state_dict() and sb.scale == cfg["final_scale"]
+    assert a.skipped_steps == b.skipped_steps == 3
+    for p, q in zip(a.param_groups[0]["params"], b.param_groups[0]["params"]):
+        assert torch.equal(p, q)
+        assert torch.equal(a.state[p]["exp_avg_sq"], b.state[q]["exp_avg_sq"])
+        assert a.state[p]["step"] == b.state[q]["step"] == 13
+
+
+def test_checked_and_detector_steps_interleave(golden_dir):
+    """Steps whose flag comes from the producer (checked=True, flag written into
+    opt.found_inf) interleaved with steps that run the detector, overflows on both
+    kinds: the same bytes, clocks and scale as the step-by-step run."""
+    cfg = json.loads((golden_dir / "loss_scale.json").read_text())["config4"]
+    shapes = [(384, 200), (777,)]
+    masters = [torch.randn(s, generator=torch.Generator().manual_seed(95 + i)) * .02
+               for i, s in enumerate(shapes)]
+    runs = []
+    for sync in (True, False):
+        scaler = DynamicLossScale(cfg["initial"], cfg["growth_interval"])
+        opt = FusedAdamW([m.to(DEV) for m in masters], lr=3e-4, betas=(.9, .95),
+                         weight_decay=.1, loss_scale=scaler, export_dtype=torch.bfloat16, sync=sync)
+        rng = np.random.RandomState(47)
+        for t in range(1, cfg["steps"] + 1):
+            grads = [g.to(DEV) for g in _config4_grads(shapes, rng, t, cfg["scale_before_step"][t - 1],
+                                                       cfg["overflow_steps"])]
+            if t % 3 == 0:  # the producer tested the gradients
+                bad = any(not torch.isfinite(g).all() for g in grads)
+                if bad:
+                    opt.found_inf.fill_(1)
+                opt.step(grads, checked=True)
+            else:
+                opt.step(grads)
+        opt.resolve()
+        runs.append((opt, scaler))
+    (a, sa), (b, sb) = runs
+    assert sa.state_dict() == sb.state_dict() and sb.scale == cfg["final_scale"]
+    assert a.skipped_steps == b.skipped_steps == 3 and b.applied_steps == 13
+    for p, q in zip(a.param_groups[0]["params"], b.param_groups[0]["params"]):
+        assert torch.equal(p, q)
+        assert torch.equal(a.state[p]["exp_avg"], b.state[q]["exp_avg"])
+    for e, f in zip(a.exports, b.exports):
+        assert torch.equal(e, f)
+
 def _config4_grads(shapes, rng, t, scale, overflow_steps):
     grads = bench.config2_grads("cpu", 2000 + t, shapes, scale=scale)
     if t in overflow_steps:
