@@ -446,6 +446,33 @@ def test_checked_and_detector_steps_interleave(golden_dir):
     for e, f in zip(a.exports, b.exports):
         assert torch.equal(e, f)
 
+
+def test_fused_close_with_a_detector_over_several_launches():
+    """400 tensors need three detector launches (160 tensors each) and nine AdamW
+    launches; the previous step's close rides in exactly one of them.  Eight steps,
+    two of them poisoned in the last launch's tensors, end where the step-by-step run ends."""
+    gen = torch.Generator().manual_seed(97)
+    sizes = [int(torch.randint(1, 3000, (1,), generator=gen)) for _ in range(400)]
+    masters = [torch.randn(n, generator=gen) * .02 for n in sizes]
+    steps = [[(torch.randn(n, generator=gen) * 1e-3 * 256).half() for n in sizes] for _ in range(8)]
+    steps[2][395][0] = float("nan")
+    steps[5][399][-1] = float("-inf")
+    runs = []
+    for sync in (True, False):
+        scaler = DynamicLossScale(256.0, growth_interval=3)
+        opt = FusedAdamW([m.to(DEV) for m in masters], lr=1e-3, betas=(.9, .95), weight_decay=.1,
+                         loss_scale=scaler, sync=sync)
+        for gs in steps:
+            opt.step([g.to(DEV) for g in gs])
+        opt.resolve()
+        runs.append((opt, scaler))
+    (a, sa), (b, sb) = runs
+    assert sa.state_dict() == sb.state_dict()
+    assert a.skipped_steps == b.skipped_steps == 2 and b.applied_steps == 6
+    for p, q in zip(a.param_groups[0]["params"], b.param_groups[0]["params"]):
+        assert torch.equal(p, q)
+        assert a.state[p]["step"] == b.state[q]["step"] == 6
+
 def _config4_grads(shapes, rng, t, scale, overflow_steps):
     grads = bench.config2_grads("cpu", 2000 + t, shapes, scale=scale)
     if t in overflow_steps:
