@@ -13,9 +13,8 @@
 // same value, so the race is benign).  Nothing is ever written on a clean
 // pass, so detector calls over several tensors OR into one flag.
 //
-// morph_nonfinite_or_close adds one workgroup past the detector's blocks that
-// closes the previous optimizer step (close_step), which saves that close its
-// own launch.  It reads and clears only the other step's flag word, so the
+// morph_nonfinite_or_close adds one workgroup (the first) that closes the
+// previous optimizer step (close_step), which saves that close its own launch.  It reads and clears only the other step's flag word, so the
 // detector workgroups and the close may run in any order.
 #include "common.h"
 #include "step_close.h"
@@ -82,12 +81,15 @@ __global__ __launch_bounds__(kBlock) void nonfinite_kernel(const LaunchArgs a,
                                                            const CloseArgs c) {
   constexpr int kElemBytes = Fmt<GT>::bytes;
   constexpr int kPerBlock = kBytesPerBlock / kElemBytes;
-  const int b = blockIdx.x;
+  int b = blockIdx.x;
   if constexpr (kClose) {
-    if (b == (int)gridDim.x - 1) {  // one workgroup past the detector's blocks
+    // Workgroup 0 closes the previous step: dispatched first, its chain of
+    // dependent accesses runs under the scan instead of after it.
+    if (b == 0) {
       close_step(c.state, c.clocks, c.list, c.n, c.slot, kBlock);
       return;
     }
+    b -= 1;
   }
   const TensorArg& T = a.t[segment_of(a.t, a.count, b)];
   const int64_t base = (int64_t)(b - T.first_block) * kPerBlock;
