@@ -14,8 +14,8 @@ muon (config 5), grads, window, fp8.
 
 Prints one JSON line.  `value` is whole-step throughput in Gparams/s;
 `roofline` is the fused AdamW kernel's algorithmic bandwidth (28 bytes per
-parameter) over its average launch time, measured with HIP events on the
-launch stream; `cpu_baseline` times torch.optim.AdamW(foreach=False) -- the
+parameter) over its average launch time in the timed steps, from HIP events
+that each launch's dispatch stamps on the launch stream; `cpu_baseline` times torch.optim.AdamW(foreach=False) -- the
 library the reference's AdamW group runs -- on this host's cores.
 """
 import argparse
@@ -98,13 +98,15 @@ def time_gpu(steps, warmup):
 
     Each step takes the next of GRAD_SETS gradient sets, so no step finds its
     gradients left in the Infinity Cache by an earlier one (one reused buffer
-    would flatter the step without a detector pass by about 10 us).  The K
-    timed steps carry no instrumentation (HIP events around a launch add about
-    6 us per step on the GPU); the AdamW launch duration comes from HIP events
-    around each launch of K further steps, run right after.  K more steps with
-    checked=True time the step without the detector pass.
+    would flatter the step without a detector pass by about 10 us).  The AdamW
+    launch of every timed step is timed by HIP events that its own dispatch
+    stamps (hipExtLaunchKernel's start/stop events on the launch stream).  Any
+    timing events cost the step about 5 us (255.5 vs 260.7 us on one box), so
+    K more steps without them follow (`step_uninstrumented`), then K steps
+    with checked=True, the step without the detector pass.
     """
     from morph_amd import DynamicLossScale, FusedAdamW
+    from morph_amd.kernels import DispatchTimer
 
     device = torch.device("cuda", 0)
     masters = config2_window(device)
@@ -115,18 +117,20 @@ def time_gpu(steps, warmup):
     for t in range(max(warmup, GRAD_SETS)):
         opt.step(sets[t % GRAD_SETS])
     opt.resolve()
+    timer = opt.dispatch_timer = DispatchTimer(steps, device)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for t in range(steps):
         opt.step(sets[t % GRAD_SETS])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    timer = opt.kernel_timer = []
+    opt.dispatch_timer = None
+    kernel_ms = timer.elapsed_ms()
+    t0 = time.perf_counter()
     for t in range(steps):
         opt.step(sets[t % GRAD_SETS])
     torch.cuda.synchronize()
-    opt.kernel_timer = None
-    kernel_ms = [a.elapsed_time(b) for a, b in timer]
+    elapsed_plain = time.perf_counter() - t0
     # The same step when the gradients' producer has already set the step's
     # non-finite flag (StageGradients.accumulate(..., final=True,
     # found_inf=opt.found_inf)): fused AdamW + step close, no detector pass.
@@ -138,7 +142,7 @@ def time_gpu(steps, warmup):
     opt.resolve()
     if opt.skipped_steps:
         raise RuntimeError(f"{opt.skipped_steps} steps skipped on synthetic finite gradients")
-    return dict(n=n, elapsed=elapsed, elapsed_checked=elapsed_checked,
+    return dict(n=n, elapsed=elapsed, elapsed_plain=elapsed_plain, elapsed_checked=elapsed_checked,
                 avg_kernel_s=sum(kernel_ms) / len(kernel_ms) / 1e3, kernel_ms=kernel_ms,
                 scale=scaler.scale, applied=opt.applied_steps)
 
@@ -581,8 +585,10 @@ def time_embedding(steps, warmup):
     """Config 3: the tied [65536, 3072] embedding, one tensor of 201,326,592 FP32 masters.
     Each step's BF16 gradient is nonzero only on rows drawn Zipf(1.1) from 4 x 1024 token IDs
     (N(0, 1e-3) there); every row still gets the dense update; wd 0, BF16 export.  A step is
-    detector + fused AdamW + step close, as in the config-2 workload."""
+    detector + fused AdamW + step close, as in the config-2 workload; the AdamW launches of the
+    timed steps are timed by dispatch-stamped events."""
     from morph_amd import FusedAdamW
+    from morph_amd.kernels import DispatchTimer
     device = torch.device("cuda", 0)
     w = torch.randn(EMBED_SHAPE, generator=torch.Generator(device=device).manual_seed(3),
                     device=device) * .02
@@ -596,18 +602,15 @@ def time_embedding(steps, warmup):
     for t in range(warmup):
         opt.step(sets[t % EMBED_GRAD_SETS])
     opt.resolve()
+    timer = opt.dispatch_timer = DispatchTimer(steps, device)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for t in range(steps):
         opt.step(sets[t % EMBED_GRAD_SETS])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    timer = opt.kernel_timer = []
-    for t in range(steps):
-        opt.step(sets[t % EMBED_GRAD_SETS])
-    torch.cuda.synchronize()
-    opt.kernel_timer = None
-    kernel_ms = [a.elapsed_time(b) for a, b in timer]
+    opt.dispatch_timer = None
+    kernel_ms = timer.elapsed_ms()
     opt.resolve()
     if opt.skipped_steps:
         raise RuntimeError(f"{opt.skipped_steps} steps skipped on synthetic finite gradients")
@@ -711,6 +714,7 @@ def time_overflow(reps):
     (2^16 -> 2^4 after four).  Fresh optimizers then give per-launch times and, step by
     step (sync=True), every decision and scale of the config's own 16 steps."""
     from morph_amd import DynamicLossScale, FusedAdamW
+    from morph_amd.kernels import DispatchTimer
     device = torch.device("cuda", 0)
     sets = config4_sequence(device)
     masters0 = config2_window(device)
@@ -737,14 +741,14 @@ def time_overflow(reps):
     if opt.skipped_steps != 3 * (reps + 1):
         raise RuntimeError(f"{opt.skipped_steps} skipped steps in {reps + 1} sequences")
     del opt
-    # per-launch AdamW times, applied vs skipped steps (HIP events around each launch)
+    # per-launch AdamW times, applied vs skipped steps (dispatch-stamped events)
     opt, _ = fresh()
-    timer = opt.kernel_timer = []
+    timer = opt.dispatch_timer = DispatchTimer(len(sets), device)
     for grads in sets:
         opt.step(grads)
     torch.cuda.synchronize()
-    opt.kernel_timer = None
-    kernel_us = [a.elapsed_time(b) * 1e3 for a, b in timer]
+    opt.dispatch_timer = None
+    kernel_us = [ms * 1e3 for ms in timer.elapsed_ms()]
     opt.resolve()
     # step by step: every decision and the scale before each step
     sopt, sscaler = fresh(sync=True)
@@ -876,11 +880,17 @@ def main():
                    "state_layout": "one arena: masters, moments, export (FusedAdamW(arena=True))",
                    "gradient_sets": GRAD_SETS},
         "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
+        "timing": "timed steps carry HIP events stamped by each AdamW dispatch "
+                  "(hipExtLaunchKernel, launch stream); the two step forms below carry none",
+        "step_uninstrumented": {
+            "gparams_per_s": round(n * args.steps / r["elapsed_plain"] / 1e9, 3),
+            "ms_per_step": round(r["elapsed_plain"] / args.steps * 1e3, 4),
+            "what": "the same step, K more times, without timing events"},
         "step_checked": {
             "gparams_per_s": round(n * args.steps / r["elapsed_checked"] / 1e9, 3),
             "ms_per_step": round(r["elapsed_checked"] / args.steps * 1e3, 4),
             "what": "fused AdamW + step close with the non-finite flag already set by the "
-                    "gradients' producer (step(checked=True)); no detector pass"},
+                    "gradients' producer (step(checked=True)); no detector pass; no timing events"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),

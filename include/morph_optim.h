@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 3
+#define MORPH_ABI_VERSION 4
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -209,11 +209,16 @@ int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dty
  * hps[] only the step-independent fields are used (clip, decay, lerp_weight,
  * beta2, one_minus_beta2, eps, flags minus MORPH_HP_DIVIDE_SCALE); scheds[]
  * parallels hps[].  Clocks are NOT advanced here: morph_step_end does that.
+ * start_event / stop_event (nullable hipEvent_t, created by the caller): the
+ * call's first kernel dispatch stamps start_event with its start and the last
+ * stamps stop_event with its end (hipExtLaunchKernel), so a caller can time
+ * the pass with no marker packets between it and its neighbours.
  */
 int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad_dtype,
                           int out_dtype, const morph_adamw_hp* hps,
                           const morph_adamw_sched* scheds, int n_hp, const int64_t* d_clocks,
-                          const morph_step_state* d_state, int slot, void* stream);
+                          const morph_step_state* d_state, int slot, void* start_event,
+                          void* stop_event, void* stream);
 
 /*
  * Closes a device-resident step (one workgroup): on overflow (found_inf[slot])

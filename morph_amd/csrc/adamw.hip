@@ -28,6 +28,8 @@
 // device-resident control (morph_adamw_multi_dev) where the loss scale, the
 // skip decision and each tensor's step clock are read from HBM, so a training
 // loop can enqueue steps without waiting for the previous outcome.
+#include <hip/hip_ext.h>
+
 #include "common.h"
 
 #ifndef MORPH_ADAMW_UNROLL
@@ -273,37 +275,51 @@ __global__ __launch_bounds__(kBlock) void adamw_multi_kernel(const LaunchArgs a,
   }
 }
 
-template <typename GT, typename OT>
-int launch(bool dev, const LaunchArgs& a, int blocks, const uint32_t* skip, hipStream_t s) {
-  if (dev)
-    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, true>), dim3(blocks), dim3(kBlock),
-                       kOccupancyLds, s, a,
-                       skip);
+// Events (nullable) are stamped by the dispatch itself (hipExtLaunchKernel):
+// e0 with the kernel's start, e1 with its end, with no marker packets between
+// this launch and its neighbours in the queue.
+struct Stamps {
+  hipEvent_t e0, e1;
+};
+
+template <typename K>
+void launch_kernel(K kernel, int blocks, const LaunchArgs& a, const uint32_t* skip, hipStream_t s,
+                   Stamps ev) {
+  if (ev.e0 == nullptr && ev.e1 == nullptr)
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlock), kOccupancyLds, s, a, skip);
   else
-    hipLaunchKernelGGL((adamw_multi_kernel<GT, OT, false>), dim3(blocks), dim3(kBlock),
-                       kOccupancyLds, s, a,
-                       skip);
+    hipExtLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlock), kOccupancyLds, s, ev.e0, ev.e1, 0u,
+                          a, skip);
+}
+
+template <typename GT, typename OT>
+int launch(bool dev, const LaunchArgs& a, int blocks, const uint32_t* skip, hipStream_t s,
+           Stamps ev) {
+  if (dev)
+    launch_kernel(adamw_multi_kernel<GT, OT, true>, blocks, a, skip, s, ev);
+  else
+    launch_kernel(adamw_multi_kernel<GT, OT, false>, blocks, a, skip, s, ev);
   return launch_status();
 }
 
 template <typename GT>
 int launch_out(bool dev, int out_dtype, const LaunchArgs& a, int blocks, const uint32_t* skip,
-               hipStream_t s) {
+               hipStream_t s, Stamps ev) {
   switch (out_dtype) {
-    case MORPH_DTYPE_NONE: return launch<GT, NoOut>(dev, a, blocks, skip, s);
-    case MORPH_DTYPE_F32: return launch<GT, F32>(dev, a, blocks, skip, s);
-    case MORPH_DTYPE_F16: return launch<GT, F16>(dev, a, blocks, skip, s);
-    case MORPH_DTYPE_BF16: return launch<GT, BF16>(dev, a, blocks, skip, s);
+    case MORPH_DTYPE_NONE: return launch<GT, NoOut>(dev, a, blocks, skip, s, ev);
+    case MORPH_DTYPE_F32: return launch<GT, F32>(dev, a, blocks, skip, s, ev);
+    case MORPH_DTYPE_F16: return launch<GT, F16>(dev, a, blocks, skip, s, ev);
+    case MORPH_DTYPE_BF16: return launch<GT, BF16>(dev, a, blocks, skip, s, ev);
     default: return MORPH_EDTYPE;
   }
 }
 
 int dispatch(bool dev, int grad_dtype, int out_dtype, const LaunchArgs& a, int blocks,
-             const uint32_t* skip, hipStream_t s) {
+             const uint32_t* skip, hipStream_t s, Stamps ev) {
   switch (grad_dtype) {
-    case MORPH_DTYPE_F32: return launch_out<F32>(dev, out_dtype, a, blocks, skip, s);
-    case MORPH_DTYPE_F16: return launch_out<F16>(dev, out_dtype, a, blocks, skip, s);
-    case MORPH_DTYPE_BF16: return launch_out<BF16>(dev, out_dtype, a, blocks, skip, s);
+    case MORPH_DTYPE_F32: return launch_out<F32>(dev, out_dtype, a, blocks, skip, s, ev);
+    case MORPH_DTYPE_F16: return launch_out<F16>(dev, out_dtype, a, blocks, skip, s, ev);
+    case MORPH_DTYPE_BF16: return launch_out<BF16>(dev, out_dtype, a, blocks, skip, s, ev);
     default: return MORPH_EDTYPE;
   }
 }
@@ -321,11 +337,12 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 // Validates everything, then splits the tensor list into launches of at most
 // kMaxTensors segments and kMaxHp constant sets.  `scheds`, `clocks` and
-// `state` are non-null exactly for the device-resident form.
+// `state` are non-null exactly for the device-resident form.  `stamps`: the
+// first launch stamps e0 with its start, the last stamps e1 with its end.
 int enqueue(const morph_adamw_tensor* tensors, int count, int grad_dtype, int out_dtype,
             const morph_adamw_hp* hps, const morph_adamw_sched* scheds, int n_hp,
             const int64_t* clocks, const morph_step_state* state, const uint32_t* d_skip,
-            void* stream) {
+            void* stream, Stamps stamps = Stamps{nullptr, nullptr}) {
   const bool dev = state != nullptr;
   if (count < 0 || (count > 0 && (tensors == nullptr || hps == nullptr)) || n_hp < 0)
     return MORPH_EINVAL;
@@ -355,9 +372,12 @@ int enqueue(const morph_adamw_tensor* tensors, int count, int grad_dtype, int ou
   int blocks = 0;
   a.count = 0;
   int n_local_hp = 0;
-  auto flush = [&]() -> int {
+  bool first_launch = true;
+  auto flush = [&](bool last) -> int {
     if (a.count == 0) return MORPH_OK;
-    const int rc = dispatch(dev, grad_dtype, out_dtype, a, blocks, d_skip, s);
+    const Stamps ev{first_launch ? stamps.e0 : nullptr, last ? stamps.e1 : nullptr};
+    first_launch = false;
+    const int rc = dispatch(dev, grad_dtype, out_dtype, a, blocks, d_skip, s, ev);
     a.count = 0;
     n_local_hp = 0;
     blocks = 0;
@@ -372,7 +392,7 @@ int enqueue(const morph_adamw_tensor* tensors, int count, int grad_dtype, int ou
       for (int k = 0; k < n_local_hp; ++k)
         if (hp_src[k] == t.hp_index) local = k;
       if (a.count == kMaxTensors || (local < 0 && n_local_hp == kMaxHp)) {
-        const int rc = flush();
+        const int rc = flush(false);
         if (rc != MORPH_OK) return rc;
         local = -1;
       }
@@ -397,7 +417,7 @@ int enqueue(const morph_adamw_tensor* tensors, int count, int grad_dtype, int ou
       blocks += (int)((n + kPerBlock - 1) / kPerBlock);
     }
   }
-  return flush();
+  return flush(true);
 }
 
 }  // namespace
@@ -416,10 +436,12 @@ extern "C" int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int coun
                                      int out_dtype, const morph_adamw_hp* hps,
                                      const morph_adamw_sched* scheds, int n_hp,
                                      const int64_t* d_clocks, const morph_step_state* d_state,
-                                     int slot, void* stream) {
+                                     int slot, void* start_event, void* stop_event,
+                                     void* stream) {
   if (d_state == nullptr || (slot != 0 && slot != 1)) return MORPH_EINVAL;
   return enqueue(tensors, count, grad_dtype, out_dtype, hps, scheds, n_hp, d_clocks, d_state,
-                 &d_state->found_inf[slot], stream);
+                 &d_state->found_inf[slot], stream,
+                 Stamps{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)});
 }
 
 extern "C" int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp_avg,

@@ -136,12 +136,13 @@ class AdamwBatch:
                                       arr, len(hps), _ptr(skip_flag), stream_handle(stream)))
 
 
-    def launch_dev(self, hps, scheds, clocks, state, slot=0, stream=None):
+    def launch_dev(self, hps, scheds, clocks, state, slot=0, stream=None, events=None):
         """Enqueue the device-resident form (morph_adamw_multi_dev).
 
         scheds: AdamwSched per constant set; clocks: device int64 tensor;
         state: device tensor holding a morph_step_state; slot: the step's
-        found_inf word (0 or 1).
+        found_inf word (0 or 1); events: optional (start, stop) pair from a
+        DispatchTimer, stamped by the launch's own dispatch.
         """
         if self.count == 0:
             return
@@ -153,9 +154,41 @@ class AdamwBatch:
             raise ValueError("clocks must be int64 and state must hold a morph_step_state")
         harr = (_lib.AdamwHP * len(hps))(*hps)
         sarr = (_lib.AdamwSched * len(scheds))(*scheds)
+        e0, e1 = (None, None) if events is None else (ctypes.c_void_p(events[0].cuda_event),
+                                                      ctypes.c_void_p(events[1].cuda_event))
         check(lib().morph_adamw_multi_dev(self.array, self.count, self.grad_dtype,
                                           self.out_dtype, harr, sarr, len(hps), _ptr(clocks),
-                                          _ptr(state), slot, stream_handle(stream)))
+                                          _ptr(state), slot, e0, e1, stream_handle(stream)))
+
+
+class DispatchTimer:
+    """Pairs of timing events that a launch's own dispatch stamps with its start and
+    end (hipExtLaunchKernel), so kernels are timed with no marker packets between
+    them and their neighbours in the queue.  The events are created (and recorded
+    once, which creates them) here, before the region they will time."""
+
+    def __init__(self, pairs, device=None):
+        stream = torch.cuda.current_stream(device)
+        self.pairs = []
+        for _ in range(pairs):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            b.record(stream)
+            self.pairs.append((a, b))
+        stream.synchronize()
+        self.used = 0
+
+    def next(self):
+        if self.used >= len(self.pairs):
+            raise RuntimeError(f"DispatchTimer holds {len(self.pairs)} pairs, all used")
+        pair = self.pairs[self.used]
+        self.used += 1
+        return pair
+
+    def elapsed_ms(self):
+        """Durations of the stamped launches (call after synchronizing)."""
+        return [a.elapsed_time(b) for a, b in self.pairs[:self.used]]
 
 
 def _check_close_args(state, clocks, clock_list):

@@ -14,9 +14,10 @@ A step is two launches on the caller's stream -- the detector (which also
 closes the previous step: loss scale, clocks) and the fused AdamW pass --
 driven by device-resident state (morph_amd.control), so no step waits for the
 host.  The last step's close is enqueued when the host next needs the state
-(resolve()) or when the next step has no detector pass of its own.  The host copies of the clocks and of the loss scale are
-refreshed by resolve(); with sync=True (or on_overflow="raise") every step
-resolves and reports its outcome like the reference does.
+(resolve()) or when the next step has no detector pass of its own.  The host
+copies of the clocks and of the loss scale are refreshed by resolve(); with
+sync=True (or on_overflow="raise") every step resolves and reports its
+outcome like the reference does.
 """
 import torch
 
@@ -107,6 +108,7 @@ class FusedAdamW:
         self._slot = 0          # found_inf word of the next step (steps alternate)
         self._pending = None    # (slot, clock_list, stream) of a step whose close is not enqueued
         self.kernel_timer = None  # optional list: (start, end) events around each AdamW launch
+        self.dispatch_timer = None  # optional kernels.DispatchTimer: stamps each AdamW launch
         self.skipped_steps = 0
         self.applied_steps = 0
 
@@ -235,6 +237,8 @@ class FusedAdamW:
             self.resolve()
             self._ctl.push_scale()
         batch, clock_list, hps, scheds = self._prepare(grads, present)
+        # everything that can fail is done before the first launch is enqueued
+        events = self.dispatch_timer.next() if self.dispatch_timer is not None else None
         ctl = self._ctl
         slot = self._slot
         s = stream or torch.cuda.current_stream(self.device)
@@ -255,11 +259,11 @@ class FusedAdamW:
         if self.kernel_timer is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s)
+            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s, events)
             e1.record(s)
             self.kernel_timer.append((e0, e1))
         else:
-            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s)
+            batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s, events)
         self._pending = (slot, clock_list, s)
         self._slot = slot ^ 1
         for i in present:

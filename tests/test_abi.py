@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_status_strings():
     from morph_amd import _lib
     lib = _lib.lib()
-    assert lib.morph_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.morph_abi_version() == _lib.ABI_VERSION == 4
     assert lib.morph_strerror(0) == b"ok"
     for code in (-1, -2, -3, -4, -5):
         assert lib.morph_strerror(code) not in (b"ok", b"unknown morph status")
@@ -58,7 +58,8 @@ def test_argument_validation_happens_before_any_launch():
     st = ctypes.c_void_p(0x10000)
     assert lib.morph_step_end(st, None, None, 0, 2, None) == -1
     assert lib.morph_step_end(None, None, None, 0, 0, None) == -1
-    assert lib.morph_adamw_multi_dev(None, 0, 1, -1, None, None, 0, None, st, 2, None) == -1
+    assert lib.morph_adamw_multi_dev(None, 0, 1, -1, None, None, 0, None, st, 2, None, None,
+                                     None) == -1
     close = lambda *a: lib.morph_nonfinite_or_close(*a)
     assert close(None, None, 0, 1, None, 0, None, None, 0, None) == -1      # no state
     assert close(None, None, 0, 1, st, 2, None, None, 0, None) == -1        # bad slot

@@ -473,6 +473,34 @@ def test_fused_close_with_a_detector_over_several_launches():
         assert torch.equal(p, q)
         assert a.state[p]["step"] == b.state[q]["step"] == 6
 
+
+@pytest.mark.parametrize("count,size", [(1, 1 << 24), (200, 1 << 16)], ids=["one", "split"])
+def test_dispatch_timer_stamps_the_adamw_launches(count, size):
+    """Events stamped by the AdamW dispatch itself (hipExtLaunchKernel) time the pass: each
+    interval is positive and lies inside the events recorded around the launch; a call
+    split into several launches (200 tensors) runs from the first start to the last end."""
+    from morph_amd.kernels import DispatchTimer
+    gen = torch.Generator(device=DEV).manual_seed(98)
+    ps = [torch.randn(size, generator=gen, device=DEV) * .02 for _ in range(count)]
+    gs = [torch.randn(size, generator=gen, device=DEV).half() for _ in range(count)]
+    opt = FusedAdamW(ps, lr=1e-3)
+    opt.step(gs)
+    opt.dispatch_timer = DispatchTimer(4, DEV)
+    opt.kernel_timer = []
+    for _ in range(4):
+        opt.step(gs)
+    torch.cuda.synchronize()
+    stamped = opt.dispatch_timer.elapsed_ms()
+    around = [a.elapsed_time(b) for a, b in opt.kernel_timer]
+    assert len(stamped) == 4
+    for x, y in zip(stamped, around):
+        assert 0.5 * y <= x <= y + 0.002, (x, y)
+    with pytest.raises(RuntimeError):
+        opt.step(gs)  # the timer holds four pairs
+    opt.dispatch_timer = None
+    opt.resolve()
+    assert opt.applied_steps == 5
+
 def _config4_grads(shapes, rng, t, scale, overflow_steps):
     grads = bench.config2_grads("cpu", 2000 + t, shapes, scale=scale)
     if t in overflow_steps:
