@@ -30,6 +30,7 @@ import torch
 ROOT = Path(__file__).resolve().parent
 TRAFFIC_PROFILE = ROOT / "profiles" / "adamw_config2_traffic.json"
 TRAFFIC_PROFILE_C3 = ROOT / "profiles" / "adamw_config3_traffic.json"
+MFMA_PROFILE = ROOT / "profiles" / "muon_config5_mfma.json"
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_PARAM = 28  # read g16 2 + w 4 + m 4 + v 4; write w 4 + m 4 + v 4 + export 2
 CONFIG2_SHAPES = [(6144, 3072), (6144, 3072), (3072, 6144)]  # W_gate, W_up, W_down (nn.Linear storage)
@@ -271,6 +272,7 @@ def muon_main(args):
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                      "traffic": None, "kernel": "gemm_kernel (3 launches per Newton-Schulz iteration, all 42 matrices batched)",
                      "flops_per_step": r["flops"]},
+        "mfma_counters": measured_mfma(),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline_muon(),
     }
     assert r["flops"] == r["expected_flops"]
@@ -802,6 +804,15 @@ def overflow_main(args):
     print(json.dumps(line), flush=True)
     if not ok:
         raise SystemExit("config-4 sequence differs from DynamicLossScale's rule")
+
+def measured_mfma():
+    """Per-product MFMA-busy fraction and clock from the committed rocprofv3 counter pass."""
+    try:
+        d = json.loads(MFMA_PROFILE.read_text())["products"]
+    except (OSError, KeyError, ValueError):
+        return None
+    return {k: {"mfma_busy_pct": v["mfma_busy_pct"], "clock_ghz": v["clock_ghz"]} for k, v in d.items()}
+
 
 def measured_traffic(path=TRAFFIC_PROFILE):
     """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""

@@ -242,6 +242,8 @@ class FusedAdamW:
         ctl = self._ctl
         slot = self._slot
         s = stream or torch.cuda.current_stream(self.device)
+        if s != torch.cuda.current_stream(self.device):
+            clock_list.record_stream(s)  # allocated on the current stream, read on `s`
         if self._pending is not None and self._pending[2] != s:
             # the previous step ran on another stream: close it there, and order
             # this step after that close
