@@ -397,6 +397,7 @@ def time_window(steps, warmup, root):
     """Resident window (f2): load the config-2 window's [3, N] files into HBM + FP16 compute
     copy, then per step DiskState.update for the 3 parameters (fused update on the resident
     state + FP16 copy, D2H write-back chunk by chunk, flush, fsync)."""
+    from morph_amd.kernels import DispatchTimer
     from morph_amd.window import ResidentWindow
     device = torch.device("cuda", 0)
     names = ["ffn.gate.weight", "ffn.up.weight", "ffn.down.weight"]
@@ -414,8 +415,10 @@ def time_window(steps, warmup, root):
         step += 1
         for n in names:
             win.update(n, grads[n], step, 3e-4, 1.0)
+    # each update launch stamps its own dispatch's start and end: events recorded
+    # around it would also count the GPU waking up after the host's file writes
+    timer = win.dispatch_timer = DispatchTimer(steps * len(names), device)
     torch.cuda.synchronize()
-    win.kernel_timer = []
     t0 = time.perf_counter()
     for _ in range(steps):
         step += 1
@@ -423,7 +426,8 @@ def time_window(steps, warmup, root):
             win.update(n, grads[n], step, 3e-4, 1.0)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    kms = [a.elapsed_time(b) for a, b in win.kernel_timer]
+    win.dispatch_timer = None
+    kms = timer.elapsed_ms()
     return dict(n=sum(store.entries[n]["size"] for n in names), t_load=t_load, elapsed=elapsed,
                 avg_kernel_s=sum(kms) / len(kms) / 1e3, kernels=len(kms) // steps,
                 timing={k: round(v, 4) for k, v in win.timing.items()})

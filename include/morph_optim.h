@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 4
+#define MORPH_ABI_VERSION 5
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -196,11 +196,13 @@ int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp
  * into launches of at most 32 tensors) sharing one grad and one export dtype.
  * Each tensor selects its constants by hp_index into hps[0..n_hp).  This is
  * the whole AdamW group of HybridMuonAdamW (optimizer.py:40, 62) or one
- * stage window in one launch.
+ * stage window in one launch.  start_event / stop_event: as for
+ * morph_adamw_multi_dev (nullable; stamped by the dispatches themselves).
  */
 int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dtype,
                       int out_dtype, const morph_adamw_hp* hps, int n_hp,
-                      const uint32_t* d_skip, void* stream);
+                      const uint32_t* d_skip, void* start_event, void* stop_event,
+                      void* stream);
 
 /*
  * Device-resident form of morph_adamw_multi.  Each tensor's step t is

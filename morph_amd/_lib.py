@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmorph_optim.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_NONE, DTYPE_F32, DTYPE_F16, DTYPE_BF16 = -1, 0, 1, 2
 HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
@@ -114,7 +114,7 @@ def lib():
             "morph_adamw_fused": ([vp, i32, vp, vp, vp, vp, i32, i64, ctypes.POINTER(AdamwHP),
                                    vp, vp], i32),
             "morph_adamw_multi": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
-                                   ctypes.POINTER(AdamwHP), i32, vp, vp], i32),
+                                   ctypes.POINTER(AdamwHP), i32, vp, vp, vp, vp], i32),
             "morph_adamw_multi_dev": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
                                        ctypes.POINTER(AdamwHP), ctypes.POINTER(AdamwSched), i32,
                                        vp, vp, i32, vp, vp, vp], i32),

@@ -427,9 +427,11 @@ using namespace morph;
 
 extern "C" int morph_adamw_multi(const morph_adamw_tensor* tensors, int count, int grad_dtype,
                                  int out_dtype, const morph_adamw_hp* hps, int n_hp,
-                                 const uint32_t* d_skip, void* stream) {
+                                 const uint32_t* d_skip, void* start_event, void* stop_event,
+                                 void* stream) {
   return enqueue(tensors, count, grad_dtype, out_dtype, hps, nullptr, n_hp, nullptr, nullptr,
-                 d_skip, stream);
+                 d_skip, stream,
+                 Stamps{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)});
 }
 
 extern "C" int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad_dtype,
@@ -457,5 +459,5 @@ extern "C" int morph_adamw_fused(const void* grad, int grad_dtype, float* param,
   t.numel = n;
   t.hp_index = 0;
   t.clock_index = 0;
-  return morph_adamw_multi(&t, 1, grad_dtype, out_dtype, hp, 1, d_skip, stream);
+  return morph_adamw_multi(&t, 1, grad_dtype, out_dtype, hp, 1, d_skip, nullptr, nullptr, stream);
 }

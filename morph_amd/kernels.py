@@ -17,6 +17,13 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
+def _event_handles(events):
+    """hipEvent_t handles of a (start, stop) pair of torch events, or (None, None)."""
+    if events is None:
+        return None, None
+    return ctypes.c_void_p(events[0].cuda_event), ctypes.c_void_p(events[1].cuda_event)
+
+
 def new_flag(device=None):
     """A device uint32 flag (stored as int32; only 0/1 are written)."""
     return torch.zeros(1, dtype=torch.int32, device=device or torch.cuda.current_device())
@@ -123,8 +130,9 @@ class AdamwBatch:
             p, m, v, _, o = self._keep[i]
             self._keep[i] = (p, m, v, g, o)
 
-    def launch(self, hps, skip_flag=None, stream=None):
-        """Enqueue the step.  hps: sequence of AdamwHP, indexed by hp_index."""
+    def launch(self, hps, skip_flag=None, stream=None, events=None):
+        """Enqueue the step.  hps: sequence of AdamwHP, indexed by hp_index; events:
+        optional (start, stop) pair from a DispatchTimer."""
         if self.count == 0:
             return
         if len(hps) < self.n_hp:
@@ -132,8 +140,10 @@ class AdamwBatch:
         arr = (_lib.AdamwHP * len(hps))(*hps)
         if skip_flag is not None:
             require_device_tensor(skip_flag, "skip_flag")
+        e0, e1 = _event_handles(events)
         check(lib().morph_adamw_multi(self.array, self.count, self.grad_dtype, self.out_dtype,
-                                      arr, len(hps), _ptr(skip_flag), stream_handle(stream)))
+                                      arr, len(hps), _ptr(skip_flag), e0, e1,
+                                      stream_handle(stream)))
 
 
     def launch_dev(self, hps, scheds, clocks, state, slot=0, stream=None, events=None):
@@ -154,8 +164,7 @@ class AdamwBatch:
             raise ValueError("clocks must be int64 and state must hold a morph_step_state")
         harr = (_lib.AdamwHP * len(hps))(*hps)
         sarr = (_lib.AdamwSched * len(scheds))(*scheds)
-        e0, e1 = (None, None) if events is None else (ctypes.c_void_p(events[0].cuda_event),
-                                                      ctypes.c_void_p(events[1].cuda_event))
+        e0, e1 = _event_handles(events)
         check(lib().morph_adamw_multi_dev(self.array, self.count, self.grad_dtype,
                                           self.out_dtype, harr, sarr, len(hps), _ptr(clocks),
                                           _ptr(state), slot, e0, e1, stream_handle(stream)))
@@ -225,8 +234,10 @@ def nonfinite_or_close(grads, state, slot, clocks, prev_clock_list, stream=None)
                                          stream_handle(stream)))
 
 
-def adamw_step(param, exp_avg, exp_avg_sq, grad, hp, out=None, skip_flag=None, stream=None):
-    """One fused AdamW step on one tensor (morph_adamw_fused)."""
+def adamw_step(param, exp_avg, exp_avg_sq, grad, hp, out=None, skip_flag=None, stream=None,
+               events=None):
+    """One fused AdamW step on one tensor (morph_adamw_fused; with `events`, a (start,
+    stop) pair from a DispatchTimer, the one-tensor morph_adamw_multi that stamps them)."""
     for name, t in (("param", param), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq),
                     ("grad", grad)):
         require_device_tensor(t, name)
@@ -242,6 +253,10 @@ def adamw_step(param, exp_avg, exp_avg_sq, grad, hp, out=None, skip_flag=None, s
             raise ValueError("export copy size differs from param")
     if skip_flag is not None:
         require_device_tensor(skip_flag, "skip_flag")
+    if events is not None:
+        AdamwBatch([param], [exp_avg], [exp_avg_sq], [grad], [out]).launch(
+            [hp], skip_flag, stream, events)
+        return
     check(lib().morph_adamw_fused(
         _ptr(grad), dtype_code(grad.dtype), _ptr(param), _ptr(exp_avg), _ptr(exp_avg_sq),
         _ptr(out), dtype_code(out.dtype) if out is not None else _lib.DTYPE_NONE, n,

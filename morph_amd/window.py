@@ -72,6 +72,7 @@ class ResidentWindow:
         self.transfer_bytes = dict(h2d_state=0, d2h_state=0)
         self.timing = dict(file_read=0.0, d2h_wait=0.0, file_write=0.0, fsync=0.0)  # seconds
         self.kernel_timer = None  # optional list: (start, end) HIP events around each update launch
+        self.dispatch_timer = None  # optional kernels.DispatchTimer: stamps each update launch
         self._copy = torch.cuda.Stream(self.device)
         self._staging = None
 
@@ -152,8 +153,9 @@ class ResidentWindow:
             if self.kernel_timer is not None:
                 t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 t0.record(compute)
+            events = self.dispatch_timer.next() if self.dispatch_timer is not None else None
             kernels.adamw_step(dev[0], dev[1], dev[2], flat, disk_constants(step=step, lr=lr, clip=clip),
-                               out=self.weights[name].reshape(-1), stream=compute)
+                               out=self.weights[name].reshape(-1), stream=compute, events=events)
             if self.kernel_timer is not None:
                 t1.record(compute)
                 self.kernel_timer.append((t0, t1))

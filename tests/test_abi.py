@@ -33,7 +33,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_status_strings():
     from morph_amd import _lib
     lib = _lib.lib()
-    assert lib.morph_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.morph_abi_version() == _lib.ABI_VERSION == 5
     assert lib.morph_strerror(0) == b"ok"
     for code in (-1, -2, -3, -4, -5):
         assert lib.morph_strerror(code) not in (b"ok", b"unknown morph status")
@@ -53,7 +53,7 @@ def test_argument_validation_happens_before_any_launch():
                                  None, None) == -1
     assert lib.morph_adamw_fused(None, 9, None, None, None, None, -1, 0, ctypes.byref(hp),
                                  None, None) == -2
-    assert lib.morph_adamw_multi(None, -1, 1, -1, None, 0, None, None) == -1
+    assert lib.morph_adamw_multi(None, -1, 1, -1, None, 0, None, None, None, None) == -1
     # step slots are 0 or 1; the fused detector + close validates before any launch
     st = ctypes.c_void_p(0x10000)
     assert lib.morph_step_end(st, None, None, 0, 2, None) == -1

@@ -156,3 +156,24 @@ def test_special_values_in_masters_and_grads():
     assert_same_bits(dm.cpu().numpy(), om, "exp_avg")
     assert_same_bits(dv.cpu().numpy(), ov, "exp_avg_sq")
     assert_same_bits(export_bits(out), oo.view(np.uint16), "export")
+
+
+def test_stamped_one_tensor_step_equals_the_plain_step():
+    """adamw_step with a DispatchTimer pair (the one-tensor morph_adamw_multi that stamps the
+    dispatch) writes the same bytes as morph_adamw_fused and times a positive interval."""
+    gen = torch.Generator().manual_seed(99)
+    n = 1 << 20
+    w = torch.randn(n, generator=gen) * .02
+    g = (torch.randn(n, generator=gen) * 1e-3).to(DEV)
+    hp = hyper.disk_constants(step=1, lr=3e-4, clip=0.5)
+    runs = []
+    timer = kernels.DispatchTimer(1)
+    for events in (None, timer.next()):
+        p, m, v = w.to(DEV), torch.zeros(n, device=DEV), torch.zeros(n, device=DEV)
+        out = torch.empty(n, dtype=torch.float16, device=DEV)
+        kernels.adamw_step(p, m, v, g, hp, out=out, events=events)
+        torch.cuda.synchronize()
+        runs.append((p, m, v, out))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    assert timer.elapsed_ms()[0] > 0
