@@ -181,6 +181,7 @@ def cpu_baseline(seconds=10.0):
     except (OSError, StopIteration):
         pass
     return dict(value=round(n / med / 1e9, 4), unit="Gparams/s", cores=threads, kind="port",
+                gbs_28b_equivalent=round(BYTES_PER_PARAM * n / med / 1e9, 2),
                 sample=f"config 2 window (N={n}), {len(times)} whole steps, median; "
                        f"torch.optim.AdamW(foreach=False) after FP16 unscale; CPU: {cpu}",
                 disk_ops=cpu_baseline_disk(masters, grads16, seconds / 2))
