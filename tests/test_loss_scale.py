@@ -76,3 +76,16 @@ def test_state_dict_roundtrip():
     t = DynamicLossScale()
     t.load_state_dict(s.state_dict())
     assert t.state_dict() == {"scale": 512., "good_steps": 1, "growth_interval": 7}
+
+
+def test_bench_config4_expectation_matches_the_golden_sequence(golden_dir):
+    """The overflow bench checks the device against bench.expected_config4_scales(): that
+    expectation is the golden config-4 sequence (steps, overflow steps, scales, final state)."""
+    import bench
+    cfg = json.loads((golden_dir / "loss_scale.json").read_text())["config4"]
+    assert bench.CONFIG4_STEPS == cfg["steps"]
+    assert list(bench.CONFIG4_OVERFLOW) == cfg["overflow_steps"]
+    assert bench.LOSS_SCALE == cfg["initial"]
+    scales, state = bench.expected_config4_scales()
+    assert scales == cfg["scale_before_step"]
+    assert state["scale"] == cfg["final_scale"]
