@@ -229,7 +229,9 @@ int morph_adamw_multi_dev(const morph_adamw_tensor* tensors, int count, int grad
  * `dynamic`, and advances the clocks d_clocks[d_clock_list[0..n)] (indices must
  * be distinct).  Then records found_inf[slot] in last_found_inf and clears it.
  * No-op while fatal is set.  Must run after the step's AdamW launch and before
- * the next step's (stream order).
+ * the next step's (stream order).  Replaces DynamicLossScale.overflow/success
+ * (precision.py:6-17, called at disk.py:483-496) and the conditional clock
+ * advance of sparse_disk.py:122-138.
  */
 int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* d_clock_list,
                    int n, int slot, void* stream);
@@ -241,6 +243,10 @@ int morph_step_end(morph_step_state* d_state, int64_t* d_clocks, const int32_t* 
  * n_prev, slot ^ 1).  The two touch disjoint words (the close reads and clears
  * only found_inf[slot ^ 1]), so their workgroups may run in any order.  This
  * saves the close's own launch on every step that runs the detector.
+ * Replaces, per step, the reference's non-finite decision (optimizer.py:49-51;
+ * disk.py:466-468, 485) and the previous step's DynamicLossScale update
+ * (precision.py:6-17, called at disk.py:483-496) with its clock advance
+ * (sparse_disk.py:122-138).
  */
 int morph_nonfinite_or_close(const void* const* grads, const int64_t* numels, int count,
                              int dtype, morph_step_state* d_state, int slot, int64_t* d_clocks,
