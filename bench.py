@@ -92,6 +92,7 @@ class Config5(torch.nn.Module):
 
 # --------------------------------------------------------------- timing --
 GRAD_SETS = 3  # gradient sets cycled over the steps: 3 x 113 MB exceeds the 256 MB Infinity Cache
+STAMP_EVERY = 4  # every 4th AdamW launch of the timed steps stamps its own start/stop events
 
 
 def time_gpu(steps, warmup):
@@ -100,11 +101,12 @@ def time_gpu(steps, warmup):
     Each step takes the next of GRAD_SETS gradient sets, so no step finds its
     gradients left in the Infinity Cache by an earlier one (one reused buffer
     would flatter the step without a detector pass by about 10 us).  The AdamW
-    launch of every timed step is timed by HIP events that its own dispatch
-    stamps (hipExtLaunchKernel's start/stop events on the launch stream).  Any
-    timing events cost the step about 5 us (255.5 vs 260.7 us on one box), so
-    K more steps without them follow (`step_uninstrumented`), then K steps
-    with checked=True, the step without the detector pass.
+    launch of every STAMP_EVERY-th timed step (the last of each group) is timed by
+    HIP events that its own dispatch stamps (hipExtLaunchKernel's start/stop
+    events on the launch stream).  Timing events cost a step about 5 us (255.5
+    vs 260.7 us on one box), so only a sample of the timed steps carries them;
+    K more steps without any follow (`step_uninstrumented`), then K steps with
+    checked=True, the step without the detector pass.
     """
     from morph_amd import DynamicLossScale, FusedAdamW
     from morph_amd.kernels import DispatchTimer
@@ -118,10 +120,14 @@ def time_gpu(steps, warmup):
     for t in range(max(warmup, GRAD_SETS)):
         opt.step(sets[t % GRAD_SETS])
     opt.resolve()
-    timer = opt.dispatch_timer = DispatchTimer(steps, device)
+    # the sampled steps are the last of each group of STAMP_EVERY (every step when
+    # fewer are timed): none is the first step after the idle synchronize
+    stamped = {t for t in range(steps) if steps < STAMP_EVERY or t % STAMP_EVERY == STAMP_EVERY - 1}
+    timer = DispatchTimer(len(stamped), device)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for t in range(steps):
+        opt.dispatch_timer = timer if t in stamped else None
         opt.step(sets[t % GRAD_SETS])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -896,8 +902,11 @@ def main():
                    "state_layout": "one arena: masters, moments, export (FusedAdamW(arena=True))",
                    "gradient_sets": GRAD_SETS},
         "kernel_gparams_per_s": round(n / r["avg_kernel_s"] / 1e9, 3),
-        "timing": "timed steps carry HIP events stamped by each AdamW dispatch "
-                  "(hipExtLaunchKernel, launch stream); the two step forms below carry none",
+        "timing": f"every {STAMP_EVERY}th AdamW launch of the timed steps (steps {STAMP_EVERY - 1}, "
+                  f"{2 * STAMP_EVERY - 1}, ...) "
+                  "stamps HIP events with its own dispatch (hipExtLaunchKernel, launch stream); "
+                  "the two step forms below carry none",
+        "kernel_samples": len(r["kernel_ms"]),
         "step_uninstrumented": {
             "gparams_per_s": round(n * args.steps / r["elapsed_plain"] / 1e9, 3),
             "ms_per_step": round(r["elapsed_plain"] / args.steps * 1e3, 4),
