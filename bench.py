@@ -598,7 +598,7 @@ def time_embedding(steps, warmup):
     """Config 3: the tied [65536, 3072] embedding, one tensor of 201,326,592 FP32 masters.
     Each step's BF16 gradient is nonzero only on rows drawn Zipf(1.1) from 4 x 1024 token IDs
     (N(0, 1e-3) there); every row still gets the dense update; wd 0, BF16 export.  A step is
-    detector + fused AdamW + step close, as in the config-2 workload; the AdamW launches of the
+    detector (carrying the previous step's close) + fused AdamW, as in the config-2 workload; the AdamW launches of the
     timed steps are timed by dispatch-stamped events."""
     from morph_amd import FusedAdamW
     from morph_amd.kernels import DispatchTimer
@@ -668,8 +668,8 @@ def embedding_main(args):
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "config 3: tied [65536, 3072] embedding, FP32 masters, BF16 "
                                "sparse-row grads (Zipf(1.1) rows of 4x1024 tokens, N(0, 1e-3)), "
-                               "dense update of every row, wd 0, BF16 export; detector + fused "
-                               "AdamW + step close",
+                               "dense update of every row, wd 0, BF16 export; detector (carrying "
+                               "the previous step's close) + fused AdamW",
                    "params": n, "shape": list(EMBED_SHAPE), "grad_dtype": "bf16",
                    "export_dtype": "bf16", "lr": 3e-4, "betas": [0.9, 0.95], "eps": 1e-8,
                    "weight_decay": 0.0, "gradient_rows_per_step": r["rows"]},
@@ -797,7 +797,8 @@ def overflow_main(args):
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "config 4: config-2 window, 16 steps from loss scale 2^16, "
                                "+inf/-inf/NaN at 1-8 seeded positions in steps 3, 7, 12; "
-                               "detector + fused AdamW + step close, enqueued back to back; "
+                               "detector (carrying the previous step's close) + fused AdamW, "
+                               "enqueued back to back; "
                                "timed: the sequence repeated on one warmed optimizer",
                    "params": n, "shapes": CONFIG2_SHAPES, "overflow_steps": list(CONFIG4_OVERFLOW),
                    "repetitions": reps},
