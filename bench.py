@@ -5,18 +5,19 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 A step is one optimizer step over the 5B-preset SwiGLU stage window
 (W_gate, W_up [6144, 3072] and W_down [3072, 6144]; N = 56,623,104 FP32
 masters, held with their moments and export copy in one arena): the
-non-finite detector over the FP16 gradients, the fused unscale + AdamW + FP16
-export kernel, and the step close that applies the skip decision and advances
-the loss scale and the clocks -- all on the device, with no host round trip
+non-finite detector over the FP16 gradients, whose launch also closes the
+previous step (skip decision, loss scale, clocks), then the fused unscale +
+AdamW + FP16 export kernel -- all on the device, with no host round trip
 between steps.  Inputs are synthetic (seeded), resident in HBM before the
 timed region.  Other workloads: embedding (config 3), overflow (config 4),
 muon (config 5), grads, window, fp8.
 
 Prints one JSON line.  `value` is whole-step throughput in Gparams/s;
 `roofline` is the fused AdamW kernel's algorithmic bandwidth (28 bytes per
-parameter) over its average launch time in the timed steps, from HIP events
-that each launch's dispatch stamps on the launch stream; `cpu_baseline` times torch.optim.AdamW(foreach=False) -- the
-library the reference's AdamW group runs -- on this host's cores.
+parameter) over its average launch time in a sample of the timed steps, from
+HIP events that those launches' dispatches stamp on the launch stream;
+`cpu_baseline` times torch.optim.AdamW(foreach=False) -- the library the
+reference's AdamW group runs -- on this host's cores.
 """
 import argparse
 import json
