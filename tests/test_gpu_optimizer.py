@@ -477,8 +477,10 @@ def test_fused_close_with_a_detector_over_several_launches():
 @pytest.mark.parametrize("count,size", [(1, 1 << 24), (200, 1 << 16)], ids=["one", "split"])
 def test_dispatch_timer_stamps_the_adamw_launches(count, size):
     """Events stamped by the AdamW dispatch itself (hipExtLaunchKernel) time the pass: each
-    interval is positive and lies inside the events recorded around the launch; a call
-    split into several launches (200 tensors) runs from the first start to the last end."""
+    interval lies inside the events recorded around the launch (which may also hold host
+    delays) and is no shorter than the HBM traffic of the FP32 state at the 8 TB/s peak
+    (24 B/param: master and moments read and written); a call split into several launches
+    (200 tensors) runs from the first start to the last end."""
     from morph_amd.kernels import DispatchTimer
     gen = torch.Generator(device=DEV).manual_seed(98)
     ps = [torch.randn(size, generator=gen, device=DEV) * .02 for _ in range(count)]
@@ -493,8 +495,9 @@ def test_dispatch_timer_stamps_the_adamw_launches(count, size):
     stamped = opt.dispatch_timer.elapsed_ms()
     around = [a.elapsed_time(b) for a, b in opt.kernel_timer]
     assert len(stamped) == 4
+    floor_ms = 24 * count * size / 8e12 * 1e3
     for x, y in zip(stamped, around):
-        assert 0.5 * y <= x <= y + 0.002, (x, y)
+        assert floor_ms <= x <= y + 0.002, (x, y, floor_ms)
     with pytest.raises(RuntimeError):
         opt.step(gs)  # the timer holds four pairs
     opt.dispatch_timer = None
