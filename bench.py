@@ -32,6 +32,7 @@ ROOT = Path(__file__).resolve().parent
 TRAFFIC_PROFILE = ROOT / "profiles" / "adamw_config2_traffic.json"
 TRAFFIC_PROFILE_C3 = ROOT / "profiles" / "adamw_config3_traffic.json"
 MFMA_PROFILE = ROOT / "profiles" / "muon_config5_mfma.json"
+TRAFFIC_PROFILE_GRADS = ROOT / "profiles" / "grads_config2_traffic.json"
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_PARAM = 28  # read g16 2 + w 4 + m 4 + v 4; write w 4 + m 4 + v 4 + export 2
 CONFIG2_SHAPES = [(6144, 3072), (6144, 3072), (3072, 6144)]  # W_gate, W_up, W_down (nn.Linear storage)
@@ -369,7 +370,8 @@ def grads_main(args):
                    "params": n, "shapes": CONFIG2_SHAPES, "grad_dtype": "f16",
                    "loss_scale": LOSS_SCALE},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(TRAFFIC_PROFILE_GRADS),
                      "kernel": "accumulate_kernel<F16,false,false> (plain pass)",
                      "avg_launch_us": round(r["avg_pass_s"] * 1e6, 2),
                      "bytes_per_launch": ACCUM_BYTES * n},
