@@ -285,6 +285,57 @@ def muon_reference_step(param, grad, momentum, lr, weight_decay):
     return update
 
 
+def _fma32(a, b, c):
+    """fp32 fma(a, b, c) with `a` an fp32 scalar and b, c fp32 tensors: the product of two
+    binary32 values is exact in binary64, so one binary64 add and one rounding to
+    binary32 give the fused result (except where that add itself rounds, which needs
+    exponents 29+ bits apart)."""
+    return (b.double() * float(a) + c.double()).float()
+
+
+def newton_schulz_bf16_emulated(u, steps=5, coeffs=(3.4445, -4.775, 2.0315), rounding=True):
+    """The bf16 Newton-Schulz chain of the GPU kernels, emulated with torch fp32 products.
+
+    Same algorithm as streamtrain/optimizer.py:13-22 (transpose the taller matrix,
+    X / (|X|_F + 1e-7), `steps` quintic iterations, transpose back) with the GPU's
+    rounding points:
+      den = fp32(sqrt(sum u^2 in binary64)) + fp32(1e-7);  X0 = bf16(u)
+      iteration 0:  A = bf16(fp32(1 / den^2) * X0 X0^T)
+                    B = bf16(fma(b, A, c * A A^T))
+                    X = bf16(fma(a / den, X0, (1 / den) * B X0))
+      later:        A = bf16(X X^T); B as above; X = bf16(fma(a, X, B X))
+    with every product accumulated in fp32 (here: torch's fp32 matmul of the bf16
+    values, exact per term, in its own summation order).  rounding=False skips the
+    bf16 roundings (X0 = u), which leaves the FP32 reference up to fp32 rounding.
+    Returns an fp32 tensor in u's layout (the values of the bf16 result).
+    """
+    import torch
+    x = u.float()
+    transpose = x.shape[0] > x.shape[1]
+    if transpose:
+        x = x.T
+    x = x.contiguous()
+    rnd = (lambda t: t.to(torch.bfloat16).float()) if rounding else (lambda t: t)
+    den = np.float32(math.sqrt(float(x.double().square().sum()))) + np.float32(1e-7)
+    inv_den = np.float32(1) / den
+    inv_den2 = f32(1.0 / (float(den) * float(den)))
+    a, b, c = (f32(v) for v in coeffs)
+    X = rnd(x)
+    for it in range(steps):
+        first = it == 0
+        A = X @ X.T
+        A = rnd(A * inv_den2 if first else A)
+        B = rnd(_fma32(b, A, A @ A.T * c))
+        BX = B @ X
+        if first:
+            X = rnd(_fma32(f32(a * float(inv_den)), X, BX * float(inv_den)))
+        else:
+            X = rnd(_fma32(a, X, BX))
+    if steps == 0:
+        X = rnd(X / float(den))
+    return X.T if transpose else X
+
+
 def accumulate_torch(destination, gradient, loss_scale):
     """sparse_disk.py:106-107 (disk.py:447 on the CPU): the per-micro-batch unscale + add."""
     destination.add_(gradient.detach().float() / loss_scale)
