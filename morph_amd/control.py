@@ -26,19 +26,32 @@ class BiasTables:
     """bias_correction1[t-1] = 1 - beta1 ** t (double) and
     bias_correction2_sqrt[t-1] = fp32((1 - beta2 ** t) ** 0.5) for t = 1..len,
     evaluated with Python floats exactly as torch/optim/adam.py:528-539 does
-    (step is a float there).  Grown by doubling; the old tables stay alive until
-    replaced, and torch's stream-ordered allocator keeps them valid for kernels
-    already enqueued."""
+    (step is a float there).  Grown by doubling.  A replaced table may still be
+    read by kernels enqueued on any stream that used it: every stream a step ran
+    on is recorded (used_on), and at replacement the old tensors are marked in
+    use on those streams, so the caching allocator does not hand their memory
+    out again before that work is done."""
 
     def __init__(self, beta1, beta2, device, length=4096):
         self.beta1, self.beta2, self.device = float(beta1), float(beta2), device
         self.length = 0
         self.bc1 = self.bc2s = None
+        self._streams = set()
         self.ensure(length)
+
+    def used_on(self, stream):
+        """Note that work reading the current tables is enqueued on `stream`."""
+        if stream != torch.cuda.current_stream(self.device):
+            self._streams.add(stream)
 
     def ensure(self, t_max):
         if t_max <= self.length:
             return
+        for old in (self.bc1, self.bc2s):
+            if old is not None:
+                for s in self._streams:
+                    old.record_stream(s)
+        self._streams = set()
         length = max(4096, self.length)
         while length < t_max:
             length *= 2
@@ -83,7 +96,10 @@ class StepControl:
 
     def _scale_fields(self):
         s = self.loss_scale
-        if isinstance(s, DynamicLossScale) or (hasattr(s, "overflow") and hasattr(s, "success")):
+        if isinstance(s, DynamicLossScale):
+            # the raw host copy: reading .scale would settle the owner's queued steps
+            return float(s._scale), int(s._good_steps), int(s.growth_interval), 1
+        if hasattr(s, "overflow") and hasattr(s, "success"):
             return float(s.scale), int(s.good_steps), int(s.growth_interval), 1
         scale = 1.0 if s is None else float(s)
         if not (scale > 0 and math.isfinite(scale)):
@@ -91,7 +107,8 @@ class StepControl:
         return scale, 0, 1 << 62, 0
 
     def push_scale(self):
-        """Write the host scaler's state into the device block (keeps counters)."""
+        """Write the host scaler's state into the device block (keeps counters and
+        the fatal bit)."""
         current = self.read() if self._initialized else StepState()
         self._initialized = True
         scale, good, interval, dynamic = self._scale_fields()
@@ -110,12 +127,24 @@ class StepControl:
         self._host.copy_(self.state)
         return StepState.from_buffer_copy(self._host.numpy().tobytes())
 
+    def scale_view(self):
+        """The device loss scale (the state block's `scale`) as a 0-d float64 view."""
+        return self.state[:8].view(torch.float64)[0]
+
+    def clear_fatal(self):
+        """Zero the sticky fatal word (stream-ordered on the current stream)."""
+        at = StepState.fatal.offset
+        self.state[at:at + 4].zero_()
+
     def mirror(self, st):
         """Refresh the host DynamicLossScale from a state read back from the device."""
         s = self.loss_scale
         if st.dynamic:
-            s.scale = st.scale
-            s.good_steps = int(st.good_steps)
+            if isinstance(s, DynamicLossScale):
+                s._scale, s._good_steps = st.scale, int(st.good_steps)
+            else:
+                s.scale = st.scale
+                s.good_steps = int(st.good_steps)
         self._mirrored = (st.scale if st.dynamic else self._mirrored[0],
                           int(st.good_steps) if st.dynamic else self._mirrored[1],
                           self._mirrored[2])

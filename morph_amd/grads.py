@@ -110,7 +110,9 @@ class StageGradients:
         squares (read with found_inf() / norm_squared()).  found_inf: a device
         int32 flag to receive that flag instead of the window's own, e.g. a
         FusedAdamW's `found_inf`, whose step(..., checked=True) then needs no
-        detector pass.
+        detector pass.  A caller's flag is only ever ORed into (never cleared
+        here), so several windows can feed one step; its owner clears it (the
+        optimizer's step close does).  The window's own flag is cleared first.
         """
         if self._finalized:
             raise RuntimeError("window already finalized; call zero_() to start again")
@@ -129,7 +131,7 @@ class StageGradients:
                 self._flag_target = found_inf
             else:
                 self._flag_target = self._flag
-            kernels.flag_clear(self._flag_target, stream)  # on the same stream as the pass
+                kernels.flag_clear(self._flag, stream)  # on the same stream as the pass
         sh = stream_handle(stream)
         flag = (self._flag_target if final else self._flag)
         check(L.morph_grad_accumulate(arr, len(self.views), code, float(loss_scale), flags,

@@ -15,15 +15,18 @@ closes the previous step: loss scale, clocks) and the fused AdamW pass --
 driven by device-resident state (morph_amd.control), so no step waits for the
 host.  The last step's close is enqueued when the host next needs the state
 (resolve()) or when the next step has no detector pass of its own.  The host
-copies of the clocks and of the loss scale are refreshed by resolve(); with
-sync=True (or on_overflow="raise") every step resolves and reports its
-outcome like the reference does.
+copies of the clocks are refreshed by resolve(); the host DynamicLossScale
+settles the queued steps itself when its scale is read, and scale_loss()
+multiplies a loss by the device scale without waiting.  With sync=True (or
+on_overflow="raise") every step resolves and reports its outcome like the
+reference does.
 """
 import torch
 
 from . import kernels
 from .control import BiasTables, StepControl
 from .hyper import adamw_constants
+from .precision import DynamicLossScale
 
 _OVERFLOW_POLICIES = ("skip", "raise")
 
@@ -101,6 +104,9 @@ class FusedAdamW:
                     self.exports.append(p.detach().to(export_dtype))
         self.device = device
         self._ctl = StepControl(device, len(flat), loss_scale)
+        if isinstance(loss_scale, DynamicLossScale):
+            loss_scale.attach(self)
+        self._dirty = False     # steps enqueued since the host last read the device state
         self._tables = {}
         self._bound = [0] * len(flat)  # upper bound of each device clock
         self._cache_key = None
@@ -120,10 +126,30 @@ class FusedAdamW:
     def found_inf(self):
         """The next step's non-finite flag in the device step state, as a 1-element
         int32 tensor.  A producer that already tests every gradient (the final pass of
-        StageGradients.accumulate(..., found_inf=opt.found_inf)) can set it and call
-        step(..., checked=True), which then skips the detector pass.  Steps alternate
-        between two flag words: read this property anew before every step."""
+        StageGradients.accumulate(..., found_inf=opt.found_inf)) ORs its result into it
+        and the caller then calls step(..., checked=True), which skips the detector
+        pass.  Several producers may OR into it for one step (e.g. one per stage
+        window); the step's close clears it.  Steps alternate between two flag words:
+        read this property anew before every step."""
         return self._ctl.found_inf_view(self._slot)
+
+    def loss_scale_tensor(self):
+        """The loss scale the next step unscales by, as a 0-d float64 device tensor (a
+        view of the device step state), without waiting for the device.  The previous
+        step's close (which may halve or double the scale) is enqueued first if it is
+        still pending, ordered before the caller's current stream."""
+        if self._pending is not None:
+            s = self._pending[2]
+            self._flush_close()
+            cur = torch.cuda.current_stream(self.device)
+            if s != cur:
+                cur.wait_stream(s)
+        return self._ctl.scale_view()
+
+    def scale_loss(self, loss):
+        """loss * (the loss scale of the next step), computed on the GPU: the
+        reference's `loss * loss_scale` (disk.py:437) with no host round trip."""
+        return loss * self.loss_scale_tensor().to(loss.dtype)
 
     # -- helpers -----------------------------------------------------------
     @torch.no_grad()
@@ -242,6 +268,8 @@ class FusedAdamW:
         ctl = self._ctl
         slot = self._slot
         s = stream or torch.cuda.current_stream(self.device)
+        for table in self._tables.values():
+            table.used_on(s)
         if s != torch.cuda.current_stream(self.device):
             clock_list.record_stream(s)  # allocated on the current stream, read on `s`
         if self._pending is not None and self._pending[2] != s:
@@ -268,6 +296,7 @@ class FusedAdamW:
             batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s, events)
         self._pending = (slot, clock_list, s)
         self._slot = slot ^ 1
+        self._dirty = True
         for i in present:
             self._bound[i] += 1
         if not self.sync:
@@ -289,9 +318,26 @@ class FusedAdamW:
         """Wait for enqueued steps; refresh clocks, counters and the host loss scale.
 
         Raises FloatingPointError if a step overflowed at loss scale <= 1 (the
-        reference raises there; on the device that step and every later one
-        changed nothing).
+        reference raises there, precision.py:9-10; on the device that step and every
+        step enqueued after it changed nothing).  The error is raised once: the
+        optimizer then stands where the reference stands after the raise (scale 1,
+        state untouched) and the next step runs normally.
         """
+        st = self._sync_state()
+        err = self._ctl.fatal_error(st)
+        if err is not None:
+            self._ctl.clear_fatal()
+            torch.cuda.current_stream(self.device).synchronize()
+            raise err
+        return st
+
+    def _refresh_scaler(self):
+        """DynamicLossScale's host view asks for the current state."""
+        if self._dirty or self._pending is not None:
+            self._sync_state()
+
+    def _sync_state(self):
+        """resolve() without raising: wait, then refresh the host mirrors."""
         if self._pending is not None:
             s = self._pending[2]
             self._flush_close()
@@ -305,16 +351,14 @@ class FusedAdamW:
         self.skipped_steps = int(st.skipped)
         self.applied_steps = int(st.applied)
         self._ctl.mirror(st)
-        err = self._ctl.fatal_error(st)
-        if err is not None:
-            raise err
+        self._dirty = False
         return st
 
     synchronize = resolve
 
     # -- persistence (torch.optim.Optimizer layout) ------------------------
     def state_dict(self):
-        self.resolve()
+        self._sync_state()
         index = {}
         groups = []
         for group in self.param_groups:
@@ -329,7 +373,8 @@ class FusedAdamW:
         return {"state": state, "param_groups": groups}
 
     def load_state_dict(self, state_dict):
-        self.resolve()
+        self._sync_state()
+        self._ctl.clear_fatal()  # a loaded state is a consistent point to go on from
         flat = [p for _, p in self._flat()]
         if len(state_dict["param_groups"]) != len(self.param_groups):
             raise ValueError("loaded state dict has a different number of parameter groups")

@@ -593,3 +593,104 @@ def test_loss_scale_growth_on_device_matches_host_rule():
         oscaler.success()
     opt.resolve()
     assert scaler.state_dict() == oscaler.state_dict() and scaler.scale == 65536.
+
+
+@pytest.mark.parametrize("mode", ["host_scale", "device_scale"])
+def test_loss_scaled_by_the_exposed_scale_across_overflow_and_growth(mode):
+    """A training loop scales each step's loss by the scale the API exposes -- the host
+    DynamicLossScale's `scale` (which settles the queued steps when read) or the
+    optimizer's device scale (scale_loss / loss_scale_tensor, no wait) -- and never
+    calls resolve().  With growth every 3 clean steps and overflows at steps 4 and 9
+    the scale moves 1024 -> 2048 -> 1024 -> 2048 -> 1024 ..., and every applied step
+    must unscale by exactly the factor its gradient was scaled with: bit-exact
+    against the oracle running the reference's loop (disk.py:483-496)."""
+    from oracle import reference as R
+    n = 5000
+    w0 = torch.randn(n, generator=torch.Generator().manual_seed(31)) * .02
+    scaler = DynamicLossScale(1024., growth_interval=3)
+    w = w0.to(DEV)
+    opt = FusedAdamW([w], lr=3e-4, betas=(.9, .95), weight_decay=.1, loss_scale=scaler)
+    gen = torch.Generator().manual_seed(32)
+    true_grads = [torch.randn(n, generator=gen) * 1e-4 for _ in range(12)]
+    ow, om, ov = w0.numpy().copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    oscaler, ot, seen = R.LossScale(1024., 3), 0, []
+    for k, g in enumerate(true_grads):
+        if mode == "host_scale":
+            scale = scaler.scale                     # the reference reads scaler.scale
+            g16 = (g * scale).half().to(DEV)         # backward of loss * scale
+        else:
+            g16 = opt.scale_loss(g.to(DEV)).half()   # the same product on the GPU
+        if k + 1 in (4, 9):
+            g16[17] = float("inf")
+        opt.step([g16])
+        seen.append(oscaler.scale)
+        o16 = (g * oscaler.scale).half()
+        if k + 1 in (4, 9):
+            oscaler.overflow()
+            continue
+        ot += 1
+        R.adamw(o16.numpy(), ow, om, ov,
+                R.torch_adamw_hp(3e-4, .9, .95, 1e-8, .1, ot, scale=oscaler.scale))
+        oscaler.success()
+    assert seen[:10] == [1024.] * 3 + [2048., 1024., 1024., 1024., 2048., 2048., 1024.]
+    assert scaler.scale == oscaler.scale and scaler.good_steps == oscaler.good_steps
+    assert_same_bits(w.cpu().numpy(), ow, "master")
+    assert_same_bits(opt.state[w]["exp_avg"].cpu().numpy(), om, "exp_avg")
+    assert opt.state[w]["step"] == ot == 10
+
+
+def test_after_the_minimum_scale_raise_the_optimizer_goes_on():
+    """precision.py:9-11 raises and leaves the scaler usable: after the raise is reported
+    (once), state_dict() works, load_state_dict() restores, and the next step applies."""
+    w = torch.randn(4096, generator=torch.Generator().manual_seed(33)).to(DEV)
+    scaler = DynamicLossScale(1., growth_interval=2000)
+    opt = FusedAdamW([w], lr=1e-3, loss_scale=scaler)
+    good = torch.randn(4096, device=DEV).half()
+    bad = good.clone()
+    bad[9] = float("nan")
+    opt.step([good])
+    saved = opt.state_dict()
+    saved = {"state": {k: {kk: vv.clone() for kk, vv in v.items()} for k, v in saved["state"].items()},
+             "param_groups": saved["param_groups"]}
+    w_saved = w.clone()
+    opt.step([bad])                      # overflow at scale 1: the reference raises here
+    snapshot = opt.state_dict()          # reading the state does not raise
+    assert snapshot["state"][0]["step"].item() == 1.0
+    with pytest.raises(FloatingPointError, match="minimum loss scale"):
+        opt.resolve()
+    opt.resolve()                        # reported once
+    opt.step([good])                     # and the optimizer goes on
+    opt.resolve()
+    assert opt.state[w]["step"] == 2 and scaler.scale == 1.0
+    # fatal again, then restore a saved state: the restored optimizer steps normally
+    opt.step([bad])
+    w.copy_(w_saved)
+    opt.load_state_dict(saved)
+    opt.step([good])
+    opt.resolve()
+    assert opt.state[w]["step"] == 2
+
+
+def test_bias_tables_grow_past_4096_steps_on_a_side_stream():
+    """The bias-correction tables double at step 4097; the old ones stay valid for the
+    side stream's queued launches.  Result bit-exact against the oracle."""
+    from oracle import reference as R
+    n = 1000
+    w0 = torch.randn(n, generator=torch.Generator().manual_seed(34)) * .02
+    w = w0.to(DEV)
+    opt = FusedAdamW([w], lr=1e-4, betas=(.9, .95), weight_decay=.1)
+    g = (torch.randn(n, generator=torch.Generator().manual_seed(35)) * 1e-3)
+    gd = g.to(DEV)
+    side = torch.cuda.Stream(DEV)
+    side.wait_stream(torch.cuda.current_stream(DEV))
+    steps = 4100
+    for _ in range(steps):
+        opt.step([gd], stream=side)
+    opt.resolve()
+    torch.cuda.synchronize()
+    ow, om, ov = w0.numpy().copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    for t in range(1, steps + 1):
+        R.adamw(g.numpy(), ow, om, ov, R.torch_adamw_hp(1e-4, .9, .95, 1e-8, .1, t))
+    assert opt.state[w]["step"] == steps
+    assert_same_bits(w.cpu().numpy(), ow, "master")
+    assert_same_bits(opt.state[w]["exp_avg_sq"].cpu().numpy(), ov, "exp_avg_sq")
