@@ -64,23 +64,45 @@ def gemm_nt(P, Q, D=None, alpha=1.0, beta=0.0, out=None, out_t=None, symmetric=F
     return out if batched else out[0]
 
 
-class _Workspaces:
-    """Zero-filled device workspaces, one per (shape, count, device, batch index), kept for reuse."""
+class Workspaces:
+    """Device workspaces of the Muon batches, one per (shape, device, batch index), each
+    sized for the largest matrix count it has served.
+
+    The workspace layout depends on the batch's matrix count, and the kernels rely
+    on its zero padding (zero-filled once, then kept by every call of the same
+    layout).  A call with another count than the workspace's last is therefore
+    preceded by a zero fill of the part it uses, on the call's stream.  Streams
+    that used a workspace are recorded, so that a workspace replaced by a larger
+    one stays allocated until their queued work is done.
+    """
 
     def __init__(self):
         self._ws = {}
 
-    def get(self, rows, cols, count, device, index=0):
-        key = (rows, cols, count, device, index)
-        if key not in self._ws:
-            nbytes = lib().morph_muon_workspace_bytes(rows, cols, count)
-            if nbytes == 0:
-                raise ValueError(f"bad Muon shape {rows}x{cols} x{count}")
-            self._ws[key] = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        return self._ws[key]
+    def get(self, rows, cols, count, device, index=0, stream=None):
+        nbytes = lib().morph_muon_workspace_bytes(rows, cols, count)
+        if nbytes == 0:
+            raise ValueError(f"bad Muon shape {rows}x{cols} x{count}")
+        key = (rows, cols, torch.device(device), index)
+        stream = stream or torch.cuda.current_stream(device)
+        entry = self._ws.get(key)
+        if entry is None or entry["buf"].numel() < nbytes:
+            if entry is not None:
+                for s in entry["streams"]:
+                    entry["buf"].record_stream(s)
+            with torch.cuda.stream(stream):
+                entry = dict(buf=torch.zeros(nbytes, dtype=torch.uint8, device=device),
+                             count=count, streams=set())
+            self._ws[key] = entry
+        elif entry["count"] != count:
+            with torch.cuda.stream(stream):
+                entry["buf"][:nbytes].zero_()
+            entry["count"] = count
+        entry["streams"].add(stream)
+        return entry["buf"]
 
 
-_WORKSPACES = _Workspaces()
+_WORKSPACES = Workspaces()  # for the free functions; each HybridMuonAdamW owns its own
 
 
 def _hp(momentum_weight=.05, nesterov_weight=.95, update_scale=1.0, decay=1.0, neg_lr=0.0,
@@ -124,7 +146,7 @@ def _prepare(mats, rows, cols, hp, orth_only, stream, workspaces, found_inf=None
     batches = []
     for k, start in enumerate(range(0, len(mats), 64)):
         chunk = mats[start:start + 64]
-        ws = workspaces.get(rows, cols, len(chunk), chunk[0][0][0].device, first + k)
+        ws = workspaces.get(rows, cols, len(chunk), chunk[0][0][0].device, first + k, stream)
         arr = (MuonMatrix * len(chunk))()
         for i, ((p, g, m, m_out), transposed) in enumerate(chunk):
             arr[i].grad, arr[i].param = g.data_ptr(), p.data_ptr()
@@ -222,6 +244,14 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
     _complete(batches, stream, timer)
 
 
+def _host_grad(p):
+    g = p.grad
+    if g.device.type != "cpu" or g.dtype != torch.float32 or g.shape != p.shape:
+        raise ValueError("with CPU masters the Muon gradients are CPU float32 tensors of the "
+                         "parameter's shape")
+    return g.contiguous()
+
+
 def partition(model):
     """optimizer.py:25-31: hidden nn.Linear weights (not lm_head) -> Muon; the rest -> AdamW."""
     hidden = {id(module.weight) for name, module in model.named_modules()
@@ -240,11 +270,37 @@ class HybridMuonAdamW:
     Muon update for the hidden matrices (batched by shape) and the AdamW group
     (betas .9/.95, FusedAdamW).  The Newton-Schulz iteration is bf16 on MFMA
     where the reference uses FP32 (optimizer.py:3-6).
+
+    The model's parameters may all live on the GPU (engine='resident') or all on
+    the CPU (engine='dls'/'async': FP32 masters in RAM, gradients left in CPU
+    p.grad by the streaming engine; runner.py:41-46, engine.py:75-88).  With CPU
+    masters the momenta and the AdamW moments stay resident in HBM; step()
+    uploads the gradients and masters, runs the same kernels on device mirrors,
+    and writes the updated masters back into the CPU tensors before returning,
+    so the engine's next stage load (engine.py:109-115) reads the new weights.
     """
 
     def __init__(self, model, lr=1e-3, muon_lr=None, weight_decay=.01):
         self.muon, adam = partition(model)
+        kinds = {p.device.type for p in self.muon + adam}
+        if len(kinds) > 1 or not kinds <= {"cpu", "cuda"}:
+            raise ValueError("parameters must all be on the GPU or all on the CPU")
+        self.host = kinds == {"cpu"}
+        self._muon_masters = self._muon_grads = None
+        if self.host and self.muon:
+            from .staging import HostStaging
+            for p in self.muon:
+                if p.dim() != 2 or p.dtype != torch.float32 or not p.is_contiguous():
+                    raise ValueError("Muon masters must be contiguous 2-D float32 tensors")
+            dev = torch.device("cuda", torch.cuda.current_device())
+            shapes = [p.shape for p in self.muon]
+            self._muon_masters = HostStaging(shapes, torch.float32, dev)
+            self._muon_grads = HostStaging(shapes, torch.float32, dev)
+            self._muon_dev = self._muon_masters.views
+        else:
+            self._muon_dev = list(self.muon)
         self.ns_timer = None  # optional list: HIP events around each Newton-Schulz chain
+        self._workspaces = Workspaces()
         self.lr = lr if muon_lr is None else muon_lr
         self.weight_decay = weight_decay
         self.momentum = {}
@@ -269,49 +325,76 @@ class HybridMuonAdamW:
     def step(self):
         """The gate of optimizer.py:49-51 covers every gradient: the AdamW group's
         by the detector, the Muon matrices' inside their momentum pass (which
-        writes only scratch buffers until the gate has passed)."""
+        writes only scratch buffers until the gate has passed).  With CPU masters
+        every gradient and master is uploaded before the gate, and nothing is
+        written back to the CPU until it has passed."""
         live = [(i, p) for i, p in enumerate(self.muon) if p.grad is not None]
-        adam_grads = [p.grad for g in (self.adam.param_groups if self.adam else [])
-                      for p in g["params"] if p.grad is not None]
-        if not live and not adam_grads:
+        adam_params = [p for g in (self.adam.param_groups if self.adam else []) for p in g["params"]]
+        adam_present = [k for k, p in enumerate(adam_params) if p.grad is not None]
+        if not live and not adam_present:
             return
+        idx = [i for i, _ in live]
+        if self.host:
+            device = self._muon_dev[0].device if self.muon else self.adam.device
+            if live:
+                self._muon_grads.upload([_host_grad(p) for _, p in live], idx)
+                self._muon_masters.upload([p for _, p in live], idx)
+            muon_grads = [self._muon_grads.views[i] for i in idx]
+            adam_grads = (self.adam._stage_in([p.grad for p in adam_params], adam_present)
+                          if adam_present else None)
+        else:
+            device = (live[0][1] if live else adam_params[adam_present[0]]).device
+            muon_grads = [p.grad for _, p in live]
+            adam_grads = [p.grad for p in adam_params]
         if self._flag is None:
-            self._flag = kernels.new_flag((live[0][1] if live else adam_grads[0]).device)
+            self._flag = kernels.new_flag(device)
         kernels.flag_clear(self._flag)
-        if adam_grads:
-            kernels.nonfinite_or(adam_grads, self._flag)
+        if adam_present:
+            kernels.nonfinite_or([adam_grads[k] for k in adam_present], self._flag)
 
         def gate():
             if self._flag.item():
                 raise FloatingPointError('nonfinite gradient; optimizer not updated')
 
         if live:
-            for i, p in live:
+            for i in idx:
                 if i not in self.momentum:
-                    self.momentum[i] = torch.zeros_like(p)
+                    self.momentum[i] = torch.zeros_like(self._muon_dev[i])
                 if i not in self._momentum_next:
-                    self._momentum_next[i] = torch.empty_like(p)
-            muon_step([p for _, p in live], [p.grad for _, p in live],
-                      [self.momentum[i] for i, _ in live], self.lr, self.weight_decay,
-                      timer=self.ns_timer, momenta_out=[self._momentum_next[i] for i, _ in live],
+                    self._momentum_next[i] = torch.empty_like(self._muon_dev[i])
+            muon_step([self._muon_dev[i] for i in idx], muon_grads,
+                      [self.momentum[i] for i in idx], self.lr, self.weight_decay,
+                      workspaces=self._workspaces, timer=self.ns_timer,
+                      momenta_out=[self._momentum_next[i] for i in idx],
                       found_inf=self._flag, gate=gate)
-            for i, _ in live:
+            for i in idx:
                 self.momentum[i], self._momentum_next[i] = self._momentum_next[i], self.momentum[i]
         else:
             gate()
-        if self.adam is not None:
+        if not adam_present:
+            pass
+        elif self.host:
+            self.adam._enqueue(adam_grads, adam_present, None, False)
+            self.adam._stage_out(adam_present)
+        else:
             self.adam.step()
+        if self.host and live:
+            self._muon_masters.download([p.data for _, p in live], idx)
 
     def state_dict(self):
         """{momentum, adam, lr, weight_decay} as optimizer.py:64-65.  The momentum
         tensors are the current ones; a later step writes its update into a
-        second buffer and swaps, so they are not updated in place afterwards."""
-        return dict(momentum=self.momentum,
+        second buffer and swaps, so they are not updated in place afterwards.
+        With CPU masters they are CPU copies, where the reference keeps them."""
+        momentum = ({i: m.cpu() for i, m in self.momentum.items()} if self.host
+                    else self.momentum)
+        return dict(momentum=momentum,
                     adam=self.adam.state_dict() if self.adam else None,
                     lr=self.lr, weight_decay=self.weight_decay)
 
     def load_state_dict(self, state):
-        self.momentum = {i: value.to(self.muon[i].device) for i, value in state['momentum'].items()}
+        self.momentum = {i: value.to(self._muon_dev[i].device)
+                         for i, value in state['momentum'].items()}
         self._momentum_next = {}
         if self.adam is not None:
             self.adam.load_state_dict(state['adam'])

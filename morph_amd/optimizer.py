@@ -49,7 +49,12 @@ def _groups(params, defaults):
 class FusedAdamW:
     """torch.optim.AdamW(foreach=False)-exact AdamW with fused unscale, skip and export.
 
-    params: FP32 CUDA tensors (or torch-style param-group dicts).
+    params: FP32 tensors (or torch-style param-group dicts), all on one GPU, or
+      all on the CPU -- the streamed engines' masters (runner.py:41-46).  With
+      CPU masters the moments stay resident in HBM; each step uploads the
+      gradients (CPU p.grad, or device tensors) and the masters through pinned
+      staging, runs the same kernels on device mirrors, and writes the updated
+      masters back into the CPU tensors before returning (morph_amd.staging).
     loss_scale: None (no scaling), a float (fixed scale), or a DynamicLossScale
       whose state this optimizer advances (on the device) after every step.
     export_dtype: torch.float16 / torch.bfloat16 to keep an export copy of
@@ -87,21 +92,40 @@ class FusedAdamW:
             raise ValueError("a parameter appears more than once")
         device = None
         for _, p in flat:
-            kernels.require_device_tensor(p, "param")
+            if not isinstance(p, torch.Tensor):
+                raise TypeError("params must be tensors")
             if p.dtype != torch.float32:
                 raise TypeError("FusedAdamW keeps FP32 masters; got " + str(p.dtype))
             if device is not None and p.device != device:
                 raise ValueError("all parameters must be on one device")
             device = p.device
+        self._staging = None   # HostStaging of CPU masters (None: masters on the GPU)
+        self._grad_staging = None
+        if device.type == "cpu":
+            for _, p in flat:
+                if not p.is_contiguous():
+                    raise ValueError("CPU masters must be contiguous")
+            if arena:
+                raise ValueError("arena=True lays out device-resident masters; these are on the CPU")
+            from .staging import HostStaging
+            device = torch.device("cuda", torch.cuda.current_device())
+            self._staging = HostStaging([p.shape for _, p in flat], torch.float32, device)
+            self._dev = self._staging.views
+            self._staging.upload([p for _, p in flat])  # for the initial export copies
+        else:
+            for _, p in flat:
+                kernels.require_device_tensor(p, "param")
+            self._dev = [p for _, p in flat]
         self.arena = None
         if arena:
             self._place_in_arena([p for _, p in flat], device, export_dtype)
+            self._dev = [p for _, p in flat]
         else:
-            for _, p in flat:
-                self.state[p] = {"step": 0, "exp_avg": torch.zeros_like(p),
-                                 "exp_avg_sq": torch.zeros_like(p)}
+            for (_, p), d in zip(flat, self._dev):
+                self.state[p] = {"step": 0, "exp_avg": torch.zeros_like(d),
+                                 "exp_avg_sq": torch.zeros_like(d)}
                 if export_dtype is not None:
-                    self.exports.append(p.detach().to(export_dtype))
+                    self.exports.append(d.detach().to(export_dtype))
         self.device = device
         self._ctl = StepControl(device, len(flat), loss_scale)
         if isinstance(loss_scale, DynamicLossScale):
@@ -212,7 +236,7 @@ class FusedAdamW:
         if key != self._cache_key:
             ps = [flat[i][1] for i in present]
             batch = kernels.AdamwBatch(
-                ps, [self.state[p]["exp_avg"] for p in ps],
+                [self._dev[i] for i in present], [self.state[p]["exp_avg"] for p in ps],
                 [self.state[p]["exp_avg_sq"] for p in ps], [grads[i] for i in present],
                 [self.exports[i] for i in present] if self.exports else None,
                 hp_index=[hp_of[flat[i][0]] for i in present], clock_index=list(present))
@@ -248,7 +272,9 @@ class FusedAdamW:
         default p.grad.  checked=True: every gradient's non-finite test is
         already in `found_inf` (set on this stream since the last step), so
         the detector pass is skipped.  Returns None, or with sync the
-        applied/skipped outcome.
+        applied/skipped outcome.  With CPU masters the step also uploads the
+        gradients and masters and returns once the updated masters are back in
+        the CPU tensors.
         """
         flat = self._flat()
         if grads is None:
@@ -259,6 +285,49 @@ class FusedAdamW:
         present = [i for i, g in enumerate(grads) if g is not None]
         if not present:
             return True if self.sync else None
+        if self._staging is None:
+            return self._enqueue(grads, present, stream, checked)
+        dev_grads = self._stage_in(grads, present, stream)
+        try:
+            return self._enqueue(dev_grads, present, stream, checked)
+        finally:
+            self._stage_out(present, stream)
+
+    def _stage_in(self, grads, present, stream=None):
+        """CPU masters: upload the listed masters and the host gradients; returns the
+        per-parameter device gradients (None where absent)."""
+        flat = self._flat()
+        host = [i for i in present if grads[i].device.type == "cpu"]
+        for i in present:
+            g = grads[i]
+            if g.shape != flat[i][1].shape:
+                raise ValueError(f"gradient {i} has shape {tuple(g.shape)}, expected "
+                                 f"{tuple(flat[i][1].shape)}")
+            if g.device.type not in ("cpu", "cuda"):
+                raise ValueError(f"gradient {i} is on {g.device}")
+        dev = list(grads)
+        if host:
+            dtypes = {grads[i].dtype for i in host}
+            if len(dtypes) != 1:
+                raise ValueError(f"host gradients must share one dtype, got {dtypes}")
+            dtype = dtypes.pop()
+            if self._grad_staging is None or self._grad_staging.dtype != dtype:
+                from .staging import HostStaging
+                self._grad_staging = HostStaging([p.shape for _, p in flat], dtype, self.device)
+            self._grad_staging.upload([grads[i].contiguous() for i in host], host, stream)
+            for i in host:
+                dev[i] = self._grad_staging.views[i]
+        self._staging.upload([flat[i][1] for i in present], present, stream)
+        return dev
+
+    def _stage_out(self, present, stream=None):
+        """CPU masters: copy the listed device masters back into the CPU tensors."""
+        flat = self._flat()
+        self._staging.download([flat[i][1].data for i in present], present, stream)
+
+    def _enqueue(self, grads, present, stream, checked):
+        """The device step over device gradients (see step())."""
+        flat = self._flat()
         if self._ctl.scaler_changed():  # the caller edited the scaler: resync the device copy
             self.resolve()
             self._ctl.push_scale()
@@ -368,8 +437,12 @@ class FusedAdamW:
                 index[p] = len(index)
                 packed["params"].append(index[p])
             groups.append(packed)
-        state = {index[p]: {"step": torch.tensor(float(s["step"])), "exp_avg": s["exp_avg"],
-                            "exp_avg_sq": s["exp_avg_sq"]} for p, s in self.state.items()}
+        # the moments live with the masters in torch.optim: CPU masters get CPU copies
+        host = self._staging is not None
+        state = {index[p]: {"step": torch.tensor(float(s["step"])),
+                            "exp_avg": s["exp_avg"].cpu() if host else s["exp_avg"],
+                            "exp_avg_sq": s["exp_avg_sq"].cpu() if host else s["exp_avg_sq"]}
+                 for p, s in self.state.items()}
         return {"state": state, "param_groups": groups}
 
     def load_state_dict(self, state_dict):

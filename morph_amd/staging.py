@@ -1,0 +1,150 @@
+"""Device mirrors of host tensors and the pinned transfers that fill and drain them.
+
+The reference's streamed engines keep the FP32 masters on the CPU
+(morph/training/runner.py:41, StreamTrainEngine requires it, engine.py:92-93)
+and leave each step's gradients in CPU `p.grad` (Slot.flush, engine.py:75-88);
+HybridMuonAdamW / torch.optim.AdamW then update those CPU tensors in place.
+Here the optimizer state stays resident in HBM and only the masters and the
+gradients cross PCIe: HostStaging keeps one flat device buffer holding a
+mirror of each host tensor (each at a 256-byte aligned offset) and moves data
+between the host tensors and the mirrors in chunks through two pinned buffers
+per direction, so the host-side copy of one chunk (pageable <-> pinned, torch's
+multi-threaded copy) overlaps the DMA of the other.  Tensors whose mirrors are
+adjacent travel in one DMA per chunk.
+"""
+import torch
+
+ALIGN = 64  # elements of 4 bytes: mirrors start 256-byte aligned
+
+
+def _align(x):
+    return (x + ALIGN - 1) // ALIGN * ALIGN
+
+
+class HostStaging:
+    """Device mirrors of `count` host tensors of the given shapes and one dtype.
+
+    views[i] is the device mirror of tensor i.  upload()/download() move the
+    listed tensors; both are ordered after the work already queued on
+    `stream` and return with the host side finished (download: the host
+    tensors hold the data; upload: the pinned buffers are free again), the
+    device side ordered before later work on `stream`.
+    """
+
+    def __init__(self, shapes, dtype, device, chunk_elements=1 << 22):
+        self.device = torch.device(device)
+        self.dtype = dtype
+        self.shapes = [tuple(s) for s in shapes]
+        self.numels = [int(torch.Size(s).numel()) for s in self.shapes]
+        self.offsets, off = [], 0
+        for n in self.numels:
+            self.offsets.append(off)
+            off = _align(off + n)
+        self.flat = torch.empty(max(off, 1), dtype=dtype, device=self.device)
+        self.views = [self.flat[o:o + n].view(s)
+                      for o, n, s in zip(self.offsets, self.numels, self.shapes)]
+        self.chunk = max(int(chunk_elements), ALIGN)
+        self._copy = torch.cuda.Stream(self.device)
+        self._pinned = None
+        self.bytes_h2d = 0
+        self.bytes_d2h = 0
+
+    def _buffers(self):
+        if self._pinned is None:
+            self._pinned = [dict(buf=torch.empty(self.chunk, dtype=self.dtype, pin_memory=True),
+                                 event=torch.cuda.Event()) for _ in range(2)]
+        return self._pinned
+
+    def _chunks(self, which):
+        """Device ranges [lo, hi) of at most `chunk` elements, each with the pieces
+        (index, tensor start, tensor end) of the listed tensors it holds.  A range only
+        spans tensors that are all listed (padding between them rides along)."""
+        chunks = []
+        which = sorted(set(which))
+        run = []
+        for k, i in enumerate(which):
+            if run and i != run[-1] + 1:
+                chunks += self._split(run)
+                run = []
+            run.append(i)
+        if run:
+            chunks += self._split(run)
+        return chunks
+
+    def _split(self, run):
+        lo = self.offsets[run[0]]
+        hi = self.offsets[run[-1]] + self.numels[run[-1]]
+        out = []
+        for a in range(lo, hi, self.chunk):
+            b = min(a + self.chunk, hi)
+            pieces = []
+            for i in run:
+                s = max(a, self.offsets[i])
+                e = min(b, self.offsets[i] + self.numels[i])
+                if s < e:
+                    pieces.append((i, s - self.offsets[i], e - self.offsets[i]))
+            out.append((a, b, pieces))
+        return out
+
+    def _check(self, tensors, which):
+        for i, t in zip(which, tensors):
+            if t.device.type != "cpu" or t.dtype != self.dtype or t.numel() != self.numels[i]:
+                raise ValueError(f"host tensor {i}: expected a CPU {self.dtype} tensor of "
+                                 f"{self.numels[i]} elements")
+            if not t.is_contiguous():
+                raise ValueError(f"host tensor {i} must be contiguous")
+
+    def upload(self, tensors, which=None, stream=None):
+        """views[which[k]] <- tensors[k] (host, contiguous)."""
+        which = list(range(len(self.numels))) if which is None else list(which)
+        tensors = list(tensors)
+        self._check(tensors, which)
+        src = {i: t.detach().reshape(-1) for i, t in zip(which, tensors)}
+        stream = stream or torch.cuda.current_stream(self.device)
+        self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
+        bufs = self._buffers()
+        for k, (lo, hi, pieces) in enumerate(self._chunks(which)):
+            slot = bufs[k % 2]
+            slot["event"].synchronize()  # the DMA that last read this buffer is done
+            buf = slot["buf"]
+            for i, s, e in pieces:
+                at = self.offsets[i] + s - lo
+                buf[at:at + e - s].copy_(src[i][s:e])
+            with torch.cuda.stream(self._copy):
+                self.flat[lo:hi].copy_(buf[:hi - lo], non_blocking=True)
+                slot["event"].record(self._copy)
+            self.bytes_h2d += (hi - lo) * self.flat.element_size()
+        stream.wait_stream(self._copy)
+        for slot in bufs:
+            slot["event"].synchronize()  # the caller may change the host tensors on return
+
+    def download(self, tensors, which=None, stream=None):
+        """tensors[k] (host, contiguous) <- views[which[k]], after the work queued on `stream`."""
+        which = list(range(len(self.numels))) if which is None else list(which)
+        tensors = list(tensors)
+        self._check(tensors, which)
+        dst = {i: t.detach().view(-1) for i, t in zip(which, tensors)}
+        stream = stream or torch.cuda.current_stream(self.device)
+        self._copy.wait_stream(stream)
+        bufs = self._buffers()
+        chunks = self._chunks(which)
+
+        def fetch(k):
+            lo, hi, _ = chunks[k]
+            slot = bufs[k % 2]
+            with torch.cuda.stream(self._copy):
+                slot["buf"][:hi - lo].copy_(self.flat[lo:hi], non_blocking=True)
+                slot["event"].record(self._copy)
+            self.bytes_d2h += (hi - lo) * self.flat.element_size()
+
+        for k in range(min(2, len(chunks))):
+            fetch(k)
+        for k, (lo, hi, pieces) in enumerate(chunks):
+            slot = bufs[k % 2]
+            slot["event"].synchronize()
+            for i, s, e in pieces:
+                at = self.offsets[i] + s - lo
+                dst[i][s:e].copy_(slot["buf"][at:at + e - s])
+            if k + 2 < len(chunks):
+                fetch(k + 2)  # this buffer is free again
+        stream.wait_stream(self._copy)

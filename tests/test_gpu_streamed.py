@@ -1,0 +1,210 @@
+"""The streamed engines' optimizer path: FP32 masters on the CPU, gradients in CPU p.grad.
+
+morph/training/runner.py builds the model on the CPU for engine='dls'/'async' (:41),
+constructs HybridMuonAdamW(model, lr, muon_lr) or torch.optim.AdamW(model.parameters(),
+lr, weight_decay=.01, foreach=False) on it (:44-46), and per step calls
+zero_grad(set_to_none=True), lets StreamTrainEngine.backward leave the gradients in CPU
+p.grad (Slot.flush, engine.py:75-88: p.grad = value.clone()), clips on the CPU (:100)
+and calls step() (:101); checkpoints hold optimizer.state_dict() (:66-74).  Here the
+same calls run with the state resident in HBM (morph_amd.staging):
+  * FusedAdamW on CPU masters: bit-exact against the oracle and against the same
+    optimizer on device-resident masters, config 1 for 10 steps;
+  * HybridMuonAdamW on a CPU model through the runner's call sequence: the AdamW group
+    bit-exact against the oracle, the Muon matrices bit-exact against the
+    device-resident optimizer fed the same gradients, state_dict on the CPU and a
+    save/restore that continues identically;
+  * the non-finite gate: raise with CPU masters, momenta and moments untouched;
+  * HostStaging round trips with small chunks, subsets and odd sizes.
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from morph_amd import FusedAdamW
+from morph_amd.muon import HybridMuonAdamW
+from morph_amd.staging import HostStaging
+from tests.golden.make_golden import CONFIG1, config1_inputs
+from tests.helpers import assert_same_bits
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def test_host_staging_round_trips():
+    gen = torch.Generator().manual_seed(1)
+    shapes = [(7,), (1000, 3), (1,), (64, 65), (4099,)]
+    st = HostStaging(shapes, torch.float32, DEV, chunk_elements=1000)
+    host = [torch.randn(s, generator=gen) for s in shapes]
+    st.upload(host)
+    for h, v in zip(host, st.views):
+        assert torch.equal(v.cpu(), h)
+    # a subset: only those mirrors change, chunks span tensor boundaries
+    new = [torch.randn(shapes[i], generator=gen) for i in (1, 3)]
+    st.upload(new, [1, 3])
+    for i, v in enumerate(st.views):
+        expect = {1: new[0], 3: new[1]}.get(i, host[i])
+        assert torch.equal(v.cpu(), expect), i
+    out = [torch.empty(s) for s in shapes]
+    st.download(out)
+    for o, v in zip(out, st.views):
+        assert torch.equal(o, v.cpu())
+    st.views[2].fill_(5.0)
+    one = [torch.zeros(1)]
+    st.download(one, [2])
+    assert float(one[0]) == 5.0
+
+
+def test_fused_adamw_on_cpu_masters_config1():
+    """BASELINE config 1 (param groups: wd .1 on 2-D only) with CPU masters and CPU FP32
+    gradients: every step bit-exact against the oracle and against device masters."""
+    from oracle import reference as R
+    masters, grads = config1_inputs()
+    cpu = [m.clone() for m in masters]
+    dev = [m.to(DEV) for m in masters]
+    groups = lambda ps: [dict(params=[p for p in ps if p.ndim == 2], weight_decay=CONFIG1["wd_2d"]),
+                         dict(params=[p for p in ps if p.ndim == 1], weight_decay=0.0)]
+    kw = dict(lr=CONFIG1["lr"], betas=CONFIG1["betas"], eps=CONFIG1["eps"])
+    opt_c, opt_d = FusedAdamW(groups(cpu), **kw), FusedAdamW(groups(dev), **kw)
+    flat_c = [p for g in opt_c.param_groups for p in g["params"]]
+    flat_d = [p for g in opt_d.param_groups for p in g["params"]]
+    W = [p.numpy().ravel().copy() for p in flat_c]
+    M = [np.zeros_like(w) for w in W]
+    V = [np.zeros_like(w) for w in W]
+    index = {id(p): i for i, p in enumerate(cpu)}
+    for t in range(1, CONFIG1["steps"] + 1):
+        gs = grads(t)
+        for p in flat_c:
+            p.grad = gs[index[id(p)]].clone()          # CPU p.grad, as Slot.flush leaves it
+        for pc, pd in zip(flat_c, flat_d):
+            pd.grad = pc.grad.to(DEV)
+        opt_c.step()
+        opt_d.step()
+        for k, p in enumerate(flat_c):
+            wd = CONFIG1["wd_2d"] if p.ndim == 2 else 0.0
+            hp = R.torch_adamw_hp(CONFIG1["lr"], *CONFIG1["betas"], CONFIG1["eps"], wd, t)
+            R.adamw(p.grad.numpy().ravel(), W[k], M[k], V[k], hp)
+            assert p.device.type == "cpu"
+            assert_same_bits(p.numpy().ravel(), W[k], f"master {k}, step {t}")
+            assert torch.equal(p, flat_d[k].cpu())
+    sd = opt_c.state_dict()
+    for k in range(len(flat_c)):
+        s = sd["state"][k]
+        assert s["exp_avg"].device.type == "cpu" and float(s["step"]) == CONFIG1["steps"]
+        assert_same_bits(s["exp_avg"].numpy().ravel(), M[k], "exp_avg")
+        assert_same_bits(s["exp_avg_sq"].numpy().ravel(), V[k], "exp_avg_sq")
+
+
+class Tiny(nn.Module):
+    """Hidden Linear layers (Muon; both orientations), a LayerNorm and an lm_head (AdamW)."""
+
+    def __init__(self):
+        super().__init__()
+        self.up = nn.Linear(64, 192, bias=True)
+        self.down = nn.Linear(192, 64, bias=False)
+        self.gate = nn.Linear(64, 192, bias=False)
+        self.norm = nn.LayerNorm(64)
+        self.lm_head = nn.Linear(64, 32, bias=False)
+
+
+def _engine_grads(model, seed):
+    """What StreamTrainEngine leaves behind: CPU FP32 p.grad (engine.py:82-84)."""
+    gen = torch.Generator().manual_seed(seed)
+    for p in model.parameters():
+        p.grad = (torch.randn(p.shape, generator=gen) * 1e-3).to(p.device)
+
+
+def test_hybrid_on_cpu_masters_through_the_runner_sequence():
+    from oracle import reference as R
+    torch.manual_seed(0)
+    cpu_model = Tiny()
+    dev_model = copy.deepcopy(cpu_model).to(DEV)
+    opt_c = HybridMuonAdamW(cpu_model, lr=.003, muon_lr=.02)
+    opt_d = HybridMuonAdamW(dev_model, lr=.003, muon_lr=.02)
+    assert opt_c.host and not opt_d.host
+    adam_names = [n for n, _ in cpu_model.named_parameters()
+                  if n not in ("up.weight", "down.weight", "gate.weight")]
+    ow = {n: p.detach().numpy().ravel().copy() for n, p in cpu_model.named_parameters()
+          if n in adam_names}
+    om = {n: np.zeros_like(w) for n, w in ow.items()}
+    ov = {n: np.zeros_like(w) for n, w in ow.items()}
+    for step in range(1, 4):
+        opt_c.zero_grad(set_to_none=True)                  # runner.py:83
+        opt_d.zero_grad(set_to_none=True)
+        _engine_grads(cpu_model, step)                     # streaming.backward (:92)
+        _engine_grads(dev_model, step)
+        torch.nn.utils.clip_grad_norm_(cpu_model.parameters(), 1.0, error_if_nonfinite=True)
+        torch.nn.utils.clip_grad_norm_(dev_model.parameters(), 1.0, error_if_nonfinite=True)
+        for (n, pc), (_, pd) in zip(cpu_model.named_parameters(), dev_model.named_parameters()):
+            pd.grad.copy_(pc.grad)  # identical clipped gradients on both sides
+        opt_c.step()                                       # runner.py:101
+        opt_d.step()
+        for n, p in cpu_model.named_parameters():
+            if n in adam_names:
+                hp = R.torch_adamw_hp(.003, .9, .95, 1e-8, .01, step)
+                R.adamw(p.grad.numpy().ravel(), ow[n], om[n], ov[n], hp)
+    for (n, pc), (_, pd) in zip(cpu_model.named_parameters(), dev_model.named_parameters()):
+        assert pc.device.type == "cpu"
+        assert torch.equal(pc.detach(), pd.detach().cpu()), n
+        if n in adam_names:
+            assert_same_bits(pc.detach().numpy().ravel(), ow[n], n)
+    sd = opt_c.state_dict()                                # runner.py:66-74 checkpoint
+    assert set(sd) == {"momentum", "adam", "lr", "weight_decay"}
+    assert all(m.device.type == "cpu" for m in sd["momentum"].values())
+    for i, m in sd["momentum"].items():
+        assert torch.equal(m, opt_d.momentum[i].cpu())
+    for k, s in sd["adam"]["state"].items():
+        n = adam_names[k]
+        assert_same_bits(s["exp_avg"].numpy().ravel(), om[n], n)
+        assert_same_bits(s["exp_avg_sq"].numpy().ravel(), ov[n], n)
+    # restore into a fresh CPU model + optimizer (runner.py:62-63) and continue identically
+    saved = copy.deepcopy(sd)
+    model2 = copy.deepcopy(cpu_model)
+    opt2 = HybridMuonAdamW(model2, lr=.003, muon_lr=.02)
+    opt2.load_state_dict(saved)
+    for m, o in ((cpu_model, opt_c), (model2, opt2)):
+        o.zero_grad(set_to_none=True)
+        _engine_grads(m, 9)
+        o.step()
+    for (n, p), (_, q) in zip(cpu_model.named_parameters(), model2.named_parameters()):
+        assert torch.equal(p, q), n
+
+
+@pytest.mark.parametrize("poisoned", ["norm.weight", "up.weight", "down.weight"])
+def test_hybrid_on_cpu_masters_raises_before_any_mutation(poisoned):
+    torch.manual_seed(1)
+    model = Tiny()
+    twin = copy.deepcopy(model)
+    opt, opt2 = HybridMuonAdamW(model, lr=.003), HybridMuonAdamW(twin, lr=.003)
+    for o, m in ((opt, model), (opt2, twin)):
+        _engine_grads(m, 1)
+        o.step()
+    before = copy.deepcopy(model.state_dict())
+    saved = copy.deepcopy(opt.state_dict())
+    _engine_grads(model, 2)
+    dict(model.named_parameters())[poisoned].grad.view(-1)[3] = float("inf")
+    with pytest.raises(FloatingPointError):
+        opt.step()
+    for k, v in model.state_dict().items():
+        assert torch.equal(v, before[k]), k
+    after = opt.state_dict()
+    for i, m in after["momentum"].items():
+        assert torch.equal(m, saved["momentum"][i]), i
+    for k, s in after["adam"]["state"].items():
+        assert torch.equal(s["exp_avg"], saved["adam"]["state"][k]["exp_avg"])
+    for o, m in ((opt, model), (opt2, twin)):
+        _engine_grads(m, 3)
+        o.step()
+    for (n, p), (_, q) in zip(model.named_parameters(), twin.named_parameters()):
+        assert torch.equal(p, q), n
+
+
+def test_mixed_devices_are_rejected():
+    model = Tiny()
+    model.norm.to(DEV)
+    with pytest.raises(ValueError, match="on the GPU or all on the CPU"):
+        HybridMuonAdamW(model)
+    with pytest.raises(ValueError, match="one device"):
+        FusedAdamW([torch.zeros(4), torch.zeros(4, device=DEV)])
