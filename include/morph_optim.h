@@ -8,7 +8,9 @@
  * Conventions shared by every entry point:
  *   - Tensor pointers are device pointers owned by the caller.  The library
  *     allocates nothing and keeps no state between calls, so calls are
- *     re-entrant from several host threads.
+ *     re-entrant from several host threads.  The one exception is the
+ *     library-owned partials array of morph_grad_accumulate_final_noalloc
+ *     (see there).
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
  *     void*; NULL means the legacy default stream).  Ordering between calls
  *     comes only from the stream.
@@ -41,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 5
+#define MORPH_ABI_VERSION 6
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -289,6 +291,27 @@ int morph_grad_accumulate(const morph_accum_tensor* tensors, int count, int grad
  * order (deterministic for a given n). */
 int morph_sumsq_total(const double* d_partials, int64_t n, double* d_out, int accumulate,
                       void* stream);
+
+/*
+ * Allocation-free final pass.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Equals
+ * morph_grad_accumulate(..., flags | MORPH_ACCUM_FINAL, d_found_inf, partials,
+ * ...) followed by morph_sumsq_total(partials, n, d_sumsq, 0, ...), with the
+ * FP64 partials in a library-owned device array of MORPH_NOALLOC_MAX_PARTIALS
+ * doubles (8 MiB on each GPU it runs on, held until the process ends) instead
+ * of a caller workspace.  flags: 0 or MORPH_ACCUM_OVERWRITE.  *d_sumsq is
+ * overwritten; d_found_inf is ORed into.  Calls needing more partials than
+ * the maximum (morph_grad_partials > 2^20, i.e. more than 2^31 elements)
+ * return MORPH_ERANGE.  Calls no allocating routine.  Every call on one GPU
+ * uses that GPU's array and leaves its partials there: calls that can overlap
+ * on one GPU (streams not ordered with each other) race, so the caller
+ * serialises them.
+ */
+#define MORPH_NOALLOC_MAX_PARTIALS (1 << 20)
+int morph_grad_accumulate_final_noalloc(const morph_accum_tensor* tensors, int count,
+                                        int grad_dtype, double loss_scale, int flags,
+                                        uint32_t* d_found_inf, double* d_sumsq, void* stream);
 
 /* ---- Master-weight conversion --------------------------------------------
  * dst = dtype(src) elementwise (FP16: round to nearest even, overflow -> inf;

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmorph_optim.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_NONE, DTYPE_F32, DTYPE_F16, DTYPE_BF16 = -1, 0, 1, 2
 HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
@@ -23,7 +23,7 @@ EXPORTS = (
     "morph_abi_version", "morph_strerror", "morph_flag_clear", "morph_nonfinite_or",
     "morph_nonfinite_or_multi", "morph_adamw_fused", "morph_adamw_multi",
     "morph_adamw_multi_dev", "morph_step_end", "morph_nonfinite_or_close",
-    "morph_grad_partials", "morph_grad_accumulate",
+    "morph_grad_partials", "morph_grad_accumulate", "morph_grad_accumulate_final_noalloc",
     "morph_sumsq_total", "morph_convert_f32", "morph_fp8_pack", "morph_fp8_unpack",
     "morph_gemm_nt_bf16",
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
@@ -33,6 +33,7 @@ GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 256, 256, 64
 GEMM_SYMMETRIC = 1
 GEMM_Q_KN = 2
 ACCUM_ELEMS_PER_BLOCK, ACCUM_OVERWRITE, ACCUM_FINAL = 2048, 1, 2
+NOALLOC_MAX_PARTIALS = 1 << 20
 FP8_BLOCK = 256
 FATAL_MIN_SCALE = 1
 
@@ -123,6 +124,8 @@ def lib():
             "morph_grad_partials": ([ctypes.POINTER(AccumTensor), i32], i64),
             "morph_grad_accumulate": ([ctypes.POINTER(AccumTensor), i32, i32, ctypes.c_double, i32,
                                        vp, vp, i64, vp], i32),
+            "morph_grad_accumulate_final_noalloc": ([ctypes.POINTER(AccumTensor), i32, i32,
+                                                     ctypes.c_double, i32, vp, vp, vp], i32),
             "morph_sumsq_total": ([vp, i64, vp, i32, vp], i32),
             "morph_convert_f32": ([vp, vp, i32, i64, vp, vp], i32),
             "morph_fp8_pack": ([vp, i32, i64, vp, vp, vp], i32),

@@ -22,7 +22,15 @@
 // squares in a fixed order and a one-workgroup pass adds the partials in index
 // order, so the result is deterministic for a given layout.  Its last bits can
 // differ from the reference's chunked torch sum, whose order is different.
+#include <mutex>
+
 #include "common.h"
+
+// FP64 partials of morph_grad_accumulate_final_noalloc: a library-owned array
+// instead of a caller workspace (8 MiB per GPU, held until the process ends).
+// Host code never uses this name as an address: the per-device address comes
+// from hipGetSymbolAddress (noalloc_partials below).
+static __device__ __align__(256) double scratch[MORPH_NOALLOC_MAX_PARTIALS];
 
 namespace morph {
 namespace {
@@ -311,4 +319,57 @@ extern "C" int morph_sumsq_total(const double* d_partials, int64_t n, double* d_
   hipLaunchKernelGGL(partial_sum_kernel, dim3(1), dim3(1024), 0, as_stream(stream), d_partials, n,
                      d_out, accumulate != 0 ? 1 : 0);
   return launch_status();
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+double* g_scratch[kMaxDevices];  // device address of `scratch` per GPU, set on first use
+
+// The address of `scratch` on the GPU that `stream` belongs to (the current GPU
+// for the legacy default stream), looked up once per GPU with that GPU current.
+int noalloc_partials(hipStream_t stream, double** out) {
+  int current = 0;
+  if (hipGetDevice(&current) != hipSuccess) return MORPH_ELAUNCH;
+  int dev = current;
+  if (stream != nullptr) {
+    hipDevice_t d = 0;
+    if (hipStreamGetDevice(stream, &d) != hipSuccess) return MORPH_EINVAL;
+    dev = d;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return MORPH_ERANGE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    if (dev != current && hipSetDevice(dev) != hipSuccess) return MORPH_ELAUNCH;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != current) (void)hipSetDevice(current);
+    if (e != hipSuccess || p == nullptr) return MORPH_ELAUNCH;
+    g_scratch[dev] = static_cast<double*>(p);
+  }
+  *out = g_scratch[dev];
+  return MORPH_OK;
+}
+
+}  // namespace
+
+extern "C" int morph_grad_accumulate_final_noalloc(const morph_accum_tensor* tensors, int count,
+                                                   int grad_dtype, double loss_scale, int flags,
+                                                   uint32_t* d_found_inf, double* d_sumsq,
+                                                   void* stream) {
+  if (flags & ~MORPH_ACCUM_OVERWRITE) return MORPH_EINVAL;
+  if (d_found_inf == nullptr || d_sumsq == nullptr) return MORPH_EINVAL;
+  if (gbytes(grad_dtype) == 0) return MORPH_EDTYPE;
+  const int64_t need = morph_grad_partials(tensors, count);
+  if (need < 0) return (int)need;
+  if (need > MORPH_NOALLOC_MAX_PARTIALS) return MORPH_ERANGE;
+  double* partials = nullptr;
+  int rc = noalloc_partials(as_stream(stream), &partials);
+  if (rc != MORPH_OK) return rc;
+  // every partial the sum reads is written by this call's pass: nothing to clear
+  rc = morph_grad_accumulate(tensors, count, grad_dtype, loss_scale, flags | MORPH_ACCUM_FINAL,
+                             d_found_inf, partials, MORPH_NOALLOC_MAX_PARTIALS, stream);
+  if (rc != MORPH_OK) return rc;
+  return morph_sumsq_total(partials, need, d_sumsq, 0, stream);
 }

@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_status_strings():
     from morph_amd import _lib
     lib = _lib.lib()
-    assert lib.morph_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.morph_abi_version() == _lib.ABI_VERSION == 6
     assert lib.morph_strerror(0) == b"ok"
     for code in (-1, -2, -3, -4, -5):
         assert lib.morph_strerror(code) not in (b"ok", b"unknown morph status")
@@ -73,6 +73,13 @@ def test_argument_validation_happens_before_any_launch():
     assert close(None, None, 0, 1, st, 2, None, None, 0, None) == -1        # bad slot
     assert close(None, None, 0, 1, st, 0, None, None, 3, None) == -1        # clock list missing
     assert close(None, None, 0, 7, st, 0, None, None, 0, None) == -2        # unknown dtype
+    # allocation-free final pass: more partials than its array holds -> ERANGE, no launch
+    big = (_lib.AccumTensor * 1)()
+    big[0].grad, big[0].dst, big[0].numel = None, 0x10000, (1 << 31) + 1
+    assert lib.morph_grad_partials(big, 1) == _lib.NOALLOC_MAX_PARTIALS + 1
+    assert lib.morph_grad_accumulate_final_noalloc(big, 1, 1, 1.0, 0, st, st, None) == -4
+    big[0].numel = 1 << 31
+    assert lib.morph_grad_partials(big, 1) == _lib.NOALLOC_MAX_PARTIALS
     # GEMM: validated on the host (fake, aligned pointers are never dereferenced)
     p = ctypes.c_void_p(0x10000)
     gemm = lambda M, N, K, flags, Ct=None: lib.morph_gemm_nt_bf16(
