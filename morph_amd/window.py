@@ -19,6 +19,13 @@ after every partial write, flush and fsync -- the reference's durability and
 fault order (disk.py:215-223).  If anything raises, the parameter's resident
 state is dropped (it may be ahead of the file; the journal rolls the file
 back) and must be loaded again.
+
+The undo journal (disk.py:110-182) restores a stage's files when a fault hits
+between its first update and its commit.  ResidentDiskUpdate.recover_stage()
+keeps the window in step with that: the resident entries of the restored
+files (and those dropped by a failed update) are reloaded from the restored
+files, state and compute copy, as CachedDiskState drops its cache on the same
+rollback (state_cache.py:147-156).
 """
 import ctypes
 import os
@@ -75,6 +82,7 @@ class ResidentWindow:
         self.dispatch_timer = None  # optional kernels.DispatchTimer: stamps each update launch
         self._copy = torch.cuda.Stream(self.device)
         self._staging = None
+        self.dropped_on_error = set()  # dropped by a failed update(); ahead of their files
 
     # -- staging buffers ----------------------------------------------------
     def _slots(self):
@@ -118,6 +126,7 @@ class ResidentWindow:
                 os.close(fd)
             compute.wait_stream(self._copy)
             self.state[name] = dev
+            self.dropped_on_error.discard(name)
             self.transfer_bytes["h2d_state"] += 12 * size
             self._compute_copy(name, compute)
         for s in slots:
@@ -162,6 +171,7 @@ class ResidentWindow:
             self._write_back(name, dev, chunk_elements, compute)
         except BaseException:
             self.drop(name)
+            self.dropped_on_error.add(name)
             compute.synchronize()
             raise
 
@@ -242,3 +252,30 @@ class ResidentDiskUpdate:
         if self.window is not None and name in self.window.state:
             return self.window.update(name, gradient, step, lr, clip, chunk_elements)
         return super().update(name, gradient, step, lr, clip, chunk_elements)
+
+    def recover_stage(self):
+        """disk.py:110-128, with the window kept in step with the restored files.
+
+        A rollback (a transaction whose journal is set and present) copies the
+        journaled [3, N] files back over the stage's files.  A resident entry of
+        such a file may be one update ahead of it (the update succeeded, the commit
+        did not happen), and the slot's compute copy with it; an entry dropped by a
+        failed update left its compute copy ahead too.  Both are loaded again from
+        the restored files once the host class has restored them.
+        """
+        window = self.window
+        transaction = self.manifest.get("transaction")
+        journal = self.root / "journal"
+        reload = []
+        if (window is not None and transaction is not None
+                and transaction.get("journal") is not None and journal.exists()):
+            restored = {path.name for path in journal.glob("*.bin")}
+            reload = [n for n in window.names
+                      if self.entries[n]["file"] in restored
+                      and (n in window.state or n in window.dropped_on_error)]
+            for name in reload:
+                window.drop(name)
+        result = super().recover_stage()
+        if reload:
+            window.load(reload)
+        return result

@@ -7,9 +7,13 @@
   weights, and the fault hook fires after every partial write-back in file order;
 - morph_convert_f32: FP16 bits equal numpy's astype('<f2') and BF16 bits torch's
   conversion on edge cases (ties, overflow, subnormals, inf/NaN); the range flag is
-  export.py:33's condition.
+  export.py:33's condition;
+- rollback (disk.py:110-128): after a fault before the stage's commit or inside an
+  update, recover_stage() reloads the window from the restored files, the retried
+  update matches the oracle, and an export from the window equals one from the files.
 """
 import ctypes
+import shutil
 
 import numpy as np
 import pytest
@@ -168,3 +172,136 @@ def test_convert_bf16_bits_equal_torch_including_nan():
     exp = torch.from_numpy(x[~nan]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got[~nan], exp)
     assert (got[nan] == 0x7FC0).all()
+
+
+class JournalBase(Store):
+    """Store plus a minimal undo journal with the behaviour streamtrain/disk.py:110-174
+    gives recover_stage: prepare_stage copies the stage's files into root/journal and
+    records the stage in the transaction; commit_stage clears both; recover_stage copies
+    the journaled files back when the transaction still names a journal."""
+
+    def __init__(self, root, weights=None, entries=None):
+        if entries is None:
+            super().__init__(root, weights)
+        else:
+            self.root, self.entries, self.points = root, entries, []
+        self.manifest = dict(transaction=None)
+        self.fail_at = None
+
+    def fault(self, point):
+        self.points.append(point)
+        if point == self.fail_at:
+            raise RuntimeError(f"injected fault at {point}")
+
+    def begin(self):
+        self.manifest["transaction"] = dict(journal=None)
+
+    def prepare_stage(self, index, names):
+        journal = self.root / "journal"
+        shutil.rmtree(journal, ignore_errors=True)
+        journal.mkdir()
+        for name in names:
+            f = self.entries[name]["file"]
+            shutil.copyfile(self.root / f, journal / f)
+        self.fault("journal_durable")
+        self.manifest["transaction"]["journal"] = index
+
+    def commit_stage(self, index):
+        self.fault("cursor_file_durable")
+        self.manifest["transaction"]["journal"] = None
+        shutil.rmtree(self.root / "journal", ignore_errors=True)
+
+    def recover_stage(self):
+        transaction = self.manifest.get("transaction")
+        journal = self.root / "journal"
+        if transaction and transaction.get("journal") is not None:
+            for path in journal.glob("*.bin"):
+                shutil.copyfile(path, self.root / path.name)
+            transaction["journal"] = None
+        shutil.rmtree(journal, ignore_errors=True)
+
+
+class ResidentJournalStore(ResidentDiskUpdate, JournalBase):
+    pass
+
+
+def _grads(store, seed):
+    rng = np.random.RandomState(seed)
+    return {n: torch.from_numpy((rng.randn(e["size"]) * 1e-2).astype(np.float32)).to(DEV)
+            for n, e in store.entries.items()}
+
+
+@pytest.mark.parametrize("fail_at", ["cursor_file_durable", "partial_state_write"])
+def test_rollback_reloads_the_window_from_the_restored_files(tmp_path, fail_at):
+    """disk.py:110-128 / state_cache.py:147-156: a fault after the stage's updates
+    (before its commit) or inside one (after a partial write-back) leaves the window --
+    state and compute copy -- ahead of the files the journal restores.  recover_stage()
+    on the same store reloads it; the retried update then equals the oracle applied to
+    the restored file, and the compute copy equals the cast of the final weights."""
+    sizes = [3001, 250000]
+    store = ResidentJournalStore(tmp_path, {f"p{i}": (np.random.RandomState(i).randn(n) * .02)
+                                            for i, n in enumerate(sizes)})
+    names = list(store.entries)
+    before = {n: store.state(n).copy() for n in names}
+    slot = torch.empty(sum(sizes), dtype=torch.bfloat16, device=DEV)
+    store.window = ResidentWindow(store, names, torch.bfloat16, weights=slot)
+    store.window.load()
+    store.begin()
+    store.prepare_stage(0, names)
+    store.fail_at = fail_at
+    first = _grads(store, 5)
+    with pytest.raises(RuntimeError, match="injected fault"):
+        for name in names:
+            store.update(name, first[name], 1, .002, .5, chunk_elements=100000)
+        store.commit_stage(0)
+    store.fail_at = None
+    store.recover_stage()
+    torch.cuda.synchronize()
+    for name in names:
+        assert_same_bits(store.state(name), before[name], "restored file")
+        assert name in store.window.state
+        assert_same_bits(store.window.state[name].cpu().numpy(), before[name], "reloaded state")
+        got = store.window.weights[name].cpu().reshape(-1).view(torch.int16)
+        assert torch.equal(got, cpu_cast(before[name][0], torch.bfloat16).view(torch.int16))
+    # the retried stage
+    store.begin()
+    store.prepare_stage(0, names)
+    retry = _grads(store, 6)
+    for name in names:
+        store.update(name, retry[name], 1, .002, .5, chunk_elements=100000)
+    store.commit_stage(0)
+    torch.cuda.synchronize()
+    for name in names:
+        expect = oracle_disk(before[name][0], [(retry[name].cpu().numpy(), 1, .002, .5)])
+        assert_same_bits(store.state(name), expect, "file after the retried update")
+        assert_same_bits(store.window.state[name].cpu().numpy(), expect, "resident state")
+        got = store.window.weights[name].cpu().reshape(-1).view(torch.int16)
+        assert torch.equal(got, cpu_cast(expect[0], torch.bfloat16).view(torch.int16))
+
+
+def test_export_from_the_window_after_rollback_equals_the_files(tmp_path):
+    """export_fp16(window=...) encodes the resident rows; after a rollback they must be the
+    restored (committed) weights, so the shards equal an export from the files."""
+    from morph_amd.export import export_fp16
+    from tests.test_gpu_export import Tiny, make_state, same_dirs
+    model = Tiny()
+    state_dir = tmp_path / "state"
+    entries = make_state(state_dir, model)
+    store = ResidentJournalStore(state_dir, entries=entries)
+    names = list(entries)
+    store.window = ResidentWindow(store, names, torch.float16)
+    store.window.load()
+    store.begin()
+    store.prepare_stage(0, names)
+    store.fail_at = "cursor_file_durable"
+    grads = _grads(store, 7)
+    with pytest.raises(RuntimeError, match="injected fault"):
+        for name in names:
+            store.update(name, grads[name] * 100, 1, .5, 1.0)
+        store.commit_stage(0)
+    store.fail_at = None
+    store.recover_stage()
+    export_fp16(state_dir, tmp_path / "from_window", model=model, window=store.window,
+                lock_held=True)
+    export_fp16(state_dir, tmp_path / "from_files", model=model, lock_held=True)
+    same_dirs(tmp_path / "from_window", tmp_path / "from_files")
