@@ -66,13 +66,15 @@ def same_dirs(a, b):
             assert (a / name).read_bytes() == (b / name).read_bytes(), name
 
 
-@pytest.mark.parametrize("chunk", [100, 1048576])
-def test_export_matches_reference_bytes_and_manifest(tmp_path, chunk):
+@pytest.mark.parametrize("chunk,segment", [(100, 1 << 22), (100, 250), (1048576, 1 << 22)])
+def test_export_matches_reference_bytes_and_manifest(tmp_path, chunk, segment):
+    """segment 250 with chunk 100: rows move in segments of two chunks (bounded memory)."""
     model = Tiny()
     make_state(tmp_path / "run" / "state", model,
                edits={("gate.weight", 5): 65504.0, ("gate.weight", 6): -65504.0,
                       ("norm.weight", 0): 65503.9, ("norm.weight", 1): 1e-8})
-    got = export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", chunk, model=model)
+    got = export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", chunk, model=model,
+                      segment_elements=segment)
     ref = R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, chunk)
     assert got == ref
     assert got["aliases"] == {"lm_head.weight": "embedding.weight"}
@@ -80,12 +82,15 @@ def test_export_matches_reference_bytes_and_manifest(tmp_path, chunk):
 
 
 @pytest.mark.parametrize("bad", [65504.5, 65519.0, float("inf"), float("nan")])
-def test_unrepresentable_weight_raises_at_the_same_chunk(tmp_path, bad):
-    """65519 rounds to 65504 in FP16 but the reference still refuses it (|w| > 65504)."""
+@pytest.mark.parametrize("segment", [1 << 22, 512])
+def test_unrepresentable_weight_raises_at_the_same_chunk(tmp_path, bad, segment):
+    """65519 rounds to 65504 in FP16 but the reference still refuses it (|w| > 65504).
+    segment 512: the bad chunk (elements 512-767) opens the row's second segment."""
     model = Tiny()
     make_state(tmp_path / "run" / "state", model, edits={("gate.weight", 700): bad})
     with pytest.raises(ValueError, match="finite FP16"):
-        export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", 256, model=model)
+        export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", 256, model=model,
+                    segment_elements=segment)
     with pytest.raises(ValueError, match="finite FP16"):
         R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, 256)
     same_dirs(tmp_path / "gpu", tmp_path / "cpu")  # same complete and partial shards
@@ -124,6 +129,7 @@ def test_export_from_resident_window_equals_file_export(tmp_path):
     store.entries = entries
     win = ResidentWindow(store, list(entries), torch.float16)
     win.load()
-    export_fp16(tmp_path / "run" / "state", tmp_path / "win", 300, model=model, window=win)
+    export_fp16(tmp_path / "run" / "state", tmp_path / "win", 300, model=model, window=win,
+                segment_elements=600)
     R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, 300)
     same_dirs(tmp_path / "win", tmp_path / "cpu")
