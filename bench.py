@@ -92,6 +92,36 @@ class Config5(torch.nn.Module):
                     lin.weight.copy_(torch.randn(lin.weight.shape, generator=gen, device=device) * .02)
 
 
+def host_cpus():
+    """Cores for the CPU baselines: every core in this process's affinity mask
+    (len(os.sched_getaffinity(0))), bounded by a cgroup CPU quota when the container
+    sets one (/sys/fs/cgroup/cpu.max) -- threads beyond the quota only time-slice.
+    Sets torch's intra-op thread count and returns the figures the line reports."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        limit, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if limit != "max":
+            quota = int(limit) / int(period)
+    except (OSError, ValueError):
+        pass
+    threads = affinity if quota is None else max(1, min(affinity, int(quota)))
+    torch.set_num_threads(threads)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return dict(threads=threads, affinity=affinity, quota=quota, model=model)
+
+
+def cpu_fields(info):
+    """The baseline's core figures: threads used, affinity mask size, cgroup quota, CPU model."""
+    return dict(cores=info["threads"], affinity_cores=info["affinity"],
+                cgroup_cpu_quota=info["quota"], cpu_model=info["model"])
+
+
 # --------------------------------------------------------------- timing --
 GRAD_SETS = 3  # gradient sets cycled over the steps: 3 x 113 MB exceeds the 256 MB Infinity Cache
 STAMP_EVERY = 4  # every 4th AdamW launch of the timed steps stamps its own start/stop events
@@ -165,8 +195,7 @@ def cpu_baseline(seconds=10.0):
     steps until `seconds` have passed (at least 2) and reports the median.
     """
     from oracle import reference as R
-    threads = min(16, R.cpu_threads())
-    torch.set_num_threads(threads)
+    cpus = host_cpus()
     masters = config2_window("cpu")
     grads16 = config2_grads("cpu", 1000)
     params = [torch.nn.Parameter(m) for m in masters]
@@ -182,13 +211,8 @@ def cpu_baseline(seconds=10.0):
     times.sort()
     med = times[len(times) // 2]
     n = sum(p.numel() for p in params)
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
-    except (OSError, StopIteration):
-        pass
-    return dict(value=round(n / med / 1e9, 4), unit="Gparams/s", cores=threads, kind="port",
+    cpu = cpus["model"]
+    return dict(value=round(n / med / 1e9, 4), unit="Gparams/s", **cpu_fields(cpus), kind="port",
                 gbs_28b_equivalent=round(BYTES_PER_PARAM * n / med / 1e9, 2),
                 sample=f"config 2 window (N={n}), {len(times)} whole steps, median; "
                        f"torch.optim.AdamW(foreach=False) after FP16 unscale; CPU: {cpu}",
@@ -249,8 +273,7 @@ def cpu_baseline_muon():
     """The reference's FP32 Muon update (optimizer.py:55-61, torch CPU) on one [6144, 3072]
     matrix of the 42, scaled by 42 to a whole step (the 1M AdamW group is negligible)."""
     from oracle import reference as R
-    threads = min(16, R.cpu_threads())
-    torch.set_num_threads(threads)
+    cpus = host_cpus()
     gen = torch.Generator().manual_seed(7)
     p = torch.randn(6144, 3072, generator=gen) * .02
     g = torch.randn(6144, 3072, generator=gen) * 1e-3
@@ -259,7 +282,7 @@ def cpu_baseline_muon():
     t0 = time.perf_counter()
     R.muon_reference_step(p, g, m, .02, .01)
     one = time.perf_counter() - t0
-    return dict(value=round(42 * one * 1e3, 1), unit="ms/step", cores=threads, kind="port",
+    return dict(value=round(42 * one * 1e3, 1), unit="ms/step", **cpu_fields(cpus), kind="port",
                 sample=f"one [6144, 3072] Muon matrix (FP32 NS, torch CPU) = {one * 1e3:.1f} ms, "
                        "x42 for the step")
 
@@ -334,8 +357,7 @@ def cpu_baseline_grads():
     """The reference's torch ops on the host (sparse_disk.py:106-107, disk.py:466-468): one
     plain micro-batch pass over the config-2 window plus the chunked FP64 norm pass."""
     from oracle import reference as R
-    threads = min(16, R.cpu_threads())
-    torch.set_num_threads(threads)
+    cpus = host_cpus()
     grads = config2_grads("cpu", 2000)
     window = [torch.zeros(s) for s in CONFIG2_SHAPES]
     n = sum(w.numel() for w in window)
@@ -349,7 +371,7 @@ def cpu_baseline_grads():
     R.norm_squared_torch(window)
     t_norm = time.perf_counter() - t0
     return dict(value=round(n / t_acc / 1e9, 4), unit="Gparams/s per micro-batch pass",
-                cores=threads, kind="port",
+                **cpu_fields(cpus), kind="port",
                 sample=f"config 2 window (N={n}): one add_(g.float()/scale) pass {t_acc * 1e3:.1f} ms; "
                        f"the FP64 chunked norm pass {t_norm * 1e3:.1f} ms")
 
@@ -448,8 +470,7 @@ def cpu_baseline_window(root):
     write-back, flush, fsync) on one [6144, 3072] parameter file of the window."""
     import numpy as np
     from oracle import reference as R
-    threads = min(16, R.cpu_threads())
-    torch.set_num_threads(threads)
+    cpus = host_cpus()
     store = _FileStore(root, [("w", CONFIG2_SHAPES[0])], seed=1)
     e = store.entries["w"]
     g = torch.randn(e["size"], generator=torch.Generator().manual_seed(2)) * 1e-4
@@ -463,7 +484,7 @@ def cpu_baseline_window(root):
     os.fsync(fd)
     os.close(fd)
     t = time.perf_counter() - t0
-    return dict(value=round(e["size"] / t / 1e9, 4), unit="Gparams/s", cores=threads, kind="port",
+    return dict(value=round(e["size"] / t / 1e9, 4), unit="Gparams/s", **cpu_fields(cpus), kind="port",
                 sample=f"DiskState.update of one [6144, 3072] state file ({e['size']} params): "
                        f"{t * 1e3:.0f} ms incl. memmap I/O, flush and fsync")
 
@@ -554,8 +575,7 @@ def time_fp8(steps, warmup):
 def cpu_baseline_fp8():
     """The reference's pack_fp8 / unpack_fp8 (torch CPU ops) on one [6144, 3072] FP16 weight."""
     from oracle import reference as R
-    threads = min(16, R.cpu_threads())
-    torch.set_num_threads(threads)
+    cpus = host_cpus()
     w = (torch.randn(6144, 3072, generator=torch.Generator().manual_seed(9)) * .02).half()
     t0 = time.perf_counter()
     enc, sc = R.pack_fp8_torch(w)
@@ -563,7 +583,7 @@ def cpu_baseline_fp8():
     t0 = time.perf_counter()
     R.unpack_fp8_torch(enc, sc, torch.float16)
     t_unpack = time.perf_counter() - t0
-    return dict(value=round(w.numel() / t_pack / 1e9, 4), unit="Gparams/s (pack)", cores=threads,
+    return dict(value=round(w.numel() / t_pack / 1e9, 4), unit="Gparams/s (pack)", **cpu_fields(cpus),
                 kind="port", sample=f"one [6144, 3072] FP16 weight: pack {t_pack * 1e3:.0f} ms, "
                                     f"unpack {t_unpack * 1e3:.0f} ms ({w.numel() / t_unpack / 1e9:.3f} Gparam/s)")
 
@@ -639,8 +659,7 @@ def cpu_baseline_embedding(seconds=20.0):
     (BF16 gradient widened to FP32, wd 0): whole steps until `seconds` have passed (at
     least 2), median."""
     from oracle import reference as R
-    threads = min(16, R.cpu_threads())
-    torch.set_num_threads(threads)
+    cpus = host_cpus()
     w = torch.nn.Parameter(torch.randn(EMBED_SHAPE, generator=torch.Generator().manual_seed(3)) * .02)
     g16, _ = config3_embedding_grad(3000)
     opt = torch.optim.AdamW([w], lr=3e-4, betas=(.9, .95), eps=1e-8, weight_decay=0.0,
@@ -654,7 +673,7 @@ def cpu_baseline_embedding(seconds=20.0):
         times.append(time.perf_counter() - t0)
     times.sort()
     med = times[len(times) // 2]
-    return dict(value=round(w.numel() / med / 1e9, 4), unit="Gparams/s", cores=threads,
+    return dict(value=round(w.numel() / med / 1e9, 4), unit="Gparams/s", **cpu_fields(cpus),
                 kind="port", sample=f"[65536, 3072] embedding, {len(times)} whole steps, median; "
                                     "torch.optim.AdamW(foreach=False), BF16 grad widened to FP32")
 
