@@ -33,6 +33,9 @@ TRAFFIC_PROFILE = ROOT / "profiles" / "adamw_config2_traffic.json"
 TRAFFIC_PROFILE_C3 = ROOT / "profiles" / "adamw_config3_traffic.json"
 MFMA_PROFILE = ROOT / "profiles" / "muon_config5_mfma.json"
 TRAFFIC_PROFILE_GRADS = ROOT / "profiles" / "grads_config2_traffic.json"
+# rocprofv3 counters cannot run inside this process: `traffic` is read from the committed
+# summary of the FETCH_SIZE / WRITE_SIZE passes over this same workload, not measured here
+TRAFFIC_SOURCE = "profiles/%s: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes of this workload (committed, not this run)"
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_PARAM = 28  # read g16 2 + w 4 + m 4 + v 4; write w 4 + m 4 + v 4 + export 2
 CONFIG2_SHAPES = [(6144, 3072), (6144, 3072), (3072, 6144)]  # W_gate, W_up, W_down (nn.Linear storage)
@@ -394,6 +397,7 @@ def grads_main(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(TRAFFIC_PROFILE_GRADS),
+                     "traffic_source": TRAFFIC_SOURCE % TRAFFIC_PROFILE_GRADS.name,
                      "kernel": "accumulate_kernel<F16,false,false> (plain pass)",
                      "avg_launch_us": round(r["avg_pass_s"] * 1e6, 2),
                      "bytes_per_launch": ACCUM_BYTES * n},
@@ -699,6 +703,7 @@ def embedding_main(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(TRAFFIC_PROFILE_C3),
+                     "traffic_source": TRAFFIC_SOURCE % TRAFFIC_PROFILE_C3.name,
                      "kernel": "adamw_multi_kernel<BF16,BF16,dev>",
                      "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
                      "bytes_per_launch": BYTES_PER_PARAM * n},
@@ -942,6 +947,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
+                     "traffic_source": TRAFFIC_SOURCE % TRAFFIC_PROFILE.name,
                      "kernel": "adamw_multi_kernel<F16,F16,dev>",
                      "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
                      "bytes_per_launch": BYTES_PER_PARAM * n},

@@ -195,7 +195,7 @@ int morph_adamw_fused(const void* grad, int grad_dtype, float* param, float* exp
 
 /*
  * Multi-tensor form: `count` tensors (any count; the library splits it
- * into launches of at most 32 tensors) sharing one grad and one export dtype.
+ * into launches of at most 48 tensors) sharing one grad and one export dtype.
  * Each tensor selects its constants by hp_index into hps[0..n_hp).  This is
  * the whole AdamW group of HybridMuonAdamW (optimizer.py:40, 62) or one
  * stage window in one launch.  start_event / stop_event: as for
