@@ -80,6 +80,53 @@ def test_config1_against_live_torch_adamw(oracle):
             assert np.abs(W[i] - w_ref).max() / np.abs(w_ref).max() <= 1e-6
 
 
+def _finish_step(w, m, v_sqrt, hp):
+    """The master's part of torch's step after the moments, in numpy binary32 (one IEEE
+    rounding per operation, as torch's CPU kernels round them), with the square root of
+    the new second moment given: p *= 1 - lr * wd (adam.py:416-419, when wd != 0);
+    d = sqrt(v) / bias_correction2_sqrt + eps; p = p + (-step_size * m) / d (544-547)."""
+    f = np.float32
+    if hp.flags & 4:  # MORPH_HP_APPLY_DECAY
+        w = w * f(hp.decay)
+    d = v_sqrt / f(hp.bias_correction2_sqrt) + f(hp.eps)
+    return w + (f(hp.neg_step_size) * m) / d
+
+
+def test_config1_every_master_difference_is_torchs_sqrt(oracle):
+    """Per element, over config 1's 10 steps: the master update restated in binary32 with
+    torch's own sqrt of the (bit-exact) second moment gives torch.optim.AdamW's masters bit
+    for bit, and with the correctly rounded sqrt gives the oracle's (which the GPU kernel
+    equals bit for bit).  So the masters differ from torch only where torch's CPU sqrt
+    rounds differently, element by element -- not merely within a norm-wise bound."""
+    masters, grads = config1_inputs()
+    params = [torch.nn.Parameter(m.clone()) for m in masters]
+    groups = [dict(params=[p for p in params if p.ndim == 2], weight_decay=.1),
+              dict(params=[p for p in params if p.ndim == 1], weight_decay=0.)]
+    opt = torch.optim.AdamW(groups, lr=3e-4, betas=(.9, .95), eps=1e-8, foreach=False)
+    W = [m.numpy().ravel().copy() for m in masters]          # oracle (correctly rounded sqrt)
+    T = [w.copy() for w in W]                                 # restatement, torch's sqrt
+    I = [w.copy() for w in W]                                 # restatement, IEEE sqrt
+    M = [np.zeros_like(w) for w in W]
+    V = [np.zeros_like(w) for w in W]
+    differing = 0
+    for t in range(1, 11):
+        gs = grads(t)
+        for p, g in zip(params, gs):
+            p.grad = g.clone()
+        opt.step()
+        for i, g in enumerate(gs):
+            hp = oracle.torch_adamw_hp(3e-4, .9, .95, 1e-8, .1 if g.ndim == 2 else 0., t)
+            oracle.adamw(g.numpy().ravel(), W[i], M[i], V[i], hp)
+            assert (bits(M[i]) == bits(opt.state[params[i]]["exp_avg"].numpy().ravel())).all()
+            T[i] = _finish_step(T[i], M[i], torch.from_numpy(V[i]).sqrt().numpy(), hp)
+            I[i] = _finish_step(I[i], M[i], np.sqrt(V[i]), hp)
+            w_torch = params[i].detach().numpy().ravel()
+            assert (bits(T[i]) == bits(w_torch)).all(), (t, i)
+            assert (bits(I[i]) == bits(W[i])).all(), (t, i)
+            differing += int((bits(W[i]) != bits(w_torch)).sum())
+    assert differing > 0  # the comparison is not vacuous: torch's sqrt did round differently
+
+
 def test_first_step_bitexact_where_torch_sqrt_is_exact(oracle):
     """From identical inputs, masters differ only where torch's sqrt rounds low."""
     gen = torch.Generator().manual_seed(5)
