@@ -712,6 +712,73 @@ def embedding_main(args):
     print(json.dumps(line), flush=True)
 
 
+def time_streamed(steps, warmup, muon=False):
+    """The streamed engines' layout (runner.py:41-46, engine.py:75-88): FP32 masters and
+    FP32 (already unscaled) gradients in pageable CPU memory, optimizer state resident in
+    HBM.  A step uploads every gradient and master through pinned staging, runs the
+    device step on the mirrors, and writes the masters back into the CPU tensors before
+    step() returns (morph_amd.staging).  muon=False: FusedAdamW over the config-2 window;
+    muon=True: HybridMuonAdamW over config 5 (42 matrices + the AdamW vectors)."""
+    from morph_amd import FusedAdamW
+    from morph_amd.muon import HybridMuonAdamW
+    cpus = host_cpus()  # the host copies run on torch's intra-op threads
+    if muon:
+        model = Config5("cpu")
+        gen = torch.Generator().manual_seed(6)
+        for p in model.parameters():
+            p.grad = torch.randn(p.shape, generator=gen) * 1e-3
+        opt = HybridMuonAdamW(model, lr=3e-4, muon_lr=0.02)
+        params = list(model.parameters())
+        stagings = [opt._muon_masters, opt._muon_grads, opt.adam._staging]
+    else:
+        params = [torch.nn.Parameter(m) for m in config2_window("cpu")]
+        for p, g in zip(params, config2_grads("cpu", 1000)):
+            p.grad = g.float() / LOSS_SCALE
+        opt = FusedAdamW(params, **HYPER)
+        stagings = [opt._staging]
+    for _ in range(warmup):
+        opt.step()
+    if not muon:
+        stagings.append(opt._grad_staging)
+    else:
+        stagings.append(opt.adam._grad_staging)
+    torch.cuda.synchronize()
+    h2d0 = sum(st.bytes_h2d for st in stagings)
+    d2h0 = sum(st.bytes_d2h for st in stagings)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        opt.step()  # returns with the new masters in the CPU tensors
+    elapsed = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    return dict(elapsed=elapsed, n=sum(p.numel() for p in params), cpus=cpus,
+                h2d=(sum(st.bytes_h2d for st in stagings) - h2d0) / steps,
+                d2h=(sum(st.bytes_d2h for st in stagings) - d2h0) / steps)
+
+
+def streamed_main(args, muon=False):
+    r = time_streamed(args.steps, args.warmup, muon)
+    n, t = r["n"], r["elapsed"] / args.steps
+    line = {
+        "metric": ("HybridMuonAdamW step" if muon else "AdamW step") + " with CPU FP32 masters "
+                  "(streamed engines), PCIe included, 1 MI355X",
+        "value": round(n / t / 1e9, 3), "unit": "Gparams/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(t * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": ("config 5 (42 x [3072, 6144] Muon + 326 AdamW vectors)" if muon
+                                else "config-2 window (N = 56,623,104)") +
+                               " with FP32 masters and FP32 gradients in pageable CPU memory; "
+                               "state resident in HBM; step = upload gradients and masters, "
+                               "device step, masters back into the CPU tensors",
+                   "params": n},
+        "pcie": {"h2d_bytes_per_step": int(r["h2d"]), "d2h_bytes_per_step": int(r["d2h"]),
+                 "h2d_plus_d2h_gb_per_s": round((r["h2d"] + r["d2h"]) / t / 1e9, 2),
+                 "host_threads": r["cpus"]["threads"]},
+        "cpu_baseline": None if args.no_cpu_baseline else (
+            cpu_baseline_muon() if muon else cpu_baseline()),
+    }
+    print(json.dumps(line), flush=True)
+
+
 CONFIG4_STEPS = 16
 CONFIG4_OVERFLOW = (3, 7, 12)
 
@@ -868,12 +935,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("adamw", "embedding", "overflow", "muon", "grads",
-                                           "window", "fp8"),
+                                           "window", "fp8", "streamed", "streamed_muon"),
                     default="adamw",
                     help="adamw: the headline config-2 step (default); embedding: config 3; "
                          "overflow: config 4's skip sequence; muon: config 5; "
                          "grads: the stage-gradient window; window: the HBM-resident [3, N] "
-                         "state; fp8: block-scaled FP8 transport encoding")
+                         "state; fp8: block-scaled FP8 transport encoding; streamed / "
+                         "streamed_muon: config 2 / config 5 with CPU FP32 masters, PCIe included")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()
@@ -903,6 +971,8 @@ def main():
         return grads_main(args)
     if args.workload == "window":
         return window_main(args)
+    if args.workload in ("streamed", "streamed_muon"):
+        return streamed_main(args, muon=args.workload == "streamed_muon")
     if args.workload == "fp8":
         return fp8_main(args)
     r = time_gpu(args.steps, args.warmup)
