@@ -416,7 +416,7 @@ size_t morph_muon_workspace_bytes(int64_t rows, int64_t cols, int count);
  * One Muon step for `count` (<= 64) matrices of one shape (in either
  * orientation), batched: momentum and Nesterov blend (fp32, torch's rounding),
  * Frobenius normalisation, ns_steps Newton-Schulz iterations in bf16 on MFMA
- * (A = X X^T, B = b A + c A A, X = a X + B X, fp32 accumulation), and the fp32
+ * (A = X X^T, B' = b A + c A A + a I, X = B' X, fp32 accumulation), and the fp32
  * master update p = p * decay + (U * scale) * neg_lr with U in p's layout
  * (transposed back when p has more rows than columns, optimizer.py:15-17, 22)
  * and scale = update_scale or update_scale_transposed by the matrix's

@@ -103,6 +103,7 @@ struct GemmArgs {
   int64_t sp, sq, sd, sc, sct;
   float alpha, beta;
   const float* bscale;       // optional per-matrix factor of alpha and beta (device)
+  float diag;                // added to the diagonal elements of a symmetric product
   int32_t tiles_m, tiles_n;
   int32_t tiles_per_matrix;  // tiles_m * tiles_n, or the upper triangle when symmetric
   int32_t flags;             // MORPH_GEMM_SYMMETRIC
@@ -158,7 +159,7 @@ __device__ __forceinline__ void store_tile(const uint16_t* E, uint16_t* dst, uin
 // element (wr + 32 i + 8 (r / 4) + 4 fh + r % 4, wc + 32 j + fr).  The D mode
 // and the alpha multiply are template parameters so that each variant is
 // straight-line code.
-template <int kDMode, bool kScaled>
+template <int kDMode, bool kScaled, bool kDiag>
 __device__ __forceinline__ void epilogue(const GemmArgs& g, float alpha, float beta,
                                          f32x16 (&acc)[4][4], uint16_t* smem, const uint16_t* D,
                                          uint16_t* C, uint16_t* T, int64_t ldt) {
@@ -209,6 +210,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, float alpha, float b
         x[r] = kScaled ? alpha * acc[i][j][r] : acc[i][j][r];
         if (kDMode != kNoD) x[r] = __fmaf_rn(beta, dval[r], x[r]);
       }
+      if constexpr (kDiag) {
+        // a diagonal tile: its diagonal runs through the blocks i == j of waves 0 and 3
+        if (i == j && wr == wc) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (rbase + (r >> 2) * 8 + (r & 3) == col) x[r] = x[r] + g.diag;
+        }
+      }
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         // w: rows row and row + 1 of column col
@@ -217,7 +226,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, float alpha, float b
         E[row * LDE + col] = (uint16_t)w;
         E[(row + 1) * LDE + col] = (uint16_t)(w >> 16);
       }
-      if (kDMode != kNoD || kScaled) {
+      if (kDMode != kNoD || kScaled || kDiag) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = x[r];
       }
@@ -522,17 +531,24 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
     alpha *= s;
     beta *= s;
   }
-  // alpha == 1 (A = X X^T, X' = a X + B X) skips the multiply, which is exact then
-  if (alpha == 1.0f) {
+  // alpha == 1 (A = X X^T, X' = B' X) skips the multiply, which is exact then.  The
+  // diagonal add runs only in diagonal tiles of a symmetric product (B' = B + a I).
+  const bool diag = (g.flags & MORPH_GEMM_SYMMETRIC) && tr == tc && g.diag != 0.0f;
+  if (diag) {
     if (D == nullptr)
-      epilogue<kNoD, false>(g, alpha, beta, acc, smem, nullptr, C, T, ldt);
+      epilogue<kNoD, true, true>(g, alpha, beta, acc, smem, nullptr, C, T, ldt);
     else
-      epilogue<kDRowMajor, false>(g, alpha, beta, acc, smem, D, C, T, ldt);
+      epilogue<kDRowMajor, true, true>(g, alpha, beta, acc, smem, D, C, T, ldt);
+  } else if (alpha == 1.0f) {
+    if (D == nullptr)
+      epilogue<kNoD, false, false>(g, alpha, beta, acc, smem, nullptr, C, T, ldt);
+    else
+      epilogue<kDRowMajor, false, false>(g, alpha, beta, acc, smem, D, C, T, ldt);
   } else {
     if (D == nullptr)
-      epilogue<kNoD, true>(g, alpha, beta, acc, smem, nullptr, C, T, ldt);
+      epilogue<kNoD, true, false>(g, alpha, beta, acc, smem, nullptr, C, T, ldt);
     else
-      epilogue<kDRowMajor, true>(g, alpha, beta, acc, smem, D, C, T, ldt);
+      epilogue<kDRowMajor, true, false>(g, alpha, beta, acc, smem, D, C, T, ldt);
   }
 }
 
@@ -544,8 +560,8 @@ int morph::gemm_nt_bf16_scaled(const uint16_t* P, const uint16_t* Q, const uint1
                                int64_t batch, int64_t ldp, int64_t ldq, int64_t ldd,
                                int64_t ldc, int64_t ldct, int64_t stride_p, int64_t stride_q,
                                int64_t stride_d, int64_t stride_c, int64_t stride_ct,
-                               float alpha, float beta, const float* bscale, int flags,
-                               void* stream) {
+                               float alpha, float beta, const float* bscale, float diag,
+                               int flags, void* stream) {
   if (P == nullptr || Q == nullptr || C == nullptr || M < 0 || N < 0 || K <= 0 || batch < 0)
     return MORPH_EINVAL;
   auto misaligned = [](const void* p, uintptr_t a) {
@@ -565,6 +581,7 @@ int morph::gemm_nt_bf16_scaled(const uint16_t* P, const uint16_t* Q, const uint1
       (D && (ldd | stride_d) % 8) || (Ct && (ldct | stride_ct) % 8))
     return MORPH_EINVAL;
   if (symmetric && (M != N || Ct != nullptr || qkn)) return MORPH_EINVAL;
+  if (diag != 0.0f && !symmetric) return MORPH_EINVAL;
   // operand-load and epilogue offsets inside a tile are 32-bit: 255 rows of
   // the widest leading dimension
   constexpr int64_t kMaxLd = int64_t(1) << 23;
@@ -597,7 +614,7 @@ int morph::gemm_nt_bf16_scaled(const uint16_t* P, const uint16_t* Q, const uint1
   const int64_t grid = (total + 7) / 8 * 8;
   if (per > (int64_t(1) << 31) - 1 || grid > (int64_t(1) << 31) - 1) return MORPH_ERANGE;
   GemmArgs g{P, Q, D, C, Ct, K, ldp, ldq, ldd, ldc, ldct,
-             stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta, bscale,
+             stride_p, stride_q, stride_d, stride_c, stride_ct, alpha, beta, bscale, diag,
              (int32_t)tm, (int32_t)tn, (int32_t)per, flags, total};
   if (qkn)
     hipLaunchKernelGGL(gemm_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0,
@@ -617,6 +634,6 @@ extern "C" int morph_gemm_nt_bf16(const uint16_t* P, const uint16_t* Q, const ui
                                   int64_t stride_d, int64_t stride_c, int64_t stride_ct,
                                   float alpha, float beta, int flags, void* stream) {
   return gemm_nt_bf16_scaled(P, Q, D, C, Ct, M, N, K, batch, ldp, ldq, ldd, ldc, ldct, stride_p,
-                             stride_q, stride_d, stride_c, stride_ct, alpha, beta, nullptr, flags,
+                             stride_q, stride_d, stride_c, stride_ct, alpha, beta, nullptr, 0.0f, flags,
                              stream);
 }

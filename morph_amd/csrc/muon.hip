@@ -7,7 +7,8 @@
 //   momentum.lerp_(g, mom_w)                    fma(mom_w, g - m, m)           (58)
 //   u = g.lerp(momentum, nesterov_w)            fma(nesterov_w - 1, m - g, m)  (59)
 //   X = u (or u^T when rows > cols) / (|u|_F + 1e-7)                      (15-18)
-//   5x: A = X X^T; X = a X + (b A + c A A) X    bf16 operands, fp32 accum   (19-21)
+//   5x: A = X X^T; B' = b A + c A A + a I; X = B' X                        (19-21)
+//       bf16 operands, fp32 accumulation
 //   p = p * decay + (U * scale) * neg_lr        U = X in p's layout           (60-61)
 //
 // The reference computes orthogonalize in FP32; here X, A and B are bf16 (the
@@ -18,14 +19,19 @@
 // the normalisation per matrix, A = X0 X0^T / den^2 and X' = (a X0 + B X0) /
 // den, so u never goes to memory.  The elementwise steps round exactly like
 // torch (explicit fmaf where its CPU kernels fuse, plain multiplies elsewhere).
+// The quintic's linear term rides on B's diagonal: X' = a X + B X = (B + a I) X,
+// so the last product of an iteration reads no third operand (a is added in fp32
+// to B's diagonal before its bf16 rounding; measured against the FP32
+// reference this is as accurate as the separate a X term or more).
 //
 // Workspace (caller-allocated, zero-filled once; morph_muon_workspace_bytes):
 // per-block partial sums f64; per-matrix 1/den, 1/den^2, den f32;
-// X0/X1 [count][Mp][Np] (iterations alternate: X' = a X + B X reads all of X
-// as its [K, N] operand, so it cannot overwrite it), A and B [count][Mp][Mp],
-// bf16, with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.
-// The zero padding is exact for Newton-Schulz: padded rows of X give zero rows
-// and columns of A and B, which keep the padding of X zero in every iteration.
+// X0/X1 [count][Mp][Np] (iterations alternate: X' = B' X reads all of X as its
+// [K, N] operand, so it cannot overwrite it), A and B' [count][Mp][Mp], bf16,
+// with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.  The
+// zero padding is exact for Newton-Schulz: padded rows of X give zero rows and
+// columns of A, and of B' apart from its diagonal (a on every diagonal
+// element), so a padded row of X' is a times the padded row of X: zero again.
 // Rows are stored kRowPad elements longer than Mp / Np (never read): with
 // rows a multiple of 4 KiB apart, the 256 rows of a GEMM operand tile fall
 // on few L2 channels; the pad spreads them (about 6% on the K = Mp products).
@@ -553,21 +559,23 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
   for (int it = 0; it < hp->ns_steps; ++it) {
     uint16_t* X = W.X[cur];
     // X0 = bf16(u) is not normalised yet: the first iteration's products take
-    // the per-matrix factors, A = (X0 X0^T) / den^2 and X' = (B X0 + a X0) / den
+    // the per-matrix factors, A = (X0 X0^T) / den^2 and X' = (B' X0) / den
     const float* inv_den = it == 0 ? W.scale : nullptr;
     const float* inv_den2 = it == 0 ? W.scale + count : nullptr;
     // A = X X^T (symmetric: upper triangle of tiles, mirrored)
     rc = gemm_nt_bf16_scaled(X, X, nullptr, W.A, nullptr, L.mp, L.mp, L.np, count, n, n, 0, m, 0,
-                             sx, sx, 0, ss, 0, 1.0f, 0.0f, inv_den2, MORPH_GEMM_SYMMETRIC, stream);
-    if (rc) return rc;
-    // B = c (A A^T) + b A (symmetric)
-    rc = morph_gemm_nt_bf16(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, m, m, m, m, 0,
-                            ss, ss, ss, ss, 0, hp->c, hp->b, MORPH_GEMM_SYMMETRIC, stream);
-    if (rc) return rc;
-    // X' = B X + a X: X as the [K, N] operand (transposing LDS reads), into the other buffer
-    rc = gemm_nt_bf16_scaled(W.B, X, X, W.X[cur ^ 1], nullptr, L.mp, L.np, L.mp, count, m, n, n,
-                             n, 0, ss, sx, sx, sx, 0, 1.0f, hp->a, inv_den, MORPH_GEMM_Q_KN,
+                             sx, sx, 0, ss, 0, 1.0f, 0.0f, inv_den2, 0.0f, MORPH_GEMM_SYMMETRIC,
                              stream);
+    if (rc) return rc;
+    // B' = c (A A^T) + b A + a I (symmetric; a added on the diagonal before rounding)
+    rc = gemm_nt_bf16_scaled(W.A, W.A, W.A, W.B, nullptr, L.mp, L.mp, L.mp, count, m, m, m, m, 0,
+                             ss, ss, ss, ss, 0, hp->c, hp->b, nullptr, hp->a, MORPH_GEMM_SYMMETRIC,
+                             stream);
+    if (rc) return rc;
+    // X' = B' X: X as the [K, N] operand (transposing LDS reads), into the other buffer
+    rc = gemm_nt_bf16_scaled(W.B, X, nullptr, W.X[cur ^ 1], nullptr, L.mp, L.np, L.mp, count, m,
+                             n, 0, n, 0, ss, sx, 0, sx, 0, 1.0f, 0.0f, inv_den, 0.0f,
+                             MORPH_GEMM_Q_KN, stream);
     if (rc) return rc;
     cur ^= 1;
   }

@@ -297,13 +297,14 @@ def newton_schulz_bf16_emulated(u, steps=5, coeffs=(3.4445, -4.775, 2.0315), rou
     """The bf16 Newton-Schulz chain of the GPU kernels, emulated with torch fp32 products.
 
     Same algorithm as streamtrain/optimizer.py:13-22 (transpose the taller matrix,
-    X / (|X|_F + 1e-7), `steps` quintic iterations, transpose back) with the GPU's
-    rounding points:
+    X / (|X|_F + 1e-7), `steps` quintic iterations, transpose back), with the
+    quintic's linear term carried on B's diagonal (a X + B X = (B + a I) X) and the
+    GPU's rounding points:
       den = fp32(sqrt(sum u^2 in binary64)) + fp32(1e-7);  X0 = bf16(u)
-      iteration 0:  A = bf16(fp32(1 / den^2) * X0 X0^T)
-                    B = bf16(fma(b, A, c * A A^T))
-                    X = bf16(fma(a / den, X0, (1 / den) * B X0))
-      later:        A = bf16(X X^T); B as above; X = bf16(fma(a, X, B X))
+      iteration 0:  A  = bf16(fp32(1 / den^2) * X0 X0^T)
+                    B' = bf16(fma(b, A, c * A A^T) + a on the diagonal)
+                    X  = bf16((1 / den) * B' X0)
+      later:        A = bf16(X X^T); B' as above; X = bf16(B' X)
     with every product accumulated in fp32 (here: torch's fp32 matmul of the bf16
     values, exact per term, in its own summation order).  rounding=False skips the
     bf16 roundings (X0 = u), which leaves the FP32 reference up to fp32 rounding.
@@ -325,12 +326,11 @@ def newton_schulz_bf16_emulated(u, steps=5, coeffs=(3.4445, -4.775, 2.0315), rou
         first = it == 0
         A = X @ X.T
         A = rnd(A * inv_den2 if first else A)
-        B = rnd(_fma32(b, A, A @ A.T * c))
+        B = _fma32(b, A, A @ A.T * c)
+        B.diagonal().add_(a)  # one fp32 add, on the diagonal only
+        B = rnd(B)
         BX = B @ X
-        if first:
-            X = rnd(_fma32(f32(a * float(inv_den)), X, BX * float(inv_den)))
-        else:
-            X = rnd(_fma32(a, X, BX))
+        X = rnd(BX * float(inv_den) if first else BX)
     if steps == 0:
         X = rnd(X / float(den))
     return X.T if transpose else X

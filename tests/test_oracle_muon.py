@@ -108,8 +108,13 @@ def _mul(a, b):
     return float(_f32_rne(Fraction(float(a)) * Fraction(float(b))))
 
 
+def _add(a, b):
+    return float(_f32_rne(Fraction(float(a)) + Fraction(float(b))))
+
+
 def scalar_recurrence(d, steps=5, coeffs=(3.4445, -4.775, 2.0315)):
-    """Each diagonal entry through the quintic with the GPU chain's roundings."""
+    """Each diagonal entry through the quintic with the GPU chain's roundings
+    (B' = bf16(fma(b, A, c A^2) + a), x' = bf16(B' x), the first iteration scaled by 1/den)."""
     a, b, c = (R.f32(v) for v in coeffs)
     den = float(np.float32(math.sqrt(math.fsum(float(v) ** 2 for v in d))) + np.float32(1e-7))
     inv_den = float(np.float32(1) / np.float32(den))
@@ -119,11 +124,8 @@ def scalar_recurrence(d, steps=5, coeffs=(3.4445, -4.775, 2.0315)):
         out = []
         for x in xs:
             A = _bf16(_mul(x * x, inv_den2) if it == 0 else x * x)  # x * x: exact in fp32
-            B = _bf16(_fma(b, A, _mul(A * A, c)))
-            if it == 0:
-                x = _bf16(_fma(_mul(a, inv_den), x, _mul(B * x, inv_den)))
-            else:
-                x = _bf16(_fma(a, x, B * x))
+            B = _bf16(_add(_fma(b, A, _mul(A * A, c)), a))           # B' = B + a on the diagonal
+            x = _bf16(_mul(B * x, inv_den) if it == 0 else B * x)   # B * x: exact in fp32
             out.append(x)
         xs = out
     return xs
