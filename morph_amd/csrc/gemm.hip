@@ -45,24 +45,18 @@
 // transposed into the mirror position, halving the work of those products.
 //
 // Epilogue.  Each lane combines alpha * acc + beta * D in fp32 and rounds once
-// to bf16 (packed converter, round to nearest even).  D and C pass through a
-// row-major LDS copy of the tile for coalesced 16-byte rows.  The MFMAs take
-// the Q fragment as their first operand, so four consecutive accumulator
-// registers of a lane are four consecutive columns of one row of C: D comes in
-// and C goes out of the LDS tile with one 64-bit access per four values.  Ct
-// and the mirror tile of a symmetric product are read out of the same LDS tile
-// with transposing reads (ds_read_b64_tr_b16).  Loads are issued in batches
-// ahead of their use so the epilogue pays memory latency a few times, not per
-// element.  (Measured per 256 x 256 tile at K = 3072: the previous layout, one
-// column per register group and 2-byte LDS accesses, spent 5.6k cycles where
-// this one spends 2.6k; the X' product runs 3% faster.)
+// to bf16 (packed converter, round to nearest even).  D and C pass through an
+// LDS copy of the tile for coalesced 16-byte rows.  In the MFMA output layout
+// four consecutive registers of a lane are four consecutive rows of one
+// column, i.e. 8 contiguous bytes of a row of the transposed tile: Ct and the
+// mirror tile of a symmetric product are written into the same LDS with one
+// 64-bit write per four values, then leave as coalesced rows too.  Loads are
+// issued in batches ahead of their use so the epilogue pays memory latency a
+// few times, not per element.
 //
 // MFMA 32x32x16 lane layout (checked on the device): lane l holds
 // A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32] for i < 8; output
-// register r of lane l is D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].  Both
-// operand fragments have this shape (a row of 8 consecutive k), so with A = the
-// Q fragment and B = the P fragment, D is the transposed block: register r of
-// lane l holds C[l % 32][8 (r / 4) + 4 (l / 32) + r % 4].
+// register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
 //
 // Dimensions must be multiples of the tile (M, N of 256, K of 64): callers pad
 // with zeros, which is exact for Newton-Schulz (zero rows stay zero).
@@ -165,49 +159,6 @@ __device__ __forceinline__ void store_tile(const uint16_t* E, uint16_t* dst, uin
 // element (wr + 32 i + 8 (r / 4) + 4 fh + r % 4, wc + 32 j + fr).  The D mode
 // and the alpha multiply are template parameters so that each variant is
 // straight-line code.
-// T rows (the transposed tile: Ct or the mirror of a symmetric product) from the
-// row-major LDS tile E.  ds_read_b64_tr_b16 lets the 16 lanes of a group read a
-// 4 x 16 block of E (source lane j: row rb + j / 4, columns c0 + 4 (j % 4) .. + 3)
-// and hands lane j the four rows of column c0 + j: four consecutive elements of
-// T row c0 + j.  Two reads give a lane 16 bytes of a T row; the four groups of a
-// wave take adjacent 8-row chunks of the same 16 T rows (64 bytes per row).
-__device__ __forceinline__ void store_tile_t(const uint16_t* E, uint16_t* dst, uint32_t ld) {
-  typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int grp = lane >> 4, j = lane & 15;
-  auto tr = [](const uint16_t* at) {
-    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (lds_bf16x4*)(__attribute__((address_space(3))) uint16_t*)at));
-  };
-  constexpr int kBatch = 8;
-#pragma unroll
-  for (int b = 0; b < 32; b += kBatch) {
-    u32x2 lo[kBatch], hi[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int item = wave * 32 + b + k;  // 128 items: 16 blocks of 16 T rows x 8 groups of 32 C rows
-      const int c0 = (item >> 3) * 16, rb = (item & 7) * 32 + grp * 8;
-      const uint16_t* at = E + (rb + (j >> 2)) * LDE + c0 + 4 * (j & 3);
-      lo[k] = tr(at);
-      hi[k] = tr(at + 4 * LDE);
-    }
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int item = wave * 32 + b + k;
-      const int c0 = (item >> 3) * 16, rb = (item & 7) * 32 + grp * 8;
-      *reinterpret_cast<u32x4*>(dst + (uint32_t)(c0 + j) * ld + rb) =
-          u32x4{lo[k].x, lo[k].y, hi[k].x, hi[k].y};
-    }
-  }
-}
-
-// Epilogue of one tile.  The MFMAs take the Q fragment as their first operand and
-// the P fragment as their second, so acc[i][j][r] of lane (fh, fr) of wave (wr, wc)
-// is tile element (wr + 32 i + fr, wc + 32 j + 8 (r / 4) + 4 fh + r % 4): each
-// group of four registers is four consecutive columns of one row, 8 bytes of the
-// row-major LDS tile.  The D mode and the alpha multiply are template parameters
-// so that each variant is straight-line code.
 template <int kDMode, bool kScaled, bool kDiag>
 __device__ __forceinline__ void epilogue(const GemmArgs& g, float alpha, float beta,
                                          f32x16 (&acc)[4][4], uint16_t* smem, const uint16_t* D,
@@ -234,38 +185,24 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, float alpha, float b
     }
     __syncthreads();
   }
-  // Per element: (alpha *) acc, fma with beta * D, one RNE rounding to bf16 by the
-  // packed converter; four consecutive columns leave with one 64-bit LDS write, over
-  // the same 8 bytes this lane read D from.
+  // Per element: (alpha *) acc, fma with beta * D, one RNE rounding to bf16 by
+  // the packed converter (two rows per instruction).  The FP32 result goes
+  // back into acc (accumulation registers, free by now) so the transposed pass
+  // can round it again to the same bits without holding 128 packed words.
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    // the 16 D reads of this row of blocks in one LDS round trip (each block's
-    // results then overwrite exactly the 8-byte groups this lane read)
-    u32x2 draw[4][4];
-    if (kDMode == kDRowMajor) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          draw[j][q] = *reinterpret_cast<const u32x2*>(E + (wr + i * 32 + fr) * LDE + wc + j * 32 +
-                                                       fh * 4 + 8 * q);
-      __builtin_amdgcn_sched_barrier(0);
-    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int row = wr + i * 32 + fr;
-      const int cbase = wc + j * 32 + fh * 4;
-      uint16_t* at = E + row * LDE + cbase;
+      const int col = wc + j * 32 + fr;
+      const int rbase = wr + i * 32 + fh * 4;
       float dval[16];
       if (kDMode == kDRowMajor) {
+        // all 16 reads of the block before its arithmetic and writes: one LDS round
+        // trip (the barrier keeps the scheduler from splitting them into short batches)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const u32x2 v = draw[j][q];
-          dval[4 * q] = bf16_bits_to_float(v.x & 0xFFFFu);
-          dval[4 * q + 1] = bf16_bits_to_float(v.x >> 16);
-          dval[4 * q + 2] = bf16_bits_to_float(v.y & 0xFFFFu);
-          dval[4 * q + 3] = bf16_bits_to_float(v.y >> 16);
-        }
+        for (int r = 0; r < 16; ++r)
+          dval[r] = bf16_bits_to_float(E[(rbase + (r >> 2) * 8 + (r & 3)) * LDE + col]);
+        __builtin_amdgcn_sched_barrier(0);
       }
       float x[16];
 #pragma unroll
@@ -278,18 +215,45 @@ __device__ __forceinline__ void epilogue(const GemmArgs& g, float alpha, float b
         if (i == j && wr == wc) {
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (cbase + (r >> 2) * 8 + (r & 3) == row) x[r] = x[r] + g.diag;
+            if (rbase + (r >> 2) * 8 + (r & 3) == col) x[r] = x[r] + g.diag;
         }
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<u32x2*>(at + 8 * q) =
-            u32x2{pack_bf16x2(x[4 * q], x[4 * q + 1]), pack_bf16x2(x[4 * q + 2], x[4 * q + 3])};
+      for (int k = 0; k < 8; ++k) {
+        // w: rows row and row + 1 of column col
+        const uint32_t w = pack_bf16x2(x[2 * k], x[2 * k + 1]);
+        const int row = rbase + (k >> 1) * 8 + (k & 1) * 2;
+        E[row * LDE + col] = (uint16_t)w;
+        E[(row + 1) * LDE + col] = (uint16_t)(w >> 16);
+      }
+      if (kDMode != kNoD || kScaled || kDiag) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = x[r];
+      }
     }
   }
   __syncthreads();
   store_tile(E, C, (uint32_t)g.ldc);  // C rows from the LDS tile
-  if (T) store_tile_t(E, T, (uint32_t)ldt);  // T rows: transposing reads of the same tile
+  if (T) {
+    // Transposed copy (Ct, or the mirror tile): ET[c][r] = tile[r][c] in the
+    // same LDS.  Four consecutive rows of one column are 8 contiguous bytes of
+    // an ET row, so every two packed pairs go out with one 64-bit LDS write;
+    // then ET's rows leave as coalesced 16-byte stores like C's.
+    __syncthreads();  // every lane has read its C rows out of E
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x2 v;
+          v.x = pack_bf16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+          v.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          *reinterpret_cast<u32x2*>(E + (wc + j * 32 + fr) * LDE + wr + i * 32 + fh * 4 + q * 8) = v;
+        }
+    __syncthreads();
+    store_tile(E, T, (uint32_t)ldt);
+  }
 }
 
 // kQKN: Q is stored [K, N] (row-major, N contiguous) instead of [N, K]; its
@@ -307,6 +271,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
   int tr, tc;
   tile_of(g, (int)(logical - b * g.tiles_per_matrix), tr, tc);
   const int64_t row0 = (int64_t)tr * BM, col0 = (int64_t)tc * BN;
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
@@ -411,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
   };
   auto mfma = [&](int n, const Frags& f) {
     const int i = n >> 2, j = n & 3;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.q[j], f.a[i], acc[i][j], 0, 0, 0);
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.q[j], acc[i][j], 0, 0, 0);
   };
   // [K, N] operand: half h (k 4h .. 4h + 3 of this lane's 8) of the Q
   // fragment of columns n0 .. n0 + 31 at depth kk.  In each 16-lane group
