@@ -134,6 +134,17 @@ def ns_flops(rows, cols, count, steps=NS_STEPS):
     return count * steps * (4 * m * m * n + 2 * m ** 3)
 
 
+def ns_executed_flops(rows, cols, count, steps=NS_STEPS):
+    """FLOPs the MFMAs execute: the symmetric products (A = X X^T, B' = c A A + b A + a I)
+    compute only the upper triangle of their 256 x 256 tiles, X' = B' X all of them; the
+    operands are zero-padded to tile multiples (Mp, Np)."""
+    m, n = min(rows, cols), max(rows, cols)
+    mp, np_ = -(-m // 256) * 256, -(-n // 256) * 256
+    t, tn = mp // 256, np_ // 256
+    macs = t * (t + 1) // 2 * 256 * 256 * (np_ + mp) + t * tn * 256 * 256 * mp
+    return 2 * count * steps * macs
+
+
 def _prepare(mats, rows, cols, hp, orth_only, stream, workspaces, found_inf=None, first=0):
     """Enqueue prepare for up to 64 matrices per batch; returns the batches for _complete.
 
@@ -164,7 +175,8 @@ def _prepare(mats, rows, cols, hp, orth_only, stream, workspaces, found_inf=None
 def _complete(batches, stream, timer=None):
     """Newton-Schulz chain and finish for the batches _prepare enqueued.
 
-    timer: optional list; (start_event, end_event, flops) around each NS chain.
+    timer: optional list; (start_event, end_event, dense flops, executed flops) around
+    each NS chain.
     """
     L = lib()
     sh = stream_handle(stream)
@@ -177,7 +189,8 @@ def _complete(batches, stream, timer=None):
         check(L.morph_muon_newton_schulz(count, rows, cols, ctypes.byref(hp), wsp, wsn, sh))
         if timer is not None:
             e1.record(s)
-            timer.append((e0, e1, ns_flops(rows, cols, count, hp.ns_steps)))
+            timer.append((e0, e1, ns_flops(rows, cols, count, hp.ns_steps),
+                          ns_executed_flops(rows, cols, count, hp.ns_steps)))
         check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), int(orth_only), wsp,
                                   wsn, sh))
 
