@@ -45,16 +45,34 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kMaxMats = 64;
-constexpr int kElemsPerBlock = kBlock * 4;   // one 128-bit access per lane (many short blocks stream best)
-constexpr int kTile = 64;                       // transpose tile
+// Workgroup shapes of the elementwise passes (HBM-bound; measured round-robin on
+// the 42-matrix [3072, 6144] batch, bit-identical results throughout):
+//   momentum_kernel: 256 lanes, one 128-bit access each (128 lanes: 6% slower);
+//   apply_flat_kernel: 64 lanes, one 128-bit access each (128: 2%, 256: 6% slower);
+//   transpose tiles of 64 stored rows x 128 stored columns: 512-byte row segments
+//   of the FP32 streams, 128-byte segments of X (64 x 64 tiles: 7% slower);
+//   momentum_t_kernel at 3 workgroups per CU and apply_t_kernel at 6, by a dynamic
+//   LDS reservation beside the static tile (uncapped: 7% and 4% slower; 2 per CU
+//   for momentum_t_kernel or 3 for apply_t_kernel: 5% slower).
+constexpr int kFlat = 256;
+constexpr int kFlatApply = 64;
+constexpr int kElemsPerBlock = kFlat * 4;
+constexpr int kTR = 64;   // stored rows per transpose tile
+constexpr int kTC = 128;  // stored columns per transpose tile
+constexpr size_t kMomentumTReserve = 24 * 1024;  // + 16.5 KiB tile: 3 workgroups per CU
+constexpr size_t kApplyTReserve = 6 * 1024;      // + 17 KiB tile: 6 workgroups per CU
 constexpr int64_t kRowPad = 64;                 // bf16 elements appended to every X/A/B row
 
+// The matrices one launch covers, by slot (blockIdx.y of the elementwise passes):
+// a pass over one orientation lists only that orientation's matrices, so no
+// workgroup is launched for another's.
 struct MatPtrs {
   const float* grad[kMaxMats];
   const float* mom[kMaxMats];
   float* mom_out[kMaxMats];  // the updated momentum (== mom when updated in place)
   float* param[kMaxMats];
   int32_t transposed[kMaxMats];  // stored [cols, rows] instead of [rows, cols]
+  int32_t index[kMaxMats];       // position in the batch: its X and partial sums
 };
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -62,7 +80,7 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 struct Layout {
   int64_t rows, cols, m, n, mp, np, count, numel;
   int64_t blocks;  // flat blocks per matrix (momentum_kernel)
-  int64_t tiles;   // 64 x 64 tiles per matrix (momentum_t_kernel, apply_kernel)
+  int64_t tiles;   // transpose tiles per matrix (momentum_t_kernel, apply_t_kernel)
   int64_t parts;   // partial sums per matrix: max(blocks, tiles)
   int64_t ldn, ldm;  // row lengths of X ([Mp][ldn]) and of A, B ([Mp][ldm])
   size_t off_part, off_scale, off_x0, off_x1, off_a, off_b, total;
@@ -81,7 +99,8 @@ Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
   L.ldm = L.mp + kRowPad;
   L.numel = rows * cols;
   L.blocks = (L.numel + kElemsPerBlock - 1) / kElemsPerBlock;
-  L.tiles = ((rows + kTile - 1) / kTile) * ((cols + kTile - 1) / kTile);
+  // tiles of a matrix stored with its long side as rows (the ones X transposes)
+  L.tiles = ((L.n + kTR - 1) / kTR) * ((L.m + kTC - 1) / kTC);
   L.parts = L.blocks > L.tiles ? L.blocks : L.tiles;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -99,6 +118,7 @@ Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
   return L;
 }
 
+template <int kLanes = kBlock>
 __device__ __forceinline__ double block_sum(double x, double* lds) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
@@ -107,7 +127,7 @@ __device__ __forceinline__ double block_sum(double x, double* lds) {
   __syncthreads();
   double s = 0.0;
   if (threadIdx.x == 0)
-    for (int w = 0; w < kBlock / 64; ++w) s += lds[w];
+    for (int w = 0; w < kLanes / 64; ++w) s += lds[w];
   return s;  // valid in thread 0
 }
 
@@ -149,18 +169,17 @@ __device__ __forceinline__ void flag_nonfinite(uint32_t* found_inf, bool bad) {
 // are 16-byte aligned, else one element per access.  Gradient and momentum
 // are touched once here, so their accesses are non-temporal.
 template <bool kMomentum>
-__global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, uint16_t* x_all,
+__global__ __launch_bounds__(kFlat) void momentum_kernel(MatPtrs mats, uint16_t* x_all,
                                                           double* part_all, int64_t rows,
                                                           int64_t cols, int64_t mp, int64_t ldn,
                                                           int64_t parts, float mom_w,
                                                           float nest_w, uint32_t* found_inf) {
-  __shared__ double lds[kBlock / 64];
-  const int mat = blockIdx.y;
-  if (!x_is_stored(mats, mat, rows, cols)) return;  // block-uniform: momentum_t_kernel's matrix
-  const int64_t pc = mats.transposed[mat] ? rows : cols, numel = rows * cols;
-  const float* g = mats.grad[mat];
-  const float* mom = mats.mom[mat];
-  float* mom_out = mats.mom_out[mat];
+  __shared__ double lds[kFlat / 64];
+  const int slot = blockIdx.y, mat = mats.index[slot];
+  const int64_t pc = mats.transposed[slot] ? rows : cols, numel = rows * cols;
+  const float* g = mats.grad[slot];
+  const float* mom = mats.mom[slot];
+  float* mom_out = mats.mom_out[slot];
   uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
   const int64_t base = (int64_t)blockIdx.x * kElemsPerBlock;
   const bool large_m = mom_w >= 0.5f, large_n = nest_w >= 0.5f;
@@ -173,8 +192,8 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, uint16_t
   bool bad = false;
   if (vec) {
 #pragma unroll
-    for (int k = 0; k < kElemsPerBlock / (4 * kBlock); ++k) {
-      const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
+    for (int k = 0; k < kElemsPerBlock / (4 * kFlat); ++k) {
+      const int64_t i = base + ((int64_t)k * kFlat + threadIdx.x) * 4;
       const f32x4 gv = load_stream<true>(reinterpret_cast<const f32x4*>(g + i));
       const u32x4 gb = __builtin_bit_cast(u32x4, gv);
       bad |= nonfinite_f32_bits(gb.x) | nonfinite_f32_bits(gb.y) | nonfinite_f32_bits(gb.z) |
@@ -195,7 +214,7 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, uint16_t
       *reinterpret_cast<u32x2*>(xm + r * ldn + c) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     }
   } else {
-    for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kBlock) {
+    for (int64_t i = base + threadIdx.x; i < base + kElemsPerBlock && i < numel; i += kFlat) {
       float m = kMomentum ? mom[i] : 0.f, ui;
       bad |= nonfinite_f32_bits(__builtin_bit_cast(uint32_t, g[i]));
       momentum_one<kMomentum>(g[i], m, ui, mom_w, nest_w, large_m, large_n);
@@ -206,35 +225,36 @@ __global__ __launch_bounds__(kBlock) void momentum_kernel(MatPtrs mats, uint16_t
     }
   }
   flag_nonfinite(found_inf, bad);
-  const double s = block_sum(ss, lds);
+  const double s = block_sum<kFlat>(ss, lds);
   if (threadIdx.x == 0) part_all[(int64_t)mat * parts + blockIdx.x] = s;
 }
 
-// Tile geometry shared by momentum_t_kernel and apply_kernel.  One 64 x 64
-// tile of the stored layout per block; the grid covers [rows, cols] in
-// 64-tiles and a transposed matrix reads block (x, y) as its tile (y, x).
-// `vec`: a whole tile with rows a multiple of 4, moved 4 consecutive elements
-// per lane access.
+// Tile geometry shared by momentum_t_kernel and apply_t_kernel: tile blockIdx.x
+// of the stored layout [pr, pc] (kTR x kTC, row-major over tiles), for the
+// matrices whose X is its transpose.  `vec`: a whole tile with dimensions a
+// multiple of 4, moved 4 consecutive elements per lane access.
 struct TileGeo {
-  int64_t pr, pc, r0, c0;
-  bool same_is_x, vec;
+  int64_t pr, pc, r0, c0, tiles_c, tile;
+  bool valid, vec;
 };
 
-__device__ __forceinline__ TileGeo tile_geo(const MatPtrs& mats, int mat, int64_t rows,
+__device__ __forceinline__ TileGeo tile_geo(const MatPtrs& mats, int slot, int64_t rows,
                                             int64_t cols) {
   TileGeo t;
-  const bool tr = mats.transposed[mat] != 0;
+  const bool tr = mats.transposed[slot] != 0;
   t.pr = tr ? cols : rows;
   t.pc = tr ? rows : cols;
-  t.same_is_x = t.pr <= t.pc;
-  t.r0 = (int64_t)(tr ? blockIdx.x : blockIdx.y) * kTile;
-  t.c0 = (int64_t)(tr ? blockIdx.y : blockIdx.x) * kTile;
-  t.vec = (t.pc & 3) == 0 && (t.pr & 3) == 0 && t.r0 + kTile <= t.pr && t.c0 + kTile <= t.pc;
+  t.tiles_c = (t.pc + kTC - 1) / kTC;
+  t.tile = blockIdx.x;
+  t.r0 = (t.tile / t.tiles_c) * kTR;
+  t.c0 = (t.tile % t.tiles_c) * kTC;
+  t.valid = t.r0 < t.pr;
+  t.vec = (t.pc & 3) == 0 && (t.pr & 3) == 0 && t.r0 + kTR <= t.pr && t.c0 + kTC <= t.pc;
   return t;
 }
 
 // Matrices whose X is the transpose of the stored layout: the momentum pass
-// per 64 x 64 tile, bf16(u) transposed through LDS so that both the stored
+// per kTR x kTC tile, bf16(u) transposed through LDS so that both the stored
 // reads and the X writes are coalesced.  One partial sum per tile, indexed by
 // the tile's place in the stored layout (row-major over tiles), so a matrix
 // sums in the same order whichever way the batch describes it.
@@ -244,14 +264,14 @@ __global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16
                                                             int64_t cols, int64_t mp, int64_t ldn,
                                                             int64_t parts, float mom_w,
                                                             float nest_w, uint32_t* found_inf) {
-  __shared__ __attribute__((aligned(8))) uint16_t tile[kTile][kTile + 4];
+  __shared__ __attribute__((aligned(8))) uint16_t tile[kTR][kTC + 4];
   __shared__ double lds[kBlock / 64];
-  const int mat = blockIdx.z;
-  const TileGeo t = tile_geo(mats, mat, rows, cols);
-  if (t.same_is_x) return;  // block-uniform: momentum_kernel's matrix
-  const float* g = mats.grad[mat];
-  const float* mom = mats.mom[mat];
-  float* mom_out = mats.mom_out[mat];
+  const int slot = blockIdx.y, mat = mats.index[slot];
+  const TileGeo t = tile_geo(mats, slot, rows, cols);
+  if (!t.valid) return;  // block-uniform
+  const float* g = mats.grad[slot];
+  const float* mom = mats.mom[slot];
+  float* mom_out = mats.mom_out[slot];
   uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
   const bool large_m = mom_w >= 0.5f, large_n = nest_w >= 0.5f;
   const uintptr_t addr = reinterpret_cast<uintptr_t>(g) |
@@ -259,10 +279,13 @@ __global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16
                                           reinterpret_cast<uintptr_t>(mom_out)
                                     : 0);
   const bool vec = t.vec && (addr & 15) == 0;
-  const int q = threadIdx.x & 15, w = threadIdx.x >> 4;  // 4-element group, row of a pass
+  constexpr int kLPR = kTC / 4, kRPP = kBlock / kLPR;  // stored rows: lanes per row, rows per pass
+  const int q = threadIdx.x % kLPR, w = threadIdx.x / kLPR;
   double ss = 0.0;
   bool bad = false;
-  for (int rr = w; rr < kTile; rr += kBlock / 16) {
+#pragma unroll
+  for (int pass = 0; pass < kTR / kRPP; ++pass) {
+    const int rr = w + pass * kRPP;
     const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
     uint32_t h[4] = {0, 0, 0, 0};
     if (vec) {
@@ -300,11 +323,15 @@ __global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16
   }
   flag_nonfinite(found_inf, bad);
   __syncthreads();
-  for (int cc = w; cc < kTile; cc += kBlock / 16) {
-    const int64_t c = t.c0 + cc, r = t.r0 + 4 * q;  // X row c, columns r .. r + 3
+  constexpr int kXL = kTR / 4, kXRP = kBlock / kXL;  // X rows: lanes per row, rows per pass
+  const int q2 = threadIdx.x % kXL, w2 = threadIdx.x / kXL;
+#pragma unroll
+  for (int pass = 0; pass < kTC / kXRP; ++pass) {
+    const int cc = w2 + pass * kXRP;
+    const int64_t c = t.c0 + cc, r = t.r0 + 4 * q2;  // X row c, columns r .. r + 3
     uint32_t h[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) h[e] = tile[4 * q + e][cc];
+    for (int e = 0; e < 4; ++e) h[e] = tile[4 * q2 + e][cc];
     if (t.vec) {
       *reinterpret_cast<u32x2*>(xm + c * ldn + r) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     } else {
@@ -314,8 +341,7 @@ __global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16
     }
   }
   const double s = block_sum(ss, lds);
-  if (threadIdx.x == 0)
-    part_all[(int64_t)mat * parts + (t.r0 / kTile) * ((t.pc + kTile - 1) / kTile) + t.c0 / kTile] = s;
+  if (threadIdx.x == 0) part_all[(int64_t)mat * parts + t.tile] = s;
 }
 
 // den = fp32(sqrt(sum)) + fp32(1e-7): x / (x.norm() + 1e-7) of optimizer.py:18.
@@ -353,8 +379,7 @@ __global__ __launch_bounds__(kBlock) void rescale_kernel(uint16_t* x_all, const 
 
 // p = p * decay + (U * scale) * neg_lr with U = X in p's layout; scale is
 // scale_t for a transposed matrix.  kExtract: p = U instead (orthogonalize
-// alone returns the fp32 value of U).  Same tiles as momentum_t_kernel: when X is
-// the transpose of p's layout the tile of X is staged through LDS first.
+// alone returns the fp32 value of U).
 template <bool kExtract>
 __device__ __forceinline__ float apply_one(float p, uint32_t u16, float scale, float decay,
                                            float neg_lr) {
@@ -366,59 +391,102 @@ __device__ __forceinline__ float apply_one(float p, uint32_t u16, float scale, f
   }
 }
 
+// Matrices whose X has the stored layout: a flat pass, kFlatApply * 4 consecutive
+// elements of p per block (rows of X read at their padded stride).
 template <bool kExtract>
-__global__ __launch_bounds__(kBlock) void apply_kernel(MatPtrs mats, const uint16_t* x_all,
-                                                       int64_t rows, int64_t cols, int64_t mp,
-                                                       int64_t ldn, float scale_n, float scale_t,
-                                                       float decay, float neg_lr) {
-  __shared__ __attribute__((aligned(8))) uint16_t tile[kTile][kTile + 4];
-  const int mat = blockIdx.z;
-  const TileGeo t = tile_geo(mats, mat, rows, cols);
-  float* p = mats.param[mat];
-  const float scale = mats.transposed[mat] ? scale_t : scale_n;
+__global__ __launch_bounds__(kFlatApply) void apply_flat_kernel(MatPtrs mats,
+                                                                const uint16_t* x_all,
+                                                                int64_t rows, int64_t cols,
+                                                                int64_t mp, int64_t ldn,
+                                                                float scale_n, float scale_t,
+                                                                float decay, float neg_lr) {
+  const int slot = blockIdx.y, mat = mats.index[slot];
+  const int64_t pc = mats.transposed[slot] ? rows : cols, numel = rows * cols;
+  float* p = mats.param[slot];
+  const float scale = mats.transposed[slot] ? scale_t : scale_n;
+  const uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
+  const int64_t base = (int64_t)blockIdx.x * kFlatApply * 4;
+  const bool vec = (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (pc & 3) == 0 &&
+                   base + kFlatApply * 4 <= numel;
+  if (vec) {
+    const int64_t i = base + (int64_t)threadIdx.x * 4;
+    const int64_t r = i / pc, c = i - r * pc;
+    const u32x2 v = *reinterpret_cast<const u32x2*>(xm + r * ldn + c);
+    const uint32_t h[4] = {v.x & 0xFFFFu, v.x >> 16, v.y & 0xFFFFu, v.y >> 16};
+    f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (!kExtract) pv = load_stream<true>(reinterpret_cast<const f32x4*>(p + i));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pv[e] = apply_one<kExtract>(pv[e], h[e], scale, decay, neg_lr);
+    store_stream<true>(reinterpret_cast<f32x4*>(p + i), pv);
+  } else {
+    for (int64_t i = base + threadIdx.x; i < base + kFlatApply * 4 && i < numel;
+         i += kFlatApply) {
+      const int64_t r = i / pc, c = i - r * pc;
+      p[i] = apply_one<kExtract>(kExtract ? 0.f : p[i], xm[r * ldn + c], scale, decay, neg_lr);
+    }
+  }
+}
+
+// Matrices whose X is the transpose of the stored layout: per kTR x kTC tile of p,
+// the X tile is staged through LDS so that the X reads and the p accesses are both
+// coalesced rows.
+template <bool kExtract>
+__global__ __launch_bounds__(kBlock) void apply_t_kernel(MatPtrs mats, const uint16_t* x_all,
+                                                         int64_t rows, int64_t cols, int64_t mp,
+                                                         int64_t ldn, float scale_n, float scale_t,
+                                                         float decay, float neg_lr) {
+  __shared__ __attribute__((aligned(8))) uint16_t tile[kTC][kTR + 4];
+  const int slot = blockIdx.y, mat = mats.index[slot];
+  const TileGeo t = tile_geo(mats, slot, rows, cols);
+  if (!t.valid) return;  // block-uniform
+  float* p = mats.param[slot];
+  const float scale = mats.transposed[slot] ? scale_t : scale_n;
   const uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
   const bool vec = t.vec && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
-  const int q = threadIdx.x & 15, w = threadIdx.x >> 4;
-  if (!t.same_is_x) {
-    // tile[c - c0][r - r0] = X[c][r]: X rows c0 .. c0 + 63, columns r0 .. r0 + 63
-    for (int cc = w; cc < kTile; cc += kBlock / 16) {
-      const int64_t c = t.c0 + cc, r = t.r0 + 4 * q;
-      u32x2 v = u32x2{0, 0};
-      if (t.vec) {
-        v = *reinterpret_cast<const u32x2*>(xm + c * ldn + r);
-      } else {
-        uint32_t h[4] = {0, 0, 0, 0};
+  constexpr int kLPR = kTC / 4, kRPP = kBlock / kLPR;  // stored rows: lanes per row, rows per pass
+  const int q = threadIdx.x % kLPR, w = threadIdx.x / kLPR;
+  // the p rows go out first: they do not wait for the X tile
+  f32x4 pv[kTR / kRPP];
+  if (vec && !kExtract) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (c < t.pc && r + e < t.pr) h[e] = xm[c * ldn + r + e];
-        v = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-      }
-      *reinterpret_cast<u32x2*>(&tile[cc][4 * q]) = v;
-    }
-    __syncthreads();
+    for (int pass = 0; pass < kTR / kRPP; ++pass)
+      pv[pass] = load_stream<true>(
+          reinterpret_cast<const f32x4*>(p + (t.r0 + w + pass * kRPP) * t.pc + t.c0 + 4 * q));
   }
-  for (int rr = w; rr < kTile; rr += kBlock / 16) {
+  // tile[c - c0][r - r0] = X[c][r]: X rows c0 .. c0 + kTC - 1, columns r0 .. r0 + kTR - 1
+  constexpr int kXL = kTR / 4, kXRP = kBlock / kXL;
+  const int q2 = threadIdx.x % kXL, w2 = threadIdx.x / kXL;
+#pragma unroll
+  for (int pass = 0; pass < kTC / kXRP; ++pass) {
+    const int cc = w2 + pass * kXRP;
+    const int64_t c = t.c0 + cc, r = t.r0 + 4 * q2;
+    u32x2 v = u32x2{0, 0};
+    if (t.vec) {
+      v = *reinterpret_cast<const u32x2*>(xm + c * ldn + r);
+    } else {
+      uint32_t h[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c < t.pc && r + e < t.pr) h[e] = xm[c * ldn + r + e];
+      v = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    }
+    *reinterpret_cast<u32x2*>(&tile[cc][4 * q2]) = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int pass = 0; pass < kTR / kRPP; ++pass) {
+    const int rr = w + pass * kRPP;
     const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
     uint32_t h[4];
-    if (t.same_is_x) {
-      if (t.vec) {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(xm + r * ldn + c);
-        h[0] = v.x & 0xFFFFu, h[1] = v.x >> 16, h[2] = v.y & 0xFFFFu, h[3] = v.y >> 16;
-      } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = (r < t.pr && c + e < t.pc) ? xm[r * ldn + c + e] : 0u;
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) h[e] = tile[4 * q + e][rr];
-    }
+    for (int e = 0; e < 4; ++e) h[e] = tile[4 * q + e][rr];
     float* pr_ = p + r * t.pc + c;
     if (vec) {
-      f32x4 pv = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (!kExtract) pv = load_stream<true>(reinterpret_cast<const f32x4*>(pr_));
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (!kExtract) v = pv[pass];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pv[e] = apply_one<kExtract>(pv[e], h[e], scale, decay, neg_lr);
-      store_stream<true>(reinterpret_cast<f32x4*>(pr_), pv);
+      for (int e = 0; e < 4; ++e) v[e] = apply_one<kExtract>(v[e], h[e], scale, decay, neg_lr);
+      store_stream<true>(reinterpret_cast<f32x4*>(pr_), v);
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -468,7 +536,9 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   const Layout L = make_layout(rows, cols, count > 0 ? count : 1);
   if (workspace == nullptr || workspace_bytes < L.total) return MORPH_EWORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return MORPH_EINVAL;
-  if ((rows + kTile - 1) / kTile > 65535) return MORPH_ERANGE;  // grid y of scale/apply
+  // grid x of the tile passes and of apply_flat_kernel (the most blocks of the flat passes)
+  if (L.tiles > INT32_MAX || (L.numel + kFlatApply * 4 - 1) / (kFlatApply * 4) > INT32_MAX)
+    return MORPH_ERANGE;
   char* ws = static_cast<char*>(workspace);
   out->L = L;
   out->part = reinterpret_cast<double*>(ws + L.off_part);
@@ -480,21 +550,34 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   return MORPH_OK;
 }
 
-// 64 x 64 tiles of [rows, cols] per matrix (momentum_t_kernel, apply_kernel).
-dim3 tile_grid(int64_t rows, int64_t cols, int count) {
-  return dim3((unsigned)((cols + kTile - 1) / kTile), (unsigned)((rows + kTile - 1) / kTile),
-              (unsigned)count);
+// The transpose tiles of `count` matrices (momentum_t_kernel, apply_t_kernel).
+dim3 tile_grid(const Layout& L, int count) { return dim3((unsigned)L.tiles, (unsigned)count); }
+
+// X0 has the stored layout of a matrix when its stored rows are the shorter side.
+bool stored_is_x(const morph_muon_matrix& m, int64_t rows, int64_t cols) {
+  const bool tr = m.transposed != 0;
+  return (tr ? cols : rows) <= (tr ? rows : cols);
 }
 
-MatPtrs pointers(const morph_muon_matrix* mats, int count) {
+enum class Orient { kAll, kStored, kTransposed };
+
+// The batch's matrices of one orientation (kAll: every one), in batch order; *n = how many.
+MatPtrs pointers(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+                 Orient which, int* n) {
   MatPtrs m;
+  int k = 0;
   for (int i = 0; i < count; ++i) {
-    m.grad[i] = mats[i].grad;
-    m.mom[i] = mats[i].momentum;
-    m.mom_out[i] = mats[i].momentum_out != nullptr ? mats[i].momentum_out : mats[i].momentum;
-    m.param[i] = mats[i].param;
-    m.transposed[i] = mats[i].transposed;
+    if (which != Orient::kAll && stored_is_x(mats[i], rows, cols) != (which == Orient::kStored))
+      continue;
+    m.grad[k] = mats[i].grad;
+    m.mom[k] = mats[i].momentum;
+    m.mom_out[k] = mats[i].momentum_out != nullptr ? mats[i].momentum_out : mats[i].momentum;
+    m.param[k] = mats[i].param;
+    m.transposed[k] = mats[i].transposed;
+    m.index[k] = i;
+    ++k;
   }
+  *n = k;
   return m;
 }
 
@@ -506,32 +589,29 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
   if (rc || count == 0) return rc;
   const Layout& L = W.L;
   hipStream_t s = as_stream(stream);
-  const MatPtrs mp_ = pointers(mats, count);
-  // X0 has the stored layout of a matrix when its stored rows are the shorter side
-  bool flat = false, tiled = false;
-  for (int i = 0; i < count; ++i) {
-    const bool tr = mats[i].transposed != 0;
-    ((tr ? cols : rows) <= (tr ? rows : cols) ? flat : tiled) = true;
-  }
+  int n_all, n_flat, n_tiled;
+  const MatPtrs mp_ = pointers(mats, count, rows, cols, Orient::kAll, &n_all);
+  const MatPtrs flat = pointers(mats, count, rows, cols, Orient::kStored, &n_flat);
+  const MatPtrs tiled = pointers(mats, count, rows, cols, Orient::kTransposed, &n_tiled);
   const float mw = hp->momentum_weight, nw = hp->nesterov_weight;
-  if (flat) {
-    const dim3 ew((unsigned)L.blocks, count);
+  if (n_flat) {
+    const dim3 ew((unsigned)L.blocks, n_flat);
     if (orth_only)
-      hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
+      hipLaunchKernelGGL(momentum_kernel<false>, ew, dim3(kFlat), 0, s, flat, W.X[0], W.part,
                          rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
     else
-      hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
+      hipLaunchKernelGGL(momentum_kernel<true>, ew, dim3(kFlat), 0, s, flat, W.X[0], W.part,
                          rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
     if ((rc = launch_status())) return rc;
   }
-  if (tiled) {
-    const dim3 tg = tile_grid(rows, cols, count);
+  if (n_tiled) {
+    const dim3 tg = tile_grid(L, n_tiled);
     if (orth_only)
-      hipLaunchKernelGGL(momentum_t_kernel<false>, tg, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
-                         rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
+      hipLaunchKernelGGL(momentum_t_kernel<false>, tg, dim3(kBlock), kMomentumTReserve, s, tiled,
+                         W.X[0], W.part, rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
     else
-      hipLaunchKernelGGL(momentum_t_kernel<true>, tg, dim3(kBlock), 0, s, mp_, W.X[0], W.part,
-                         rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
+      hipLaunchKernelGGL(momentum_t_kernel<true>, tg, dim3(kBlock), kMomentumTReserve, s, tiled,
+                         W.X[0], W.part, rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
     if ((rc = launch_status())) return rc;
   }
   hipLaunchKernelGGL(norm_kernel, dim3(count), dim3(kBlock), 0, s, mp_, W.part, W.scale, rows,
@@ -589,18 +669,31 @@ int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   int rc = setup(mats, count, rows, cols, hp, workspace, workspace_bytes, true, false, &W);
   if (rc || count == 0) return rc;
   const Layout& L = W.L;
-  const MatPtrs mp_ = pointers(mats, count);
   const uint16_t* x = W.X[hp->ns_steps & 1];  // the buffer the last iteration wrote
   hipStream_t s = as_stream(stream);
-  const dim3 grid = tile_grid(rows, cols, count);
-  if (orth_only)
-    hipLaunchKernelGGL(apply_kernel<true>, grid, dim3(kBlock), 0, s, mp_, x, rows, cols, L.mp,
-                       L.ldn, hp->update_scale, hp->update_scale_transposed, hp->decay,
-                       hp->neg_lr);
-  else
-    hipLaunchKernelGGL(apply_kernel<false>, grid, dim3(kBlock), 0, s, mp_, x, rows, cols, L.mp,
-                       L.ldn, hp->update_scale, hp->update_scale_transposed, hp->decay,
-                       hp->neg_lr);
+  int n_flat, n_tiled;
+  const MatPtrs flat = pointers(mats, count, rows, cols, Orient::kStored, &n_flat);
+  const MatPtrs tiled = pointers(mats, count, rows, cols, Orient::kTransposed, &n_tiled);
+  const float sn = hp->update_scale, st = hp->update_scale_transposed;
+  if (n_flat) {
+    const dim3 ew((unsigned)((L.numel + kFlatApply * 4 - 1) / (kFlatApply * 4)), n_flat);
+    if (orth_only)
+      hipLaunchKernelGGL(apply_flat_kernel<true>, ew, dim3(kFlatApply), 0, s, flat, x, rows,
+                         cols, L.mp, L.ldn, sn, st, hp->decay, hp->neg_lr);
+    else
+      hipLaunchKernelGGL(apply_flat_kernel<false>, ew, dim3(kFlatApply), 0, s, flat, x, rows,
+                         cols, L.mp, L.ldn, sn, st, hp->decay, hp->neg_lr);
+    if ((rc = launch_status())) return rc;
+  }
+  if (n_tiled) {
+    const dim3 tg = tile_grid(L, n_tiled);
+    if (orth_only)
+      hipLaunchKernelGGL(apply_t_kernel<true>, tg, dim3(kBlock), kApplyTReserve, s, tiled, x,
+                         rows, cols, L.mp, L.ldn, sn, st, hp->decay, hp->neg_lr);
+    else
+      hipLaunchKernelGGL(apply_t_kernel<false>, tg, dim3(kBlock), kApplyTReserve, s, tiled, x,
+                         rows, cols, L.mp, L.ldn, sn, st, hp->decay, hp->neg_lr);
+  }
   return launch_status();
 }
 
