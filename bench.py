@@ -32,6 +32,7 @@ ROOT = Path(__file__).resolve().parent
 TRAFFIC_PROFILE = ROOT / "profiles" / "adamw_config2_traffic.json"
 TRAFFIC_PROFILE_C3 = ROOT / "profiles" / "adamw_config3_traffic.json"
 MFMA_PROFILE = ROOT / "profiles" / "muon_config5_mfma.json"
+TRAFFIC_PROFILE_MUON = ROOT / "profiles" / "muon_config5_traffic.json"
 TRAFFIC_PROFILE_GRADS = ROOT / "profiles" / "grads_config2_traffic.json"
 # rocprofv3 counters cannot run inside this process: `traffic` is read from the committed
 # summary of the FETCH_SIZE / WRITE_SIZE passes over this same workload, not measured here
@@ -307,7 +308,11 @@ def muon_main(args):
         "ns_ms_per_step": round(r["ns_s"] * 1e3, 3),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "gemm_kernel (3 launches per Newton-Schulz iteration, all 42 matrices batched)",
+                     "traffic": measured_traffic(TRAFFIC_PROFILE_MUON),
+                     "traffic_source": TRAFFIC_SOURCE % TRAFFIC_PROFILE_MUON.name
+                     + "; the mean over the three products' launches",
+                     "kernel": "gemm_kernel (3 launches per Newton-Schulz iteration, all 42 "
+                               "matrices batched)",
                      "flops_per_step": r["executed"],
                      "flops_counted": "executed by the MFMAs: the symmetric products A and B' "
                                       "compute 78 of 144 tiles per matrix",

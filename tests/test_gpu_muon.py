@@ -86,7 +86,7 @@ def test_gemm_output_rounding_is_round_to_nearest_even(alpha):
 
 
 def test_gemm_nt_in_place_output_over_D():
-    """D may alias C (the X' = a X + B X step writes over X)."""
+    """D may alias C: the epilogue reads each D element before it writes that C element."""
     P, Q = rand_bf16((256, 256), 4).to(DEV), rand_bf16((512, 256), 5).to(DEV)
     X = rand_bf16((256, 512), 6).to(DEV)
     expect = muon.gemm_nt(P, Q, X.clone(), 1.0, 3.4445)
