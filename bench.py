@@ -20,6 +20,7 @@ HIP events that those launches' dispatches stamp on the launch stream;
 reference's AdamW group runs -- on this host's cores.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -187,7 +188,35 @@ def time_gpu(steps, warmup):
         raise RuntimeError(f"{opt.skipped_steps} steps skipped on synthetic finite gradients")
     return dict(n=n, elapsed=elapsed, elapsed_plain=elapsed_plain, elapsed_checked=elapsed_checked,
                 avg_kernel_s=sum(kernel_ms) / len(kernel_ms) / 1e3, kernel_ms=kernel_ms,
-                scale=scaler.scale, applied=opt.applied_steps)
+                scale=scaler.scale, applied=opt.applied_steps,
+                copy=copy_ceiling(BYTES_PER_PARAM * n, device))
+
+
+def copy_ceiling(nbytes, device, reps=10):
+    """The HBM rate of a plain FP32 copy moving the bytes of one AdamW launch (half
+    read, half written): the library's convert kernel with FP32 output, timed by events
+    on its stream after the timed steps, median of `reps` launches."""
+    from morph_amd import _lib
+    n = nbytes // 8
+    src = torch.ones(n, device=device)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream(device)
+    times = []
+    for r in range(reps + 2):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        _lib.check(_lib.lib().morph_convert_f32(
+            ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), _lib.DTYPE_F32, n,
+            None, _lib.stream_handle(stream)))
+        e1.record(stream)
+        torch.cuda.synchronize(device)
+        if r >= 2:  # the first launches warm the code object and the buffers
+            times.append(e0.elapsed_time(e1))
+    med = sorted(times)[len(times) // 2]
+    gbs = 8 * n / med / 1e6
+    return {"achieved": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel": "convert_kernel<F32> (morph_convert_f32, FP32 -> FP32 copy)",
+            "bytes_per_launch": 8 * n, "median_launch_us": round(med * 1e3, 2), "launches": reps}
 
 
 def cpu_baseline(seconds=10.0):
@@ -1031,7 +1060,9 @@ def main():
                      "traffic_source": TRAFFIC_SOURCE % TRAFFIC_PROFILE.name,
                      "kernel": "adamw_multi_kernel<F16,F16,dev>",
                      "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
-                     "bytes_per_launch": BYTES_PER_PARAM * n},
+                     "bytes_per_launch": BYTES_PER_PARAM * n,
+                     "frac_of_copy": round(achieved / r["copy"]["achieved"], 4)},
+        "copy_ceiling": r["copy"],
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
     print(json.dumps(line), flush=True)

@@ -13,7 +13,10 @@
 // Rounding: FP16 by the hardware conversion (round to nearest even, overflow
 // to inf, as numpy and torch); BF16 by round to nearest even with NaN ->
 // 0x7FC0 (torch's c10::BFloat16).  Each lane converts 8 consecutive values
-// (two 128-bit loads, one 128-bit store for 16-bit output).
+// (two 128-bit loads, one 128-bit store for 16-bit output).  The FP32 -> FP32
+// copy instead moves 4 consecutive values per access with consecutive lanes on
+// consecutive 16 bytes (every access instruction covers whole lines) and streams
+// them non-temporally: nothing rereads a copy's source or output soon.
 #include "common.h"
 
 namespace morph {
@@ -38,7 +41,20 @@ __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict
                                                          int vector_ok, uint32_t* flag) {
   const int64_t base = (int64_t)blockIdx.x * kPerBlock;
   bool bad = false;
-  if (vector_ok && base + kPerBlock <= n) {
+  constexpr bool kCopy = std::is_same_v<OT, F32>;
+  if (kCopy && vector_ok && base + kPerBlock <= n) {
+#pragma unroll
+    for (int k = 0; k < kPerLane / 4; ++k) {
+      const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
+      const f32x4 v = load_stream<true>(reinterpret_cast<const f32x4*>(src + i));
+      if constexpr (kCheck) {
+        const u32x4 u = __builtin_bit_cast(u32x4, v);
+        bad |= nonfinite_f32_bits(u.x) | nonfinite_f32_bits(u.y) | nonfinite_f32_bits(u.z) |
+               nonfinite_f32_bits(u.w);
+      }
+      store_stream<true>(reinterpret_cast<f32x4*>(static_cast<float*>(dst) + i), v);
+    }
+  } else if (vector_ok && base + kPerBlock <= n) {
     const int64_t e = base + (int64_t)threadIdx.x * kPerLane;
     const f32x4 a = *reinterpret_cast<const f32x4*>(src + e);
     const f32x4 b = *reinterpret_cast<const f32x4*>(src + e + 4);
@@ -47,10 +63,7 @@ __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict
 #pragma unroll
       for (int k = 0; k < 8; ++k) bad |= out_of_range<OT>(x[k]);
     }
-    if constexpr (std::is_same_v<OT, F32>) {
-      *reinterpret_cast<f32x4*>(static_cast<float*>(dst) + e) = a;
-      *reinterpret_cast<f32x4*>(static_cast<float*>(dst) + e + 4) = b;
-    } else {
+    if constexpr (!kCopy) {
       u32x4 w;
       w.x = from_float<OT>(x[0]) | (from_float<OT>(x[1]) << 16);
       w.y = from_float<OT>(x[2]) | (from_float<OT>(x[3]) << 16);

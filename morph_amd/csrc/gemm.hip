@@ -8,8 +8,9 @@
 // contiguous bytes of one row.  Q is [N, K] likewise ("NT"), or [K, N] with N
 // contiguous (MORPH_GEMM_Q_KN): then its fragments come from LDS through
 // gfx950's transposing reads (ds_read_b64_tr_b16) and the product is P . Q.
-// One NS iteration is three products: A = X X^T and B = b A + c A A^T (A is
-// symmetric) in the NT form, and X' = a X + B X with X as the [K, N] operand.
+// One NS iteration is three products: A = X X^T and B' = c A A^T + b A + a I
+// (A is symmetric; a is added to the diagonal in fp32 before the rounding) in
+// the NT form, and X' = B' X with X as the [K, N] operand.
 //
 // Tiling.  A workgroup (256 lanes, 4 wave64) owns a 256 x 256 tile of C; wave w
 // owns the 128 x 128 quarter (w / 2, w % 2) as 4 x 4 tiles of
@@ -40,7 +41,7 @@
 // column by column), and each XCD gets a contiguous range of that numbering:
 // the concurrently running tiles of an XCD share operand panels in its L2.
 //
-// Symmetric mode (A = X X^T and B = b A + c A A^T are symmetric): only tiles
+// Symmetric mode (A = X X^T and B' = c A A^T + b A + a I are symmetric): only tiles
 // with tile_row <= tile_col run, and each off-diagonal tile is also written
 // transposed into the mirror position, halving the work of those products.
 //

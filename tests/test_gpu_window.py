@@ -7,7 +7,7 @@
   weights, and the fault hook fires after every partial write-back in file order;
 - morph_convert_f32: FP16 bits equal numpy's astype('<f2') and BF16 bits torch's
   conversion on edge cases (ties, overflow, subnormals, inf/NaN); the range flag is
-  export.py:33's condition;
+  export.py:33's condition; FP32 output is a bit copy;
 - rollback (disk.py:110-128): after a fault before the stage's commit or inside an
   update, recover_stage() reloads the window from the restored files, the retried
   update matches the oracle, and an export from the window equals one from the files.
@@ -172,6 +172,37 @@ def test_convert_bf16_bits_equal_torch_including_nan():
     exp = torch.from_numpy(x[~nan]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert np.array_equal(got[~nan], exp)
     assert (got[nan] == 0x7FC0).all()
+
+
+@pytest.mark.parametrize("n,offset", [(100003, 0), (3 * 2048, 0), (5000, 1)])
+def test_convert_f32_copies_bits_and_flags_nonfinite(n, offset):
+    """FP32 output is a bit copy (NaN payloads, -0, subnormals kept): whole blocks, a
+    partial last block, and an unaligned source (element path); the flag is set exactly
+    when some value is inf or NaN."""
+    rng = np.random.RandomState(4)
+    x = (rng.randn(n) * 10).astype(np.float32)
+    x[:len(EDGE)] = EDGE
+    bits = x.view(np.uint32)
+    bits[len(EDGE)] = 0x7FC01234  # a NaN with a payload
+    bits[len(EDGE) + 1] = 0x00000001  # the smallest subnormal
+    base = torch.zeros(n + offset, dtype=torch.float32, device=DEV)
+    base[offset:] = torch.from_numpy(x).to(DEV)
+    src = base[offset:]
+    for check in (False, True):
+        dst = torch.empty(n, dtype=torch.float32, device=DEV)
+        flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+        _lib.check(_lib.lib().morph_convert_f32(
+            ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), _lib.DTYPE_F32, n,
+            ctypes.c_void_p(flag.data_ptr()) if check else None, None))
+        assert np.array_equal(dst.cpu().numpy().view(np.uint32), bits)
+        assert bool(flag.item()) == check
+    finite = torch.from_numpy(np.where(np.isfinite(x), x, 0).astype(np.float32)).to(DEV)
+    flag = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.empty_like(finite)
+    _lib.check(_lib.lib().morph_convert_f32(
+        ctypes.c_void_p(finite.data_ptr()), ctypes.c_void_p(out.data_ptr()), _lib.DTYPE_F32, n,
+        ctypes.c_void_p(flag.data_ptr()), None))
+    assert torch.equal(out, finite) and not bool(flag.item())
 
 
 class JournalBase(Store):
