@@ -16,8 +16,8 @@
 // one rounding per product, so parity with the reference is a tolerance, not
 // bit equality.  The momentum pass writes X0 = bf16(u) (transposed when
 // rows > cols) and the FP64 sum of u^2; the first iteration's products apply
-// the normalisation per matrix, A = X0 X0^T / den^2 and X' = (a X0 + B X0) /
-// den, so u never goes to memory.  The elementwise steps round exactly like
+// the normalisation per matrix, A = X0 X0^T / den^2 and X' = B' X0 / den, so u
+// never goes to memory.  The elementwise steps round exactly like
 // torch (explicit fmaf where its CPU kernels fuse, plain multiplies elsewhere).
 // The quintic's linear term rides on B's diagonal: X' = a X + B X = (B + a I) X,
 // so the last product of an iteration reads no third operand (a is added in fp32
