@@ -172,11 +172,13 @@ def _prepare(mats, rows, cols, hp, orth_only, stream, workspaces, found_inf=None
     return batches
 
 
-def _complete(batches, stream, timer=None):
-    """Newton-Schulz chain and finish for the batches _prepare enqueued.
+def _complete(batches, stream, timer=None, before_finish=None):
+    """Newton-Schulz chains, then the finish of every batch _prepare enqueued.
 
     timer: optional list; (start_event, end_event, dense flops, executed flops) around
-    each NS chain.
+    each NS chain.  before_finish: optional callable run on the host once every
+    chain is enqueued and before the first finish (the pass that reads and writes
+    the parameters) is.
     """
     L = lib()
     sh = stream_handle(stream)
@@ -191,8 +193,11 @@ def _complete(batches, stream, timer=None):
             e1.record(s)
             timer.append((e0, e1, ns_flops(rows, cols, count, hp.ns_steps),
                           ns_executed_flops(rows, cols, count, hp.ns_steps)))
-        check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), int(orth_only), wsp,
-                                  wsn, sh))
+    if before_finish is not None:
+        before_finish()
+    for arr, count, rows, cols, hp, orth_only, ws in batches:
+        check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), int(orth_only),
+                                  ctypes.c_void_p(ws.data_ptr()), ws.numel(), sh))
 
 
 def _check_matrix(t, name):
@@ -223,7 +228,8 @@ def orthogonalize(gradients, steps=NS_STEPS, stream=None, workspaces=_WORKSPACES
 
 
 def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=None,
-              workspaces=_WORKSPACES, timer=None, momenta_out=None, found_inf=None, gate=None):
+              workspaces=_WORKSPACES, timer=None, momenta_out=None, found_inf=None, gate=None,
+              before_finish=None):
     """The Muon loop body of optimizer.py:55-61 for every (param, grad, momentum) triple.
 
     In place on params and momenta.  Scalars follow the reference: decay
@@ -232,7 +238,9 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
     (momenta are then only read).  found_inf: optional device flag set when a
     gradient is non-finite, tested in the momentum pass.  gate: optional
     callable run after that pass and before anything the caller keeps is
-    mutated (with momenta_out); it may raise to drop the step.
+    mutated (with momenta_out); it may raise to drop the step.  before_finish:
+    optional callable run once the Newton-Schulz chains are enqueued, before the
+    parameter update is (the params are not read before it).
     """
     items = []
     outs = momenta_out if momenta_out is not None else [None] * len(params)
@@ -254,7 +262,7 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
                             first=len(batches))
     if gate is not None:
         gate()
-    _complete(batches, stream, timer)
+    _complete(batches, stream, timer, before_finish)
 
 
 def _host_grad(p):
@@ -347,11 +355,18 @@ class HybridMuonAdamW:
         if not live and not adam_present:
             return
         idx = [i for i, _ in live]
+        upload_masters = None
         if self.host:
             device = self._muon_dev[0].device if self.muon else self.adam.device
             if live:
                 self._muon_grads.upload([_host_grad(p) for _, p in live], idx)
-                self._muon_masters.upload([p for _, p in live], idx)
+                # Only the update reads the masters: they cross PCIe while the
+                # Newton-Schulz chain runs.  Nothing queued touches the mirrors
+                # (the last step's write-back has finished), so the copy stream
+                # need not wait for the chain; the update waits for the copy.
+                masters = [p for _, p in live]
+                self._muon_masters._check(masters, idx)  # fail before anything is enqueued
+                upload_masters = (lambda: self._muon_masters.upload(masters, idx, wait=False))
             muon_grads = [self._muon_grads.views[i] for i in idx]
             adam_grads = (self.adam._stage_in([p.grad for p in adam_params], adam_present)
                           if adam_present else None)
@@ -379,7 +394,7 @@ class HybridMuonAdamW:
                       [self.momentum[i] for i in idx], self.lr, self.weight_decay,
                       workspaces=self._workspaces, timer=self.ns_timer,
                       momenta_out=[self._momentum_next[i] for i in idx],
-                      found_inf=self._flag, gate=gate)
+                      found_inf=self._flag, gate=gate, before_finish=upload_masters)
             for i in idx:
                 self.momentum[i], self._momentum_next[i] = self._momentum_next[i], self.momentum[i]
         else:

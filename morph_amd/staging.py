@@ -94,14 +94,19 @@ class HostStaging:
             if not t.is_contiguous():
                 raise ValueError(f"host tensor {i} must be contiguous")
 
-    def upload(self, tensors, which=None, stream=None):
-        """views[which[k]] <- tensors[k] (host, contiguous)."""
+    def upload(self, tensors, which=None, stream=None, wait=True):
+        """views[which[k]] <- tensors[k] (host, contiguous).
+
+        wait=False: the copies do not wait for the work already queued on
+        `stream`; only for a caller that knows no queued work reads or writes
+        these mirrors (later work on `stream` still waits for the copies)."""
         which = list(range(len(self.numels))) if which is None else list(which)
         tensors = list(tensors)
         self._check(tensors, which)
         src = {i: t.detach().reshape(-1) for i, t in zip(which, tensors)}
         stream = stream or torch.cuda.current_stream(self.device)
-        self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
+        if wait:
+            self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
         bufs = self._buffers()
         for k, (lo, hi, pieces) in enumerate(self._chunks(which)):
             slot = bufs[k % 2]
