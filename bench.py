@@ -194,8 +194,9 @@ def time_gpu(steps, warmup):
 
 def copy_ceiling(nbytes, device, reps=10):
     """The HBM rate of a plain FP32 copy moving the bytes of one AdamW launch (half
-    read, half written): the library's convert kernel with FP32 output, timed by events
-    on its stream after the timed steps, median of `reps` launches."""
+    read, half written): the library's streaming copy (morph_convert_f32 with FP32
+    output), timed by events on its stream after the timed steps, median of `reps`
+    launches."""
     from morph_amd import _lib
     n = nbytes // 8
     src = torch.ones(n, device=device)
@@ -215,7 +216,8 @@ def copy_ceiling(nbytes, device, reps=10):
     med = sorted(times)[len(times) // 2]
     gbs = 8 * n / med / 1e6
     return {"achieved": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "kernel": "convert_kernel<F32> (morph_convert_f32, FP32 -> FP32 copy)",
+            "kernel": "copy_kernel (morph_convert_f32 with FP32 output: 64 lanes, one "
+                      "non-temporal 16-byte load and store each)",
             "bytes_per_launch": 8 * n, "median_launch_us": round(med * 1e3, 2), "launches": reps}
 
 

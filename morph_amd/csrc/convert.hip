@@ -14,9 +14,12 @@
 // to inf, as numpy and torch); BF16 by round to nearest even with NaN ->
 // 0x7FC0 (torch's c10::BFloat16).  Each lane converts 8 consecutive values
 // (two 128-bit loads, one 128-bit store for 16-bit output).  The FP32 -> FP32
-// copy instead moves 4 consecutive values per access with consecutive lanes on
-// consecutive 16 bytes (every access instruction covers whole lines) and streams
-// them non-temporally: nothing rereads a copy's source or output soon.
+// copy has a kernel of its own (copy_kernel): 64-lane workgroups, one 16-byte
+// non-temporal load and store per lane, nothing rereads a copy soon.  Of the
+// plain copies measured on 1.585 GB (64, 128 or 256 lanes, 1-4 accesses per
+// lane, temporal or not, with or without a residency cap) this shape was the
+// fastest, 6.58 TB/s against 6.40-6.48 for 128 or 256 lanes and 5.9-6.0 for
+// two temporal or non-temporal accesses per lane of 256.
 #include "common.h"
 
 namespace morph {
@@ -26,6 +29,8 @@ constexpr int kBlock = 256;
 constexpr int kPerLane = 8;
 constexpr int kPerBlock = kBlock * kPerLane;
 constexpr float kF16Max = 65504.0f;
+constexpr int kCopyLanes = 64;
+constexpr int kCopyPerBlock = kCopyLanes * 4;
 
 template <typename OT>
 __device__ __forceinline__ bool out_of_range(float x) {
@@ -39,22 +44,10 @@ template <typename OT, bool kCheck>
 __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict__ src,
                                                          void* __restrict__ dst, int64_t n,
                                                          int vector_ok, uint32_t* flag) {
+  static_assert(!std::is_same_v<OT, F32>, "the FP32 copy is copy_kernel");
   const int64_t base = (int64_t)blockIdx.x * kPerBlock;
   bool bad = false;
-  constexpr bool kCopy = std::is_same_v<OT, F32>;
-  if (kCopy && vector_ok && base + kPerBlock <= n) {
-#pragma unroll
-    for (int k = 0; k < kPerLane / 4; ++k) {
-      const int64_t i = base + ((int64_t)k * kBlock + threadIdx.x) * 4;
-      const f32x4 v = load_stream<true>(reinterpret_cast<const f32x4*>(src + i));
-      if constexpr (kCheck) {
-        const u32x4 u = __builtin_bit_cast(u32x4, v);
-        bad |= nonfinite_f32_bits(u.x) | nonfinite_f32_bits(u.y) | nonfinite_f32_bits(u.z) |
-               nonfinite_f32_bits(u.w);
-      }
-      store_stream<true>(reinterpret_cast<f32x4*>(static_cast<float*>(dst) + i), v);
-    }
-  } else if (vector_ok && base + kPerBlock <= n) {
+  if (vector_ok && base + kPerBlock <= n) {
     const int64_t e = base + (int64_t)threadIdx.x * kPerLane;
     const f32x4 a = *reinterpret_cast<const f32x4*>(src + e);
     const f32x4 b = *reinterpret_cast<const f32x4*>(src + e + 4);
@@ -63,7 +56,7 @@ __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict
 #pragma unroll
       for (int k = 0; k < 8; ++k) bad |= out_of_range<OT>(x[k]);
     }
-    if constexpr (!kCopy) {
+    {
       u32x4 w;
       w.x = from_float<OT>(x[0]) | (from_float<OT>(x[1]) << 16);
       w.y = from_float<OT>(x[2]) | (from_float<OT>(x[3]) << 16);
@@ -76,10 +69,7 @@ __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict
     for (int64_t i = base + threadIdx.x; i < end; i += kBlock) {
       const float x = src[i];
       if constexpr (kCheck) bad |= out_of_range<OT>(x);
-      if constexpr (std::is_same_v<OT, F32>)
-        static_cast<float*>(dst)[i] = x;
-      else
-        static_cast<uint16_t*>(dst)[i] = (uint16_t)from_float<OT>(x);
+      static_cast<uint16_t*>(dst)[i] = (uint16_t)from_float<OT>(x);
     }
   }
   if constexpr (kCheck) {
@@ -88,6 +78,51 @@ __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict
       *f = 1u;
     }
   }
+}
+
+// dst = src (FP32), flag as for FP32 output: some value is inf or NaN.
+template <bool kCheck>
+__global__ __launch_bounds__(kCopyLanes) void copy_kernel(const float* __restrict__ src,
+                                                          float* __restrict__ dst, int64_t n,
+                                                          int vector_ok, uint32_t* flag) {
+  const int64_t base = (int64_t)blockIdx.x * kCopyPerBlock;
+  bool bad = false;
+  if (vector_ok && base + kCopyPerBlock <= n) {
+    const int64_t i = base + (int64_t)threadIdx.x * 4;
+    const f32x4 v = load_stream<true>(reinterpret_cast<const f32x4*>(src + i));
+    if constexpr (kCheck) {
+      const u32x4 u = __builtin_bit_cast(u32x4, v);
+      bad = nonfinite_f32_bits(u.x) | nonfinite_f32_bits(u.y) | nonfinite_f32_bits(u.z) |
+            nonfinite_f32_bits(u.w);
+    }
+    store_stream<true>(reinterpret_cast<f32x4*>(dst + i), v);
+  } else {
+    const int64_t end = base + kCopyPerBlock < n ? base + kCopyPerBlock : n;
+    for (int64_t i = base + threadIdx.x; i < end; i += kCopyLanes) {
+      const float x = src[i];
+      if constexpr (kCheck) bad |= nonfinite_f32_bits(__builtin_bit_cast(uint32_t, x));
+      dst[i] = x;
+    }
+  }
+  if constexpr (kCheck) {
+    if (__builtin_amdgcn_ballot_w64(bad) != 0 && threadIdx.x == 0) {
+      volatile uint32_t* f = flag;
+      *f = 1u;
+    }
+  }
+}
+
+int launch_copy(const float* src, float* dst, int64_t n, int vector_ok, uint32_t* flag,
+                hipStream_t s) {
+  const int64_t blocks = (n + kCopyPerBlock - 1) / kCopyPerBlock;
+  if (blocks > 0x7FFFFFFF) return MORPH_ERANGE;
+  if (flag)
+    hipLaunchKernelGGL(copy_kernel<true>, dim3((unsigned)blocks), dim3(kCopyLanes), 0, s, src,
+                       dst, n, vector_ok, flag);
+  else
+    hipLaunchKernelGGL(copy_kernel<false>, dim3((unsigned)blocks), dim3(kCopyLanes), 0, s, src,
+                       dst, n, vector_ok, flag);
+  return launch_status();
 }
 
 template <typename OT>
@@ -120,6 +155,6 @@ extern "C" int morph_convert_f32(const float* src, void* dst, int dst_dtype, int
   switch (dst_dtype) {
     case MORPH_DTYPE_F16: return launch<F16>(src, dst, n, vector_ok, d_range_flag, s);
     case MORPH_DTYPE_BF16: return launch<BF16>(src, dst, n, vector_ok, d_range_flag, s);
-    default: return launch<F32>(src, dst, n, vector_ok, d_range_flag, s);
+    default: return launch_copy(src, static_cast<float*>(dst), n, vector_ok, d_range_flag, s);
   }
 }
