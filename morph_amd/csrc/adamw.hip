@@ -15,12 +15,16 @@
 // lanes cover consecutive 16-byte pieces, so every wave-wide access is one
 // contiguous 1 KiB (FP32) or 512 B (16-bit) segment.  All loads of a lane are
 // issued before any arithmetic.  Measured on MI355X (config 2 window), small
-// workgroups with one access per lane (128 x 1) stream best: many short-lived
+// workgroups with one access per lane stream best: many short-lived
 // workgroups keep every CU's memory pipeline full, while longer per-lane
-// chains (unroll 4/8) or 1024-lane groups lose 3-7%; and fewer of them per CU
-// at a time (8, set by the launch's LDS reservation), with each lane's stream
-// loads issued before the step's control words are read, are 0-6% faster
-// than the hardware's own limit.  Chunks map to workgroups
+// chains (unroll 2/4/8) or 1024-lane groups lose 3-7%; and fewer of them per
+// CU at a time (16 waves, set by the launch's LDS reservation), with each
+// lane's stream loads issued before the step's control words are read, are
+// 0-6% faster than the hardware's own limit.  One-wave workgroups (64 x 1, 16
+// per CU) beat two-wave ones (128 x 1, 8 per CU) by 1.5% (234.4-235.9 against
+// 237.2-238.4 us, one variant per process, alternated on one box); 64 x 1 at
+// 11, 13 or 20 per CU, 64 x 2 and 128 x 1 at 16 per CU were slower, uncapped
+// 64 x 1 by 3%.  Chunks map to workgroups
 // in address order; the dispatcher spreads consecutive workgroups round-robin
 // over the 8 XCDs, which is what a pure stream with no reuse wants.
 //
@@ -44,7 +48,7 @@
 #define MORPH_ADAMW_GRAD_NT 0
 #endif
 #ifndef MORPH_ADAMW_BLOCK
-#define MORPH_ADAMW_BLOCK 128
+#define MORPH_ADAMW_BLOCK 64
 #endif
 #ifndef MORPH_ADAMW_NT
 #define MORPH_ADAMW_NT 1
@@ -61,14 +65,14 @@ constexpr int kPerBlock = kBlock * 4 * kUnroll;
 constexpr int kMaxTensors = 48;
 constexpr int kMaxHp = 8;
 // Residency cap: every workgroup reserves this much LDS, which it does not
-// use, so at most 160 KiB / 20 KiB = 8 workgroups (16 waves) share a CU.  The
-// stream runs faster with fewer workgroups in flight per CU, by an amount that
-// depends on where the buffers sit in physical memory: config-2 window,
-// round-robin against the uncapped kernel in one process, 0-15 us faster in
-// most placements and up to 3 us slower in a few; a cap of 7 is as fast, 6 is
-// slower and 5 far slower (277 us).  The cap pays off with the loads issued
-// before the control words (adamw_multi_kernel).
-constexpr unsigned kOccupancyLds = 20 * 1024;
+// use, so at most 160 KiB / 10 KiB = 16 one-wave workgroups share a CU.  The
+// stream runs faster with fewer waves in flight per CU, by an amount that
+// depends on where the buffers sit in physical memory (measured with two-wave
+// workgroups, config-2 window, round-robin against the uncapped kernel in one
+// process: 0-15 us faster in most placements and up to 3 us slower in a few;
+// 14 waves as fast, 12 slower and 10 far slower, 277 us).  The cap pays off
+// with the loads issued before the control words (adamw_multi_kernel).
+constexpr unsigned kOccupancyLds = 10 * 1024;
 // A tensor is cut into segments of at most this many elements so block
 // counts stay far inside the 32-bit grid limits.
 constexpr int64_t kMaxSegment = int64_t(1) << 30;
