@@ -390,6 +390,25 @@ def test_mixed_orientation_batch_equals_separate_batches():
         assert torch.equal(outs[i], muon.orthogonalize(g[i])), i
 
 
+def test_more_than_64_matrices_run_as_several_batches():
+    """A shape's matrices go to the library 64 per call: 70 of them (both orientations) come
+    out bit-identical to running each alone, and so does orthogonalize."""
+    gen = torch.Generator().manual_seed(13)
+    shapes = [(96, 64) if i % 3 == 0 else (64, 96) for i in range(70)]
+    p0 = [torch.randn(s, generator=gen) * .02 for s in shapes]
+    m0 = [torch.randn(s, generator=gen) * 1e-3 for s in shapes]
+    g = [(torch.randn(s, generator=gen) * 1e-3).to(DEV) for s in shapes]
+    pa, ma = [t.to(DEV) for t in p0], [t.to(DEV) for t in m0]
+    muon.muon_step(pa, g, ma, .02, .01)
+    for i in (0, 1, 63, 64, 69):
+        pb, mb = p0[i].to(DEV), m0[i].to(DEV)
+        muon.muon_step([pb], [g[i]], [mb], .02, .01)
+        assert torch.equal(pa[i], pb) and torch.equal(ma[i], mb), i
+    outs = muon.orthogonalize(g)
+    for i in (2, 64, 68):
+        assert torch.equal(outs[i], muon.orthogonalize(g[i])), i
+
+
 def test_transposed_flag_equals_passing_the_transposed_shape():
     """C ABI: a [c, r] matrix flagged transposed under (rows, cols) = (r, c) equals the
     same matrix passed unflagged as (c, r)."""
