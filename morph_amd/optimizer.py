@@ -101,6 +101,7 @@ class FusedAdamW:
             device = p.device
         self._staging = None   # HostStaging of CPU masters (None: masters on the GPU)
         self._grad_staging = None
+        self._chunk_cache = None  # per-chunk descriptor batches of the CPU-master pipeline
         if device.type == "cpu":
             for _, p in flat:
                 if not p.is_contiguous():
@@ -287,15 +288,15 @@ class FusedAdamW:
             return True if self.sync else None
         if self._staging is None:
             return self._enqueue(grads, present, stream, checked)
-        dev_grads = self._stage_in(grads, present, stream)
-        try:
-            return self._enqueue(dev_grads, present, stream, checked)
-        finally:
-            self._stage_out(present, stream)
+        # CPU masters: the gradients go up first (the gate needs all of them), then
+        # the masters stream through the update chunk by chunk, each chunk coming
+        # back while the next goes up
+        dev_grads = self._stage_in(grads, present, stream, masters=False)
+        return self._enqueue(dev_grads, present, stream, checked, pipeline=True)
 
-    def _stage_in(self, grads, present, stream=None):
-        """CPU masters: upload the listed masters and the host gradients; returns the
-        per-parameter device gradients (None where absent)."""
+    def _stage_in(self, grads, present, stream=None, masters=True):
+        """CPU masters: upload the host gradients (and with `masters` the listed
+        masters); returns the per-parameter device gradients (None where absent)."""
         flat = self._flat()
         host = [i for i in present if grads[i].device.type == "cpu"]
         for i in present:
@@ -317,7 +318,8 @@ class FusedAdamW:
             self._grad_staging.upload([grads[i].contiguous() for i in host], host, stream)
             for i in host:
                 dev[i] = self._grad_staging.views[i]
-        self._staging.upload([flat[i][1] for i in present], present, stream)
+        if masters:
+            self._staging.upload([flat[i][1] for i in present], present, stream)
         return dev
 
     def _stage_out(self, present, stream=None):
@@ -325,8 +327,37 @@ class FusedAdamW:
         flat = self._flat()
         self._staging.download([flat[i][1].data for i in present], present, stream)
 
-    def _enqueue(self, grads, present, stream, checked):
-        """The device step over device gradients (see step())."""
+    def _chunk_batches(self, grads, present, hp_of):
+        """One descriptor batch per staging chunk of the listed tensors (CPU masters):
+        views of the mirrors, moments, gradients and exports over the chunk's
+        elements, each with its tensor's constants and clock."""
+        flat = self._flat()
+        key = (tuple(present), tuple(grads[i].dtype for i in present),
+               tuple(grads[i].data_ptr() for i in present),
+               tuple(e.data_ptr() for e in self.exports) if self.exports else None)
+        if self._chunk_cache is not None and self._chunk_cache[0] == key:
+            return self._chunk_cache[1]
+        batches = []
+        for _, _, pieces in self._staging._chunks(present):
+            ps, ms, vs, gs, outs, hpi, ci = [], [], [], [], [], [], []
+            for i, a, b in pieces:
+                p = flat[i][1]
+                ps.append(self._dev[i].view(-1)[a:b])
+                ms.append(self.state[p]["exp_avg"].view(-1)[a:b])
+                vs.append(self.state[p]["exp_avg_sq"].view(-1)[a:b])
+                gs.append(grads[i].reshape(-1)[a:b])
+                outs.append(self.exports[i].view(-1)[a:b] if self.exports else None)
+                hpi.append(hp_of[flat[i][0]])
+                ci.append(i)
+            batches.append(kernels.AdamwBatch(ps, ms, vs, gs, outs if self.exports else None,
+                                              hp_index=hpi, clock_index=ci))
+        self._chunk_cache = (key, batches)
+        return batches
+
+    def _enqueue(self, grads, present, stream, checked, pipeline=False):
+        """The device step over device gradients (see step()).  pipeline: CPU
+        masters, streamed through the update by HostStaging.pipeline (the launch
+        timers do not apply)."""
         flat = self._flat()
         if self._ctl.scaler_changed():  # the caller edited the scaler: resync the device copy
             self.resolve()
@@ -355,7 +386,17 @@ class FusedAdamW:
             self._pending = None
         else:
             kernels.nonfinite_or([grads[i] for i in present], ctl.found_inf_ptr(slot), s)
-        if self.kernel_timer is not None:
+        if pipeline:
+            flat = self._flat()
+            groups = sorted({flat[i][0] for i in present})
+            chunk_batches = self._chunk_batches(grads, present, {g: k for k, g in enumerate(groups)})
+            launches = iter(chunk_batches)
+            self._staging.pipeline(
+                [flat[i][1].data for i in present], present,
+                lambda lo, hi, pieces, st: next(launches).launch_dev(hps, scheds, ctl.clocks,
+                                                                     ctl.state, slot, st, None),
+                s)
+        elif self.kernel_timer is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
             batch.launch_dev(hps, scheds, ctl.clocks, ctl.state, slot, s, events)

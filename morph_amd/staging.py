@@ -10,7 +10,10 @@ mirror of each host tensor (each at a 256-byte aligned offset) and moves data
 between the host tensors and the mirrors in chunks through two pinned buffers
 per direction, so the host-side copy of one chunk (pageable <-> pinned, torch's
 multi-threaded copy) overlaps the DMA of the other.  Tensors whose mirrors are
-adjacent travel in one DMA per chunk.
+adjacent travel in one DMA per chunk.  pipeline() streams chunks through a
+device pass: chunk k goes up while chunk k - 1 comes back, on one copy stream
+per direction (PCIe carries both directions at once: 88 GB/s together against
+56 GB/s either way alone, measured on MI355X).
 """
 import torch
 
@@ -31,6 +34,8 @@ class HostStaging:
     device side ordered before later work on `stream`.
     """
 
+    _LAG = 2  # pipeline(): chunks between a chunk's download and its copy out
+
     def __init__(self, shapes, dtype, device, chunk_elements=1 << 22):
         self.device = torch.device(device)
         self.dtype = dtype
@@ -45,14 +50,19 @@ class HostStaging:
                       for o, n, s in zip(self.offsets, self.numels, self.shapes)]
         self.chunk = max(int(chunk_elements), ALIGN)
         self._copy = torch.cuda.Stream(self.device)
+        self._copy_down = None
         self._pinned = None
+        self._pinned_down = None
         self.bytes_h2d = 0
         self.bytes_d2h = 0
 
+    def _new_buffers(self, count=2):
+        return [dict(buf=torch.empty(self.chunk, dtype=self.dtype, pin_memory=True),
+                     event=torch.cuda.Event()) for _ in range(count)]
+
     def _buffers(self):
         if self._pinned is None:
-            self._pinned = [dict(buf=torch.empty(self.chunk, dtype=self.dtype, pin_memory=True),
-                                 event=torch.cuda.Event()) for _ in range(2)]
+            self._pinned = self._new_buffers()
         return self._pinned
 
     def _chunks(self, which):
@@ -153,3 +163,61 @@ class HostStaging:
             if k + 2 < len(chunks):
                 fetch(k + 2)  # this buffer is free again
         stream.wait_stream(self._copy)
+
+    def pipeline(self, tensors, which, launch, stream=None):
+        """Per chunk of the listed mirrors: upload it from the host tensors, run
+        launch(lo, hi, pieces, stream) (device work on those elements, enqueued on
+        `stream`), then download it back into the same host tensors.  Chunk k + 1
+        goes up while chunk k comes back.  Ordered after the work already queued on
+        `stream`; returns with every host tensor updated, later work on `stream`
+        ordered after the downloads.  pieces: (index, start, end) of each listed
+        tensor's elements in the chunk.  The host copies chunk k - 2 out of its
+        pinned buffer while chunk k goes up, so it rarely waits for a download."""
+        which = list(which)
+        tensors = list(tensors)
+        self._check(tensors, which)
+        host = {i: t.detach().view(-1) for i, t in zip(which, tensors)}
+        stream = stream or torch.cuda.current_stream(self.device)
+        if self._copy_down is None:
+            self._copy_down = torch.cuda.Stream(self.device)
+        if self._pinned_down is None:
+            self._pinned_down = self._new_buffers(self._LAG + 1)
+        up, down = self._buffers(), self._pinned_down
+        self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
+        size = self.flat.element_size()
+
+        def copy_out(k, lo, hi, pieces):
+            slot = down[k % len(down)]
+            slot["event"].synchronize()  # this chunk's download has landed
+            for i, s, e in pieces:
+                at = self.offsets[i] + s - lo
+                host[i][s:e].copy_(slot["buf"][at:at + e - s])
+
+        pending = []
+        for k, (lo, hi, pieces) in enumerate(self._chunks(which)):
+            slot = up[k % 2]
+            slot["event"].synchronize()  # the upload that last read this buffer is done
+            for i, s, e in pieces:
+                at = self.offsets[i] + s - lo
+                slot["buf"][at:at + e - s].copy_(host[i][s:e])
+            with torch.cuda.stream(self._copy):
+                self.flat[lo:hi].copy_(slot["buf"][:hi - lo], non_blocking=True)
+                slot["event"].record(self._copy)
+            self.bytes_h2d += (hi - lo) * size
+            stream.wait_stream(self._copy)
+            launch(lo, hi, pieces, stream)
+            # down[k % (LAG + 1)] last held chunk k - LAG - 1, copied out already
+            dslot = down[k % len(down)]
+            self._copy_down.wait_stream(stream)
+            with torch.cuda.stream(self._copy_down):
+                dslot["buf"][:hi - lo].copy_(self.flat[lo:hi], non_blocking=True)
+                dslot["event"].record(self._copy_down)
+            self.bytes_d2h += (hi - lo) * size
+            pending.append((k, lo, hi, pieces))
+            if len(pending) > self._LAG:
+                copy_out(*pending.pop(0))
+        for item in pending:
+            copy_out(*item)
+        for slot in up:
+            slot["event"].synchronize()  # the caller may change the host tensors on return
+        stream.wait_stream(self._copy_down)

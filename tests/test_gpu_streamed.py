@@ -57,9 +57,12 @@ def test_host_staging_round_trips():
     assert float(one[0]) == 5.0
 
 
-def test_fused_adamw_on_cpu_masters_config1():
+@pytest.mark.parametrize("chunk", [None, 5000])
+def test_fused_adamw_on_cpu_masters_config1(chunk):
     """BASELINE config 1 (param groups: wd .1 on 2-D only) with CPU masters and CPU FP32
-    gradients: every step bit-exact against the oracle and against device masters."""
+    gradients: every step bit-exact against the oracle and against device masters.  With
+    chunk=5000 the masters stream through the update in 60 chunks, most spanning two
+    tensors at offsets that are not multiples of 64."""
     from oracle import reference as R
     masters, grads = config1_inputs()
     cpu = [m.clone() for m in masters]
@@ -68,6 +71,8 @@ def test_fused_adamw_on_cpu_masters_config1():
                          dict(params=[p for p in ps if p.ndim == 1], weight_decay=0.0)]
     kw = dict(lr=CONFIG1["lr"], betas=CONFIG1["betas"], eps=CONFIG1["eps"])
     opt_c, opt_d = FusedAdamW(groups(cpu), **kw), FusedAdamW(groups(dev), **kw)
+    if chunk is not None:
+        opt_c._staging.chunk = chunk
     flat_c = [p for g in opt_c.param_groups for p in g["params"]]
     flat_d = [p for g in opt_d.param_groups for p in g["params"]]
     W = [p.numpy().ravel().copy() for p in flat_c]
@@ -199,6 +204,39 @@ def test_hybrid_on_cpu_masters_raises_before_any_mutation(poisoned):
         o.step()
     for (n, p), (_, q) in zip(model.named_parameters(), twin.named_parameters()):
         assert torch.equal(p, q), n
+
+
+def test_fused_adamw_on_cpu_masters_raises_before_any_mutation():
+    """on_overflow="raise" with CPU masters: a non-finite gradient raises with the CPU masters
+    and the moments untouched, and the next finite step equals that of an optimizer that never
+    saw the poisoned one."""
+    gen = torch.Generator().manual_seed(5)
+    shapes = [(300, 70), (70,), (128, 300)]
+    params = [torch.randn(s, generator=gen) * .02 for s in shapes]
+    twin = [p.clone() for p in params]
+    kw = dict(lr=1e-3, betas=(.9, .95), weight_decay=.1, on_overflow="raise")
+    opt, opt2 = FusedAdamW(params, **kw), FusedAdamW(twin, **kw)
+    opt._staging.chunk = 7000
+    g1 = [torch.randn(s, generator=gen) * 1e-3 for s in shapes]
+    opt.step([g.clone() for g in g1])
+    opt2.step([g.clone() for g in g1])
+    before = [p.clone() for p in params]
+    moments = copy.deepcopy(opt.state_dict()["state"])
+    bad = [torch.randn(s, generator=gen) * 1e-3 for s in shapes]
+    bad[2].view(-1)[12345] = float("nan")
+    with pytest.raises(FloatingPointError):
+        opt.step(bad)
+    for p, b in zip(params, before):
+        assert torch.equal(p, b)
+    after = opt.state_dict()["state"]
+    for k, st in moments.items():
+        assert torch.equal(after[k]["exp_avg"], st["exp_avg"])
+        assert torch.equal(after[k]["exp_avg_sq"], st["exp_avg_sq"])
+    g3 = [torch.randn(s, generator=gen) * 1e-3 for s in shapes]
+    opt.step([g.clone() for g in g3])
+    opt2.step([g.clone() for g in g3])
+    for p, q in zip(params, twin):
+        assert torch.equal(p, q)
 
 
 def test_mixed_devices_are_rejected():
