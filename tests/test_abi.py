@@ -80,6 +80,12 @@ def test_argument_validation_happens_before_any_launch():
     assert lib.morph_grad_accumulate_final_noalloc(big, 1, 1, 1.0, 0, st, st, None) == -4
     big[0].numel = 1 << 31
     assert lib.morph_grad_partials(big, 1) == _lib.NOALLOC_MAX_PARTIALS
+    # conversion: grid limits of the copy (FP32) and of the 16-bit conversions -> ERANGE
+    src, dst = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x20000)
+    conv = lambda dtype, n: lib.morph_convert_f32(src, dst, dtype, ctypes.c_int64(n), None, None)
+    assert conv(_lib.DTYPE_F32, 256 * (2 ** 31 - 1) + 1) == -4
+    assert conv(_lib.DTYPE_F16, 2048 * (2 ** 31 - 1) + 1) == -4
+    assert conv(5, 10) == -2 and conv(_lib.DTYPE_F32, -1) == -1
     # GEMM: validated on the host (fake, aligned pointers are never dereferenced)
     p = ctypes.c_void_p(0x10000)
     gemm = lambda M, N, K, flags, Ct=None: lib.morph_gemm_nt_bf16(
