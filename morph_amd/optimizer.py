@@ -52,9 +52,10 @@ class FusedAdamW:
     params: FP32 tensors (or torch-style param-group dicts), all on one GPU, or
       all on the CPU -- the streamed engines' masters (runner.py:41-46).  With
       CPU masters the moments stay resident in HBM; each step uploads the
-      gradients (CPU p.grad, or device tensors) and the masters through pinned
-      staging, runs the same kernels on device mirrors, and writes the updated
-      masters back into the CPU tensors before returning (morph_amd.staging).
+      gradients (CPU p.grad, or device tensors) through pinned staging, runs
+      the gate, then streams the masters through the update chunk by chunk
+      (morph_amd.staging.HostStaging.pipeline) and returns with the updated
+      masters in the CPU tensors.
     loss_scale: None (no scaling), a float (fixed scale), or a DynamicLossScale
       whose state this optimizer advances (on the device) after every step.
     export_dtype: torch.float16 / torch.bfloat16 to keep an export copy of
