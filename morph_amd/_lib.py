@@ -8,6 +8,7 @@ pointers are valid in both.  There is no fallback: when the library is missing
 every entry point raises.
 """
 import ctypes
+import threading
 from pathlib import Path
 
 import torch  # noqa: F401  (must load the HIP runtime before the library)
@@ -94,64 +95,72 @@ class MuonHP(ctypes.Structure):
 
 
 _lib = None
+_load_lock = threading.Lock()
 
 
 def lib():
-    """The loaded library; raises if it has not been built."""
-    global _lib
+    """The loaded library (loaded once, by whichever thread asks first); raises if
+    it has not been built."""
     if _lib is None:
-        if not LIB_PATH.exists():
-            raise ImportError(
-                f"{LIB_PATH} is missing: build the HIP library first "
-                "(python -m morph_amd.build); morph_amd has no CPU fallback")
-        handle = ctypes.CDLL(str(LIB_PATH))
-        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
-        sig = {
-            "morph_abi_version": ([], i32),
-            "morph_strerror": ([i32], ctypes.c_char_p),
-            "morph_flag_clear": ([vp, vp], i32),
-            "morph_nonfinite_or": ([vp, i32, i64, vp, vp], i32),
-            "morph_nonfinite_or_multi": ([vp, vp, i32, i32, vp, vp], i32),
-            "morph_adamw_fused": ([vp, i32, vp, vp, vp, vp, i32, i64, ctypes.POINTER(AdamwHP),
-                                   vp, vp], i32),
-            "morph_adamw_multi": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
-                                   ctypes.POINTER(AdamwHP), i32, vp, vp, vp, vp], i32),
-            "morph_adamw_multi_dev": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
-                                       ctypes.POINTER(AdamwHP), ctypes.POINTER(AdamwSched), i32,
-                                       vp, vp, i32, vp, vp, vp], i32),
-            "morph_step_end": ([vp, vp, vp, i32, i32, vp], i32),
-            "morph_nonfinite_or_close": ([vp, vp, i32, i32, vp, i32, vp, vp, i32, vp], i32),
-            "morph_grad_partials": ([ctypes.POINTER(AccumTensor), i32], i64),
-            "morph_grad_accumulate": ([ctypes.POINTER(AccumTensor), i32, i32, ctypes.c_double, i32,
-                                       vp, vp, i64, vp], i32),
-            "morph_grad_accumulate_final_noalloc": ([ctypes.POINTER(AccumTensor), i32, i32,
-                                                     ctypes.c_double, i32, vp, vp, vp], i32),
-            "morph_sumsq_total": ([vp, i64, vp, i32, vp], i32),
-            "morph_convert_f32": ([vp, vp, i32, i64, vp, vp], i32),
-            "morph_fp8_pack": ([vp, i32, i64, vp, vp, vp], i32),
-            "morph_fp8_unpack": ([vp, vp, i64, vp, i32, vp], i32),
-            "morph_gemm_nt_bf16": ([vp, vp, vp, vp, vp] + [i64] * 14 +
-                                   [ctypes.c_float, ctypes.c_float, i32, vp], i32),
-            "morph_muon_workspace_bytes": ([i64, i64, i32], ctypes.c_size_t),
-            "morph_muon_step": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
-                                 ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
-            "morph_muon_orthogonalize": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
-                                          ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
-            "morph_muon_prepare": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
-                                    ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp, vp], i32),
-            "morph_muon_newton_schulz": ([i32, i64, i64, ctypes.POINTER(MuonHP), vp,
-                                          ctypes.c_size_t, vp], i32),
-            "morph_muon_finish": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
-                                   ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp], i32),
-        }
-        for name, (args, res) in sig.items():
-            fn = getattr(handle, name)
-            fn.argtypes, fn.restype = args, res
-        version = handle.morph_abi_version()
-        if version != ABI_VERSION:
-            raise ImportError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}")
-        _lib = handle
+        with _load_lock:
+            if _lib is None:
+                _load()
     return _lib
+
+
+def _load():
+    global _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build the HIP library first "
+            "(python -m morph_amd.build); morph_amd has no CPU fallback")
+    handle = ctypes.CDLL(str(LIB_PATH))
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    sig = {
+        "morph_abi_version": ([], i32),
+        "morph_strerror": ([i32], ctypes.c_char_p),
+        "morph_flag_clear": ([vp, vp], i32),
+        "morph_nonfinite_or": ([vp, i32, i64, vp, vp], i32),
+        "morph_nonfinite_or_multi": ([vp, vp, i32, i32, vp, vp], i32),
+        "morph_adamw_fused": ([vp, i32, vp, vp, vp, vp, i32, i64, ctypes.POINTER(AdamwHP),
+                               vp, vp], i32),
+        "morph_adamw_multi": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
+                               ctypes.POINTER(AdamwHP), i32, vp, vp, vp, vp], i32),
+        "morph_adamw_multi_dev": ([ctypes.POINTER(AdamwTensor), i32, i32, i32,
+                                   ctypes.POINTER(AdamwHP), ctypes.POINTER(AdamwSched), i32,
+                                   vp, vp, i32, vp, vp, vp], i32),
+        "morph_step_end": ([vp, vp, vp, i32, i32, vp], i32),
+        "morph_nonfinite_or_close": ([vp, vp, i32, i32, vp, i32, vp, vp, i32, vp], i32),
+        "morph_grad_partials": ([ctypes.POINTER(AccumTensor), i32], i64),
+        "morph_grad_accumulate": ([ctypes.POINTER(AccumTensor), i32, i32, ctypes.c_double, i32,
+                                   vp, vp, i64, vp], i32),
+        "morph_grad_accumulate_final_noalloc": ([ctypes.POINTER(AccumTensor), i32, i32,
+                                                 ctypes.c_double, i32, vp, vp, vp], i32),
+        "morph_sumsq_total": ([vp, i64, vp, i32, vp], i32),
+        "morph_convert_f32": ([vp, vp, i32, i64, vp, vp], i32),
+        "morph_fp8_pack": ([vp, i32, i64, vp, vp, vp], i32),
+        "morph_fp8_unpack": ([vp, vp, i64, vp, i32, vp], i32),
+        "morph_gemm_nt_bf16": ([vp, vp, vp, vp, vp] + [i64] * 14 +
+                               [ctypes.c_float, ctypes.c_float, i32, vp], i32),
+        "morph_muon_workspace_bytes": ([i64, i64, i32], ctypes.c_size_t),
+        "morph_muon_step": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                             ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
+        "morph_muon_orthogonalize": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                                      ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp], i32),
+        "morph_muon_prepare": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                                ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp, vp], i32),
+        "morph_muon_newton_schulz": ([i32, i64, i64, ctypes.POINTER(MuonHP), vp,
+                                      ctypes.c_size_t, vp], i32),
+        "morph_muon_finish": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
+                               ctypes.POINTER(MuonHP), i32, vp, ctypes.c_size_t, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(handle, name)
+        fn.argtypes, fn.restype = args, res
+    version = handle.morph_abi_version()
+    if version != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH} has ABI {version}, expected {ABI_VERSION}")
+    _lib = handle
 
 
 def check(status):

@@ -91,6 +91,39 @@ def test_random_parameters_bitexact_and_torch_close(tmp_path, n, chunk):
     assert np.abs(got[0] - ref[0]).max() <= 1e-6 * np.abs(ref[0]).max()
 
 
+def test_updates_from_two_threads_at_once(tmp_path):
+    """disk.py:287-300: the main thread calls update() while SlotPrefetch's worker works on
+    other parameters.  Two threads updating their own stores at the same time (each
+    chunk's launches and copies ordered on the calling thread's stream) both end
+    bit-exact against the oracle."""
+    rng = np.random.RandomState(21)
+    n = 300001
+    w0 = {k: (rng.randn(n) * .02).astype(np.float32) for k in ("a", "b")}
+    ups = {k: [((rng.randn(n) * 1e-2).astype(np.float32), s, .001, .7) for s in (1, 2, 3)]
+           for k in ("a", "b")}
+    stores = {k: Store(tmp_path / k, {"p": w0[k]}) for k in ("a", "b")}
+    errors = []
+
+    def run(k):
+        try:
+            side = torch.cuda.Stream() if k == "b" else None  # one thread on its own stream
+            with torch.cuda.stream(side) if side is not None else torch.cuda.stream(
+                    torch.cuda.current_stream()):
+                for g, step, lr, clip in ups[k]:
+                    stores[k].update("p", torch.from_numpy(g), step, lr, clip, chunk_elements=65536)
+        except Exception as e:  # surfaced on the main thread below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(k,)) for k in ("a", "b")]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for k in ("a", "b"):
+        assert_same_bits(stores[k].state("p"), oracle_disk(w0[k], ups[k]), f"store {k}")
+
+
 def test_device_gradient_input(tmp_path):
     rng = np.random.RandomState(3)
     w0 = (rng.randn(70000) * .02).astype(np.float32)
