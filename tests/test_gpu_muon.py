@@ -281,6 +281,36 @@ def test_hybrid_partition_and_adam_group_match_torch():
         assert (p.detach().cpu() - q.detach()).abs().max() <= 1e-6 * q.detach().abs().max()
 
 
+def test_adam_group_bitexact_with_torch_on_the_reference_known_answer():
+    """tests/test_training.py:9-28's known answer: every AdamW-group gradient 0.2 for three
+    steps; the group equals torch.optim.AdamW(betas .9/.95, foreach=False) with rtol = atol = 0
+    (masters included: this input never meets torch's 1-ulp CPU sqrt), then a NaN gradient
+    raises with the whole model untouched."""
+    torch.manual_seed(3)
+    cpu = Tiny()
+    gpu = copy.deepcopy(cpu).to(DEV)
+    opt = muon.HybridMuonAdamW(gpu, lr=.003)
+    names = [n for n, _ in cpu.named_parameters() if n not in ("up.weight", "down.weight")]
+    ref_params = [dict(cpu.named_parameters())[n] for n in names]
+    ref = torch.optim.AdamW(ref_params, lr=.003, weight_decay=.01, betas=(.9, .95), foreach=False)
+    for _ in range(3):
+        for n, p in gpu.named_parameters():
+            p.grad = torch.full_like(p, .2) if n in names else torch.zeros_like(p)
+        for q in ref_params:
+            q.grad = torch.full_like(q, .2)
+        opt.step()
+        ref.step()
+    for n, q in zip(names, ref_params):
+        torch.testing.assert_close(dict(gpu.named_parameters())[n].detach().cpu(), q.detach(),
+                                   rtol=0, atol=0)
+    before = {k: v.clone() for k, v in gpu.state_dict().items()}
+    dict(gpu.named_parameters())[names[0]].grad.fill_(float("nan"))
+    with pytest.raises(FloatingPointError):
+        opt.step()
+    for k, v in gpu.state_dict().items():
+        torch.testing.assert_close(v, before[k], rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("poisoned,bad", [("norm.weight", float("nan")),
                                           ("up.weight", float("inf")),
                                           ("down.weight", float("nan"))])
