@@ -12,8 +12,10 @@
 //
 // Rounding: FP16 by the hardware conversion (round to nearest even, overflow
 // to inf, as numpy and torch); BF16 by round to nearest even with NaN ->
-// 0x7FC0 (torch's c10::BFloat16).  Each lane converts 8 consecutive values
-// (two 128-bit loads, one 128-bit store for 16-bit output).  The FP32 -> FP32
+// 0x7FC0 (torch's c10::BFloat16).  Each lane converts 4 consecutive values of
+// each half of its workgroup's 2048 (a 128-bit non-temporal load, a 64-bit
+// store), so every access instruction covers whole lines: 2.5% faster than 8
+// consecutive values per lane with temporal loads.  The FP32 -> FP32
 // copy has a kernel of its own (copy_kernel): 64-lane workgroups, one 16-byte
 // non-temporal load and store per lane, nothing rereads a copy soon.  Of the
 // plain copies measured on 1.585 GB (64, 128 or 256 lanes, 1-4 accesses per
@@ -48,21 +50,18 @@ __global__ __launch_bounds__(kBlock) void convert_kernel(const float* __restrict
   const int64_t base = (int64_t)blockIdx.x * kPerBlock;
   bool bad = false;
   if (vector_ok && base + kPerBlock <= n) {
-    const int64_t e = base + (int64_t)threadIdx.x * kPerLane;
-    const f32x4 a = *reinterpret_cast<const f32x4*>(src + e);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(src + e + 4);
-    const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    if constexpr (kCheck) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) bad |= out_of_range<OT>(x[k]);
-    }
-    {
-      u32x4 w;
-      w.x = from_float<OT>(x[0]) | (from_float<OT>(x[1]) << 16);
-      w.y = from_float<OT>(x[2]) | (from_float<OT>(x[3]) << 16);
-      w.z = from_float<OT>(x[4]) | (from_float<OT>(x[5]) << 16);
-      w.w = from_float<OT>(x[6]) | (from_float<OT>(x[7]) << 16);
-      *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(dst) + e) = w;
+    for (int h = 0; h < kPerLane / 4; ++h) {
+      const int64_t e = base + ((int64_t)h * kBlock + threadIdx.x) * 4;
+      const f32x4 a = load_stream<true>(reinterpret_cast<const f32x4*>(src + e));
+      const float x[4] = {a.x, a.y, a.z, a.w};
+      if constexpr (kCheck) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bad |= out_of_range<OT>(x[k]);
+      }
+      const u32x2 w = u32x2{from_float<OT>(x[0]) | (from_float<OT>(x[1]) << 16),
+                            from_float<OT>(x[2]) | (from_float<OT>(x[3]) << 16)};
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(dst) + e) = w;
     }
   } else {
     const int64_t end = base + kPerBlock < n ? base + kPerBlock : n;
