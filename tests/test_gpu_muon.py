@@ -180,13 +180,14 @@ def test_orthogonalize_without_iterations_is_the_normalised_input(shape):
     assert bool(((out - ref).abs() <= ref.abs() * 2 ** -7).all())
 
 
-@pytest.mark.parametrize("shape", [(128, 256), (100, 300), (45, 70), (300, 100), (70, 45),
-                                   (4100, 1024)])
+@pytest.mark.parametrize("shape", [(128, 256), (100, 300), (45, 70), (96, 96), (1, 300),
+                                   (300, 100), (70, 45), (300, 1), (4100, 1024)])
 def test_muon_step_elementwise_bitexact(shape):
     """momentum/Nesterov and the master update match the oracle bit for bit: the flat
     passes (X in the stored layout: (128, 256) whole blocks, (100, 300) a partial last
-    block, (45, 70) rows not a multiple of 4) and the transposing tile passes ((300, 100)
-    and (70, 45) partial tiles only, (4100, 1024) whole tiles and a partial last band)."""
+    block, (45, 70) rows not a multiple of 4, (96, 96) square, (1, 300) a single row) and
+    the transposing tile passes ((300, 100) and (70, 45) partial tiles only, (300, 1) a
+    single column, (4100, 1024) whole tiles and a partial last band)."""
     from oracle import reference as R
     gen = torch.Generator().manual_seed(7)
     p0 = torch.randn(shape, generator=gen) * .02
