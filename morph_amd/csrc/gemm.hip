@@ -55,11 +55,15 @@
 // issued in batches ahead of their use so the epilogue pays memory latency a
 // few times, not per element.
 //
-// The [K, N] kernel (X' = B' X) passes the Q fragment as the MFMA's first
-// operand: its accumulators are then row chunks of C (register r of lane l holds
-// C[l % 32][8 (r / 4) + 4 (l / 32) + r % 4]; both fragment shapes are "a row of 8
-// consecutive k"), so its C leaves the LDS tile with 64-bit writes instead of
-// 2-byte ones (epilogue_rows); sustained over the whole chain, 0.7% faster.
+// The [K, N] kernel (X' = B' X) and the diagonal-add kernel (B' = c A A + b A +
+// a I) pass the Q fragment as the MFMA's first operand: their accumulators are
+// then row chunks of C (register r of lane l holds C[l % 32][8 (r / 4) +
+// 4 (l / 32) + r % 4]; both fragment shapes are "a row of 8 consecutive k"), so
+// C and D move through the LDS tile with 64-bit accesses instead of 2-byte ones
+// and the mirror tile leaves through transposing LDS reads (epilogue_rows).
+// Sustained over the whole chain: 0.7% faster for X', then 0.4% more for B'
+// (whose kernel also spills no registers this way: 0 against 14).  The same
+// change in the A = X X^T kernel measured even (36.10 against 36.12 ms).
 //
 // Each epilogue variant (D or not, alpha multiply or not, diagonal add or not)
 // is a kernel of its own, chosen on the host: a kernel holding every variant
@@ -308,11 +312,11 @@ __device__ __forceinline__ void store_tile_t(const uint16_t* E, uint16_t* dst, u
 // 8 (r / 4) + 4 fh + r % 4), four consecutive columns of a row per group of four
 // registers, so D and C move through the row-major LDS tile with one 64-bit access
 // per four values (T, the transposed copy, with transposing reads).
-template <int kDMode, bool kScaled>
+template <int kDMode, bool kScaled, bool kDiag = false>
 __device__ __forceinline__ void epilogue_rows(const GemmArgs& g, float alpha, float beta,
                                               f32x16 (&acc)[4][4], uint16_t* smem,
                                               const uint16_t* D, uint16_t* C, uint16_t* T,
-                                              int64_t ldt) {
+                                              int64_t ldt, bool diag_tile = false) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
   const int fr = lane & 31, fh = lane >> 5;
@@ -356,6 +360,14 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& g, float alpha, fl
           const u32x2 v = draw[j][r >> 2];
           const uint32_t w = (r & 2) ? v.y : v.x;
           x[r] = __fmaf_rn(beta, bf16_bits_to_float((r & 1) ? (w >> 16) : (w & 0xFFFFu)), x[r]);
+        }
+      }
+      if constexpr (kDiag) {
+        // element (wr + 32 i + fr, wc + 32 j + 8 (r / 4) + 4 fh + r % 4) is diagonal
+        if (diag_tile && i == j && wr == wc) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (fr == 8 * (r >> 2) + 4 * fh + (r & 3)) x[r] = x[r] + g.diag;
         }
       }
 #pragma unroll
@@ -489,7 +501,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
   };
   auto mfma = [&](int n, const Frags& f) {
     const int i = n >> 2, j = n & 3;
-    if constexpr (kQKN)  // row-chunk accumulators (epilogue_rows)
+    if constexpr (kQKN || kDiag)  // row-chunk accumulators (epilogue_rows)
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.q[j], f.a[i], acc[i][j], 0, 0, 0);
     else
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.q[j], acc[i][j], 0, 0, 0);
@@ -652,6 +664,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
   // diagonal add or not); only a diagonal tile of a symmetric product takes the add.
   if constexpr (kQKN)
     epilogue_rows<kDMode, kScaled>(g, alpha, beta, acc, smem, D, C, T, ldt);
+  else if constexpr (kDiag)
+    epilogue_rows<kDMode, kScaled, true>(g, alpha, beta, acc, smem, D, C, T, ldt, tr == tc);
   else if (kDiag && tr == tc)
     epilogue<kDMode, kScaled, true>(g, alpha, beta, acc, smem, D, C, T, ldt);
   else
