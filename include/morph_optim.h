@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 6
+#define MORPH_ABI_VERSION 7
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -461,6 +461,17 @@ int morph_muon_newton_schulz(int count, int64_t rows, int64_t cols, const morph_
 int morph_muon_finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
                       const morph_muon_hp* hp, int orthogonalize_only, void* workspace,
                       size_t workspace_bytes, void* stream);
+/*
+ * finish for matrices first .. first + n - 1 of the batch only (mats and count
+ * as given to prepare): a caller that stages the parameters in and out of
+ * device memory can update each matrix as soon as it has arrived and send it
+ * back while the next ones arrive.  Calls over disjoint ranges that together
+ * cover the batch equal one morph_muon_finish.  0 <= first, 0 <= n,
+ * first + n <= count.
+ */
+int morph_muon_finish_range(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+                            const morph_muon_hp* hp, int orthogonalize_only, int first, int n,
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -561,12 +561,14 @@ bool stored_is_x(const morph_muon_matrix& m, int64_t rows, int64_t cols) {
 
 enum class Orient { kAll, kStored, kTransposed };
 
-// The batch's matrices of one orientation (kAll: every one), in batch order; *n = how many.
+// The batch's matrices of one orientation (kAll: every one) among positions
+// first .. last - 1, in batch order; *n = how many.
 MatPtrs pointers(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
-                 Orient which, int* n) {
+                 Orient which, int* n, int first = 0, int last = -1) {
   MatPtrs m;
   int k = 0;
-  for (int i = 0; i < count; ++i) {
+  if (last < 0) last = count;
+  for (int i = first; i < last; ++i) {
     if (which != Orient::kAll && stored_is_x(mats[i], rows, cols) != (which == Orient::kStored))
       continue;
     m.grad[k] = mats[i].grad;
@@ -664,16 +666,20 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
 
 int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
            const morph_muon_hp* hp, void* workspace, size_t workspace_bytes, bool orth_only,
-           void* stream) {
+           void* stream, int first = 0, int n = -1) {
+  if (n < 0) n = count;
+  if (first < 0 || first > count || n > count - first) return MORPH_EINVAL;
   Bufs W;
   int rc = setup(mats, count, rows, cols, hp, workspace, workspace_bytes, true, false, &W);
-  if (rc || count == 0) return rc;
+  if (rc || n == 0) return rc;
   const Layout& L = W.L;
   const uint16_t* x = W.X[hp->ns_steps & 1];  // the buffer the last iteration wrote
   hipStream_t s = as_stream(stream);
   int n_flat, n_tiled;
-  const MatPtrs flat = pointers(mats, count, rows, cols, Orient::kStored, &n_flat);
-  const MatPtrs tiled = pointers(mats, count, rows, cols, Orient::kTransposed, &n_tiled);
+  const MatPtrs flat = pointers(mats, count, rows, cols, Orient::kStored, &n_flat, first,
+                                first + n);
+  const MatPtrs tiled = pointers(mats, count, rows, cols, Orient::kTransposed, &n_tiled, first,
+                                 first + n);
   const float sn = hp->update_scale, st = hp->update_scale_transposed;
   if (n_flat) {
     const dim3 ew((unsigned)((L.numel + kFlatApply * 4 - 1) / (kFlatApply * 4)), n_flat);
@@ -718,6 +724,14 @@ extern "C" int morph_muon_finish(const morph_muon_matrix* mats, int count, int64
                                  void* workspace, size_t workspace_bytes, void* stream) {
   return finish(mats, count, rows, cols, hp, workspace, workspace_bytes, orthogonalize_only != 0,
                 stream);
+}
+
+extern "C" int morph_muon_finish_range(const morph_muon_matrix* mats, int count, int64_t rows,
+                                       int64_t cols, const morph_muon_hp* hp,
+                                       int orthogonalize_only, int first, int n, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  return finish(mats, count, rows, cols, hp, workspace, workspace_bytes, orthogonalize_only != 0,
+                stream, first, n);
 }
 
 extern "C" int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t rows,

@@ -172,13 +172,22 @@ def _prepare(mats, rows, cols, hp, orth_only, stream, workspaces, found_inf=None
     return batches
 
 
-def _complete(batches, stream, timer=None, before_finish=None):
+def _finish_range(batch, first, n, stream):
+    """The parameter update (or U into param) of matrices first .. first + n - 1 of a
+    batch _prepare enqueued."""
+    arr, count, rows, cols, hp, orth_only, ws = batch
+    check(lib().morph_muon_finish_range(arr, count, rows, cols, ctypes.byref(hp), int(orth_only),
+                                        first, n, ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                        stream_handle(stream)))
+
+
+def _complete(batches, stream, timer=None, finish=None):
     """Newton-Schulz chains, then the finish of every batch _prepare enqueued.
 
     timer: optional list; (start_event, end_event, dense flops, executed flops) around
-    each NS chain.  before_finish: optional callable run on the host once every
-    chain is enqueued and before the first finish (the pass that reads and writes
-    the parameters) is.
+    each NS chain.  finish: optional callable(batches, stream) run once every chain is
+    enqueued, in place of the finish passes (it enqueues them itself, e.g. per
+    matrix as the parameters arrive, with _finish_range).
     """
     L = lib()
     sh = stream_handle(stream)
@@ -193,8 +202,9 @@ def _complete(batches, stream, timer=None, before_finish=None):
             e1.record(s)
             timer.append((e0, e1, ns_flops(rows, cols, count, hp.ns_steps),
                           ns_executed_flops(rows, cols, count, hp.ns_steps)))
-    if before_finish is not None:
-        before_finish()
+    if finish is not None:
+        finish(batches, stream)
+        return
     for arr, count, rows, cols, hp, orth_only, ws in batches:
         check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), int(orth_only),
                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), sh))
@@ -229,7 +239,7 @@ def orthogonalize(gradients, steps=NS_STEPS, stream=None, workspaces=_WORKSPACES
 
 def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=None,
               workspaces=_WORKSPACES, timer=None, momenta_out=None, found_inf=None, gate=None,
-              before_finish=None):
+              finish=None):
     """The Muon loop body of optimizer.py:55-61 for every (param, grad, momentum) triple.
 
     In place on params and momenta.  Scalars follow the reference: decay
@@ -238,9 +248,9 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
     (momenta are then only read).  found_inf: optional device flag set when a
     gradient is non-finite, tested in the momentum pass.  gate: optional
     callable run after that pass and before anything the caller keeps is
-    mutated (with momenta_out); it may raise to drop the step.  before_finish:
-    optional callable run once the Newton-Schulz chains are enqueued, before the
-    parameter update is (the params are not read before it).
+    mutated (with momenta_out); it may raise to drop the step.  finish: optional
+    callable(batches, stream) that enqueues the parameter updates itself once the
+    Newton-Schulz chains are enqueued (the params are not read before that).
     """
     items = []
     outs = momenta_out if momenta_out is not None else [None] * len(params)
@@ -262,7 +272,7 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
                             first=len(batches))
     if gate is not None:
         gate()
-    _complete(batches, stream, timer, before_finish)
+    _complete(batches, stream, timer, finish)
 
 
 def _host_grad(p):
@@ -315,7 +325,11 @@ class HybridMuonAdamW:
                     raise ValueError("Muon masters must be contiguous 2-D float32 tensors")
             dev = torch.device("cuda", torch.cuda.current_device())
             shapes = [p.shape for p in self.muon]
-            self._muon_masters = HostStaging(shapes, torch.float32, dev)
+            sizes = {p.numel() for p in self.muon}
+            # one matrix per staging chunk when they are all the same size, so each
+            # can be updated as soon as it is on the device (_streamed_finish)
+            chunk = sizes.pop() if len(sizes) == 1 else 1 << 22
+            self._muon_masters = HostStaging(shapes, torch.float32, dev, chunk_elements=chunk)
             self._muon_grads = HostStaging(shapes, torch.float32, dev)
             self._muon_dev = self._muon_masters.views
         else:
@@ -355,18 +369,14 @@ class HybridMuonAdamW:
         if not live and not adam_present:
             return
         idx = [i for i, _ in live]
-        upload_masters = None
+        finish = None
         if self.host:
             device = self._muon_dev[0].device if self.muon else self.adam.device
             if live:
                 self._muon_grads.upload([_host_grad(p) for _, p in live], idx)
-                # Only the update reads the masters: they cross PCIe while the
-                # Newton-Schulz chain runs.  Nothing queued touches the mirrors
-                # (the last step's write-back has finished), so the copy stream
-                # need not wait for the chain; the update waits for the copy.
                 masters = [p for _, p in live]
                 self._muon_masters._check(masters, idx)  # fail before anything is enqueued
-                upload_masters = (lambda: self._muon_masters.upload(masters, idx, wait=False))
+                finish = self._streamed_finish(masters, idx)
             muon_grads = [self._muon_grads.views[i] for i in idx]
             adam_grads = (self.adam._stage_in([p.grad for p in adam_params], adam_present)
                           if adam_present else None)
@@ -394,7 +404,7 @@ class HybridMuonAdamW:
                       [self.momentum[i] for i in idx], self.lr, self.weight_decay,
                       workspaces=self._workspaces, timer=self.ns_timer,
                       momenta_out=[self._momentum_next[i] for i in idx],
-                      found_inf=self._flag, gate=gate, before_finish=upload_masters)
+                      found_inf=self._flag, gate=gate, finish=finish)
             for i in idx:
                 self.momentum[i], self._momentum_next[i] = self._momentum_next[i], self.momentum[i]
         else:
@@ -406,8 +416,36 @@ class HybridMuonAdamW:
             self.adam._stage_out(adam_present)
         else:
             self.adam.step()
-        if self.host and live:
-            self._muon_masters.download([p.data for _, p in live], idx)
+
+    def _streamed_finish(self, masters, idx):
+        """The finish of a step with CPU masters.  Only the update reads the masters,
+        so they cross PCIe while the Newton-Schulz chains run: nothing queued touches
+        the mirrors (the last step's write-back has finished), so the uploads need not
+        wait for the chains.  When every staging chunk holds whole matrices, each
+        matrix is updated as soon as it has arrived and sent back while the next ones
+        arrive; otherwise all are uploaded, updated and sent back in turn."""
+        staging = self._muon_masters
+
+        def run(batches, stream):
+            if staging.whole_tensor_chunks(idx):
+                where = {}
+                for b, batch in enumerate(batches):
+                    arr, count = batch[0], batch[1]
+                    for j in range(count):
+                        where[arr[j].param] = (b, j)
+
+                def launch(lo, hi, pieces, st):
+                    for i, _, _ in pieces:
+                        b, j = where[self._muon_dev[i].data_ptr()]
+                        _finish_range(batches[b], j, 1, st)
+
+                staging.pipeline(masters, idx, launch, stream, wait=False)
+            else:
+                staging.upload(masters, idx, stream, wait=False)
+                for batch in batches:
+                    _finish_range(batch, 0, batch[1], stream)
+                staging.download([p.data for p in masters], idx, stream)
+        return run
 
     def state_dict(self):
         """{momentum, adam, lr, weight_decay} as optimizer.py:64-65.  The momentum

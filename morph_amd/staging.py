@@ -15,6 +15,8 @@ device pass: chunk k goes up while chunk k - 1 comes back, on one copy stream
 per direction (PCIe carries both directions at once: 88 GB/s together against
 56 GB/s either way alone, measured on MI355X).
 """
+import collections
+
 import torch
 
 ALIGN = 64  # elements of 4 bytes: mirrors start 256-byte aligned
@@ -34,7 +36,7 @@ class HostStaging:
     device side ordered before later work on `stream`.
     """
 
-    _LAG = 2  # pipeline(): chunks between a chunk's download and its copy out
+    _DOWN_BUFFERS = 3  # pipeline(): pinned buffers (downloads in flight) on the way back
 
     def __init__(self, shapes, dtype, device, chunk_elements=1 << 22):
         self.device = torch.device(device)
@@ -164,15 +166,19 @@ class HostStaging:
                 fetch(k + 2)  # this buffer is free again
         stream.wait_stream(self._copy)
 
-    def pipeline(self, tensors, which, launch, stream=None):
+    def pipeline(self, tensors, which, launch, stream=None, wait=True):
         """Per chunk of the listed mirrors: upload it from the host tensors, run
         launch(lo, hi, pieces, stream) (device work on those elements, enqueued on
-        `stream`), then download it back into the same host tensors.  Chunk k + 1
-        goes up while chunk k comes back.  Ordered after the work already queued on
-        `stream`; returns with every host tensor updated, later work on `stream`
-        ordered after the downloads.  pieces: (index, start, end) of each listed
-        tensor's elements in the chunk.  The host copies chunk k - 2 out of its
-        pinned buffer while chunk k goes up, so it rarely waits for a download."""
+        `stream`), then download it back into the same host tensors.  Uploads go
+        ahead as fast as the link takes them; each chunk comes back (one of
+        _DOWN_BUFFERS pinned buffers, a second copy stream) once its launch has run,
+        and the host copies finished downloads out between uploads, so chunks go
+        up and come back at the same time.  Returns with every host tensor
+        updated, later work on `stream` ordered after the downloads.  wait=False:
+        the uploads do not wait for the work already queued on `stream` (for a
+        caller that knows none of it touches these mirrors; the launches still
+        follow it).  pieces: (index, start, end) of each listed tensor's elements
+        in the chunk."""
         which = list(which)
         tensors = list(tensors)
         self._check(tensors, which)
@@ -181,19 +187,40 @@ class HostStaging:
         if self._copy_down is None:
             self._copy_down = torch.cuda.Stream(self.device)
         if self._pinned_down is None:
-            self._pinned_down = self._new_buffers(self._LAG + 1)
-        up, down = self._buffers(), self._pinned_down
-        self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
+            self._pinned_down = self._new_buffers(self._DOWN_BUFFERS)
+        up = self._buffers()
+        free = list(self._pinned_down)
+        if wait:
+            self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
         size = self.flat.element_size()
+        launched = collections.deque()   # chunks whose download is not enqueued yet
+        inflight = collections.deque()   # downloads not copied out yet
 
-        def copy_out(k, lo, hi, pieces):
-            slot = down[k % len(down)]
-            slot["event"].synchronize()  # this chunk's download has landed
+        def copy_out(item):
+            lo, hi, pieces, slot = item
+            slot["event"].synchronize()
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
                 host[i][s:e].copy_(slot["buf"][at:at + e - s])
+            free.append(slot)
 
-        pending = []
+        def service(block):
+            done = False
+            while inflight and inflight[0][3]["event"].query():
+                copy_out(inflight.popleft())
+                done = True
+            if block and not done and inflight:
+                copy_out(inflight.popleft())
+            while launched and free:
+                lo, hi, pieces = launched.popleft()
+                slot = free.pop(0)
+                self._copy_down.wait_stream(stream)  # after this chunk's launch
+                with torch.cuda.stream(self._copy_down):
+                    slot["buf"][:hi - lo].copy_(self.flat[lo:hi], non_blocking=True)
+                    slot["event"].record(self._copy_down)
+                self.bytes_d2h += (hi - lo) * size
+                inflight.append((lo, hi, pieces, slot))
+
         for k, (lo, hi, pieces) in enumerate(self._chunks(which)):
             slot = up[k % 2]
             slot["event"].synchronize()  # the upload that last read this buffer is done
@@ -206,18 +233,15 @@ class HostStaging:
             self.bytes_h2d += (hi - lo) * size
             stream.wait_stream(self._copy)
             launch(lo, hi, pieces, stream)
-            # down[k % (LAG + 1)] last held chunk k - LAG - 1, copied out already
-            dslot = down[k % len(down)]
-            self._copy_down.wait_stream(stream)
-            with torch.cuda.stream(self._copy_down):
-                dslot["buf"][:hi - lo].copy_(self.flat[lo:hi], non_blocking=True)
-                dslot["event"].record(self._copy_down)
-            self.bytes_d2h += (hi - lo) * size
-            pending.append((k, lo, hi, pieces))
-            if len(pending) > self._LAG:
-                copy_out(*pending.pop(0))
-        for item in pending:
-            copy_out(*item)
+            launched.append((lo, hi, pieces))
+            service(block=False)
+        while launched or inflight:
+            service(block=True)
         for slot in up:
             slot["event"].synchronize()  # the caller may change the host tensors on return
         stream.wait_stream(self._copy_down)
+
+    def whole_tensor_chunks(self, which):
+        """True when every chunk of the listed mirrors holds whole tensors only."""
+        return all(s == 0 and e == self.numels[i]
+                   for _, _, pieces in self._chunks(which) for i, s, e in pieces)

@@ -177,6 +177,44 @@ def test_hybrid_on_cpu_masters_through_the_runner_sequence():
         assert torch.equal(p, q), n
 
 
+class Uneven(nn.Module):
+    """Hidden Linear layers of different sizes (one not a multiple of 64 elements)."""
+
+    def __init__(self):
+        super().__init__()
+        self.a = nn.Linear(64, 192, bias=False)
+        self.b = nn.Linear(192, 70, bias=False)
+        self.c = nn.Linear(70, 33, bias=True)
+        self.lm_head = nn.Linear(33, 16, bias=False)
+
+
+@pytest.mark.parametrize("model_cls", [Tiny, Uneven])
+def test_hybrid_on_cpu_masters_equals_device_masters(model_cls):
+    """Per-matrix streamed updates (each staging chunk one whole matrix, updated as it
+    arrives) and the whole-batch fallback (uneven sizes, 5000-element chunks that cut
+    matrices) both equal the device-resident optimizer bit for bit over three steps,
+    masters and momenta."""
+    torch.manual_seed(4)
+    cpu_model = model_cls()
+    dev_model = copy.deepcopy(cpu_model).to(DEV)
+    opt_c = HybridMuonAdamW(cpu_model, lr=.003, muon_lr=.02)
+    opt_d = HybridMuonAdamW(dev_model, lr=.003, muon_lr=.02)
+    idx = list(range(len(opt_c.muon)))
+    if model_cls is Uneven:
+        opt_c._muon_masters.chunk = 5000
+    assert opt_c._muon_masters.whole_tensor_chunks(idx) == (model_cls is Tiny)
+    for step in range(3):
+        _engine_grads(cpu_model, 10 + step)
+        for (_, pc), (_, pd) in zip(cpu_model.named_parameters(), dev_model.named_parameters()):
+            pd.grad = pc.grad.to(DEV)
+        opt_c.step()
+        opt_d.step()
+    for (n, pc), (_, pd) in zip(cpu_model.named_parameters(), dev_model.named_parameters()):
+        assert torch.equal(pc.detach(), pd.detach().cpu()), n
+    for i, m in opt_d.momentum.items():
+        assert torch.equal(opt_c.momentum[i].cpu(), m.cpu()), i
+
+
 @pytest.mark.parametrize("poisoned", ["norm.weight", "up.weight", "down.weight"])
 def test_hybrid_on_cpu_masters_raises_before_any_mutation(poisoned):
     torch.manual_seed(1)
