@@ -754,14 +754,17 @@ def embedding_main(args):
     print(json.dumps(line), flush=True)
 
 
-def time_streamed(steps, warmup, muon=False):
+def time_streamed(steps, warmup, muon=False, pinned=False):
     """The streamed engines' layout (runner.py:41-46, engine.py:75-88): FP32 masters and
     FP32 (already unscaled) gradients in pageable CPU memory, optimizer state resident in
     HBM.  A step uploads every gradient and master through pinned staging, runs the
     device step on the mirrors, and writes the masters back into the CPU tensors before
     step() returns (morph_amd.staging).  muon=False: FusedAdamW over the config-2 window;
-    muon=True: HybridMuonAdamW over config 5 (42 matrices + the AdamW vectors)."""
-    from morph_amd import FusedAdamW
+    muon=True: HybridMuonAdamW over config 5 (42 matrices + the AdamW vectors).
+    pinned=True: the masters are moved into page-locked memory first (pin_host_tensors),
+    so they cross PCIe by DMA alone; the gradients stay pageable, as the engine leaves
+    them."""
+    from morph_amd import FusedAdamW, pin_host_tensors
     from morph_amd.muon import HybridMuonAdamW
     cpus = host_cpus()  # the host copies run on torch's intra-op threads
     if muon:
@@ -769,6 +772,8 @@ def time_streamed(steps, warmup, muon=False):
         gen = torch.Generator().manual_seed(6)
         for p in model.parameters():
             p.grad = torch.randn(p.shape, generator=gen) * 1e-3
+        if pinned:
+            pin_host_tensors(model.parameters())
         opt = HybridMuonAdamW(model, lr=3e-4, muon_lr=0.02)
         params = list(model.parameters())
         stagings = [opt._muon_masters, opt._muon_grads, opt.adam._staging]
@@ -776,6 +781,8 @@ def time_streamed(steps, warmup, muon=False):
         params = [torch.nn.Parameter(m) for m in config2_window("cpu")]
         for p, g in zip(params, config2_grads("cpu", 1000)):
             p.grad = g.float() / LOSS_SCALE
+        if pinned:
+            pin_host_tensors(params)
         opt = FusedAdamW(params, **HYPER)
         stagings = [opt._staging]
     for _ in range(warmup):
@@ -798,7 +805,7 @@ def time_streamed(steps, warmup, muon=False):
 
 
 def streamed_main(args, muon=False):
-    r = time_streamed(args.steps, args.warmup, muon)
+    r = time_streamed(args.steps, args.warmup, muon, args.pinned)
     n, t = r["n"], r["elapsed"] / args.steps
     line = {
         "metric": ("HybridMuonAdamW step" if muon else "AdamW step") + " with CPU FP32 masters "
@@ -808,10 +815,12 @@ def streamed_main(args, muon=False):
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": ("config 5 (42 x [3072, 6144] Muon + 326 AdamW vectors)" if muon
                                 else "config-2 window (N = 56,623,104)") +
-                               " with FP32 masters and FP32 gradients in pageable CPU memory; "
+                               (" with FP32 masters in pinned and FP32 gradients in pageable CPU "
+                                "memory (pin_host_tensors); " if args.pinned else
+                                " with FP32 masters and FP32 gradients in pageable CPU memory; ") +
                                "state resident in HBM; step = upload gradients and masters, "
                                "device step, masters back into the CPU tensors",
-                   "params": n},
+                   "params": n, "masters": "pinned" if args.pinned else "pageable"},
         "pcie": {"h2d_bytes_per_step": int(r["h2d"]), "d2h_bytes_per_step": int(r["d2h"]),
                  "h2d_plus_d2h_gb_per_s": round((r["h2d"] + r["d2h"]) / t / 1e9, 2),
                  "host_threads": r["cpus"]["threads"]},
@@ -984,6 +993,9 @@ def main():
                          "grads: the stage-gradient window; window: the HBM-resident [3, N] "
                          "state; fp8: block-scaled FP8 transport encoding; streamed / "
                          "streamed_muon: config 2 / config 5 with CPU FP32 masters, PCIe included")
+    ap.add_argument("--pinned", action="store_true",
+                    help="streamed / streamed_muon: masters in page-locked host memory "
+                         "(pin_host_tensors), moved by DMA alone")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()

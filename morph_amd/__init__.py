@@ -6,5 +6,6 @@ requires the built library (python -m morph_amd.build) and GPU tensors.
 """
 from .precision import DynamicLossScale
 from .optimizer import FusedAdamW
+from .staging import pin_host_tensors
 
-__all__ = ["DynamicLossScale", "FusedAdamW"]
+__all__ = ["DynamicLossScale", "FusedAdamW", "pin_host_tensors"]

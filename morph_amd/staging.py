@@ -10,7 +10,10 @@ mirror of each host tensor (each at a 256-byte aligned offset) and moves data
 between the host tensors and the mirrors in chunks through two pinned buffers
 per direction, so the host-side copy of one chunk (pageable <-> pinned, torch's
 multi-threaded copy) overlaps the DMA of the other.  Tensors whose mirrors are
-adjacent travel in one DMA per chunk.  pipeline() streams chunks through a
+adjacent travel in one DMA per chunk.  A host tensor that is already in
+page-locked memory (pin_host_tensors, or a caller's own pinned allocation) is
+reached by the DMA directly: its chunks skip the pinned buffers and the host
+copy, which bounds the pageable transfers (about 72 GB/s of host memcpy).  pipeline() streams chunks through a
 device pass: chunk k goes up while chunk k - 1 comes back, on one copy stream
 per direction (PCIe carries both directions at once: 88 GB/s together against
 56 GB/s either way alone, measured on MI355X).
@@ -24,6 +27,30 @@ ALIGN = 64  # elements of 4 bytes: mirrors start 256-byte aligned
 
 def _align(x):
     return (x + ALIGN - 1) // ALIGN * ALIGN
+
+
+def pin_host_tensors(tensors):
+    """Move the data of CPU tensors (e.g. a streamed model's FP32 master parameters) into
+    page-locked host memory in place: t.data becomes a pinned copy, so every reference
+    to the tensor (a module's Parameter, an optimizer's parameter list) sees it.  The
+    staging of the optimizers then moves these tensors by DMA alone.  Tensors already
+    pinned are left alone.  Two distinct tensors that share storage cannot both be moved
+    without losing the sharing, so that raises ValueError before anything is moved.
+    Returns the number of bytes moved."""
+    tensors = [t for t in tensors if t.device.type == "cpu"]
+    owners = {}
+    for t in tensors:
+        key = t.untyped_storage().data_ptr()
+        if key in owners and owners[key] is not t:
+            raise ValueError("two tensors share host storage; pin the storage's owner instead")
+        owners[key] = t
+    moved = 0
+    for t in owners.values():
+        if t.is_pinned():
+            continue
+        t.data = t.data.pin_memory()
+        moved += t.numel() * t.element_size()
+    return moved
 
 
 class HostStaging:
@@ -106,6 +133,29 @@ class HostStaging:
             if not t.is_contiguous():
                 raise ValueError(f"host tensor {i} must be contiguous")
 
+    @staticmethod
+    def _pinned_of(host):
+        """Indices of the host tensors in page-locked memory (DMA reaches them directly)."""
+        return {i for i, t in host.items() if t.is_pinned()}
+
+    @staticmethod
+    def _direct(pieces, pinned):
+        return all(i in pinned for i, _, _ in pieces)
+
+    def _up_direct(self, pieces, host):
+        """DMA of each piece from its pinned host tensor (on the current stream)."""
+        for i, s, e in pieces:
+            at = self.offsets[i] + s
+            self.flat[at:at + e - s].copy_(host[i][s:e], non_blocking=True)
+            self.bytes_h2d += (e - s) * self.flat.element_size()
+
+    def _down_direct(self, pieces, host):
+        """DMA of each piece into its pinned host tensor (on the current stream)."""
+        for i, s, e in pieces:
+            at = self.offsets[i] + s
+            host[i][s:e].copy_(self.flat[at:at + e - s], non_blocking=True)
+            self.bytes_d2h += (e - s) * self.flat.element_size()
+
     def upload(self, tensors, which=None, stream=None, wait=True):
         """views[which[k]] <- tensors[k] (host, contiguous).
 
@@ -116,12 +166,20 @@ class HostStaging:
         tensors = list(tensors)
         self._check(tensors, which)
         src = {i: t.detach().reshape(-1) for i, t in zip(which, tensors)}
+        pinned = self._pinned_of(src)
         stream = stream or torch.cuda.current_stream(self.device)
         if wait:
             self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
-        bufs = self._buffers()
-        for k, (lo, hi, pieces) in enumerate(self._chunks(which)):
-            slot = bufs[k % 2]
+        bufs = None
+        staged = 0
+        for lo, hi, pieces in self._chunks(which):
+            if self._direct(pieces, pinned):
+                with torch.cuda.stream(self._copy):
+                    self._up_direct(pieces, src)
+                continue
+            bufs = bufs or self._buffers()
+            slot = bufs[staged % 2]
+            staged += 1
             slot["event"].synchronize()  # the DMA that last read this buffer is done
             buf = slot["buf"]
             for i, s, e in pieces:
@@ -132,8 +190,11 @@ class HostStaging:
                 slot["event"].record(self._copy)
             self.bytes_h2d += (hi - lo) * self.flat.element_size()
         stream.wait_stream(self._copy)
-        for slot in bufs:
-            slot["event"].synchronize()  # the caller may change the host tensors on return
+        # the caller may change the host tensors on return
+        if pinned:
+            self._copy.synchronize()
+        for slot in bufs or ():
+            slot["event"].synchronize()
 
     def download(self, tensors, which=None, stream=None):
         """tensors[k] (host, contiguous) <- views[which[k]], after the work queued on `stream`."""
@@ -141,10 +202,17 @@ class HostStaging:
         tensors = list(tensors)
         self._check(tensors, which)
         dst = {i: t.detach().view(-1) for i, t in zip(which, tensors)}
+        pinned = self._pinned_of(dst)
         stream = stream or torch.cuda.current_stream(self.device)
         self._copy.wait_stream(stream)
-        bufs = self._buffers()
-        chunks = self._chunks(which)
+        chunks = []
+        for lo, hi, pieces in self._chunks(which):
+            if self._direct(pieces, pinned):
+                with torch.cuda.stream(self._copy):
+                    self._down_direct(pieces, dst)
+            else:
+                chunks.append((lo, hi, pieces))
+        bufs = self._buffers() if chunks else []
 
         def fetch(k):
             lo, hi, _ = chunks[k]
@@ -164,6 +232,8 @@ class HostStaging:
                 dst[i][s:e].copy_(slot["buf"][at:at + e - s])
             if k + 2 < len(chunks):
                 fetch(k + 2)  # this buffer is free again
+        if pinned:
+            self._copy.synchronize()  # the host tensors hold the data on return
         stream.wait_stream(self._copy)
 
     def pipeline(self, tensors, which, launch, stream=None, wait=True):
@@ -183,13 +253,16 @@ class HostStaging:
         tensors = list(tensors)
         self._check(tensors, which)
         host = {i: t.detach().view(-1) for i, t in zip(which, tensors)}
+        pinned = self._pinned_of(host)
         stream = stream or torch.cuda.current_stream(self.device)
         if self._copy_down is None:
             self._copy_down = torch.cuda.Stream(self.device)
-        if self._pinned_down is None:
+        chunks = self._chunks(which)
+        staged_chunks = sum(not self._direct(pieces, pinned) for _, _, pieces in chunks)
+        if staged_chunks and self._pinned_down is None:
             self._pinned_down = self._new_buffers(self._DOWN_BUFFERS)
-        up = self._buffers()
-        free = list(self._pinned_down)
+        up = self._buffers() if staged_chunks else []
+        free = list(self._pinned_down) if staged_chunks else []
         if wait:
             self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
         size = self.flat.element_size()
@@ -221,8 +294,21 @@ class HostStaging:
                 self.bytes_d2h += (hi - lo) * size
                 inflight.append((lo, hi, pieces, slot))
 
-        for k, (lo, hi, pieces) in enumerate(self._chunks(which)):
-            slot = up[k % 2]
+        staged = 0
+        for lo, hi, pieces in chunks:
+            if self._direct(pieces, pinned):
+                # pinned host tensors: DMA up, the launch, DMA back, nothing for the host
+                with torch.cuda.stream(self._copy):
+                    self._up_direct(pieces, host)
+                stream.wait_stream(self._copy)
+                launch(lo, hi, pieces, stream)
+                self._copy_down.wait_stream(stream)
+                with torch.cuda.stream(self._copy_down):
+                    self._down_direct(pieces, host)
+                service(block=False)
+                continue
+            slot = up[staged % 2]
+            staged += 1
             slot["event"].synchronize()  # the upload that last read this buffer is done
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
@@ -239,6 +325,8 @@ class HostStaging:
             service(block=True)
         for slot in up:
             slot["event"].synchronize()  # the caller may change the host tensors on return
+        if pinned:
+            self._copy_down.synchronize()  # the direct downloads have landed
         stream.wait_stream(self._copy_down)
 
     def whole_tensor_chunks(self, which):

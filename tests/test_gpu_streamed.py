@@ -14,7 +14,9 @@ same calls run with the state resident in HBM (morph_amd.staging):
     device-resident optimizer fed the same gradients, state_dict on the CPU and a
     save/restore that continues identically;
   * the non-finite gate: raise with CPU masters, momenta and moments untouched;
-  * HostStaging round trips with small chunks, subsets and odd sizes.
+  * HostStaging round trips with small chunks, subsets and odd sizes, with pageable,
+    pinned (direct DMA) and mixed host tensors; pinned masters (pin_host_tensors) give
+    the same bits as pageable ones through both optimizers.
 """
 import copy
 
@@ -23,7 +25,7 @@ import pytest
 import torch
 from torch import nn
 
-from morph_amd import FusedAdamW
+from morph_amd import FusedAdamW, pin_host_tensors
 from morph_amd.muon import HybridMuonAdamW
 from morph_amd.staging import HostStaging
 from tests.golden.make_golden import CONFIG1, config1_inputs
@@ -33,39 +35,98 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 
 
-def test_host_staging_round_trips():
+def _pin(pin, tensors):
+    """Pinned copies of all, every other or none of the tensors."""
+    return [t.pin_memory() if pin == "all" or (pin == "some" and k % 2) else t
+            for k, t in enumerate(tensors)]
+
+
+@pytest.mark.parametrize("pin", ["none", "all", "some"])
+def test_host_staging_round_trips(pin):
     gen = torch.Generator().manual_seed(1)
     shapes = [(7,), (1000, 3), (1,), (64, 65), (4099,)]
     st = HostStaging(shapes, torch.float32, DEV, chunk_elements=1000)
-    host = [torch.randn(s, generator=gen) for s in shapes]
+    host = _pin(pin, [torch.randn(s, generator=gen) for s in shapes])
     st.upload(host)
     for h, v in zip(host, st.views):
         assert torch.equal(v.cpu(), h)
     # a subset: only those mirrors change, chunks span tensor boundaries
-    new = [torch.randn(shapes[i], generator=gen) for i in (1, 3)]
+    new = _pin(pin, [torch.randn(shapes[i], generator=gen) for i in (1, 3)])
     st.upload(new, [1, 3])
     for i, v in enumerate(st.views):
         expect = {1: new[0], 3: new[1]}.get(i, host[i])
         assert torch.equal(v.cpu(), expect), i
-    out = [torch.empty(s) for s in shapes]
+    out = _pin(pin, [torch.empty(s) for s in shapes])
     st.download(out)
     for o, v in zip(out, st.views):
         assert torch.equal(o, v.cpu())
     st.views[2].fill_(5.0)
-    one = [torch.zeros(1)]
+    one = _pin(pin, [torch.zeros(1)])
     st.download(one, [2])
     assert float(one[0]) == 5.0
+    assert st.bytes_h2d > 0 and st.bytes_d2h > 0
 
 
-@pytest.mark.parametrize("chunk", [None, 5000])
-def test_fused_adamw_on_cpu_masters_config1(chunk):
+@pytest.mark.parametrize("pin", ["none", "all", "some"])
+def test_host_staging_pipeline_updates_every_chunk(pin):
+    """pipeline(): every listed tensor goes up, through the launch (x -> 2 x + 1 on the
+    device, per chunk) and back into the same host tensor; unlisted mirrors untouched."""
+    gen = torch.Generator().manual_seed(2)
+    shapes = [(300,), (64, 65), (1,), (2000,), (77, 3)]
+    st = HostStaging(shapes, torch.float32, DEV, chunk_elements=512)
+    host = _pin(pin, [torch.randn(s, generator=gen) for s in shapes])
+    before = [h.clone() for h in host]
+    st.upload(host)
+    st.views[2].fill_(9.0)
+    which = [0, 1, 3, 4]
+    seen = []
+
+    def launch(lo, hi, pieces, stream):
+        seen.extend(i for i, _, _ in pieces)
+        with torch.cuda.stream(stream):
+            for i, s, e in pieces:
+                v = st.views[i].view(-1)[s:e]
+                v.mul_(2.0).add_(1.0)
+
+    st.pipeline([host[i] for i in which], which, launch)
+    assert sorted(set(seen)) == which
+    for i in which:
+        assert torch.equal(host[i], before[i] * 2.0 + 1.0), i
+        assert torch.equal(st.views[i].cpu(), host[i]), i
+    assert torch.equal(host[2], before[2]) and float(st.views[2]) == 9.0
+
+
+def test_pin_host_tensors_moves_data_in_place():
+    gen = torch.Generator().manual_seed(3)
+    lin = nn.Linear(16, 8)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(8, 16, generator=gen))
+    w0, b0 = lin.weight.detach().clone(), lin.bias.detach().clone()
+    moved = pin_host_tensors(lin.parameters())
+    assert moved == (8 * 16 + 8) * 4
+    assert lin.weight.is_pinned() and lin.bias.is_pinned()
+    assert isinstance(lin.weight, nn.Parameter)
+    assert torch.equal(lin.weight.detach(), w0) and torch.equal(lin.bias.detach(), b0)
+    assert pin_host_tensors(lin.parameters()) == 0  # already pinned
+    base = torch.zeros(10)
+    with pytest.raises(ValueError, match="share host storage"):
+        pin_host_tensors([base[:5], base[5:]])
+    assert not base.is_pinned()
+
+
+@pytest.mark.parametrize("chunk,pinned", [(None, False), (5000, False), (None, True),
+                                          (5000, True)])
+def test_fused_adamw_on_cpu_masters_config1(chunk, pinned):
     """BASELINE config 1 (param groups: wd .1 on 2-D only) with CPU masters and CPU FP32
     gradients: every step bit-exact against the oracle and against device masters.  With
     chunk=5000 the masters stream through the update in 60 chunks, most spanning two
-    tensors at offsets that are not multiples of 64."""
+    tensors at offsets that are not multiples of 64.  pinned: the masters live in
+    page-locked memory (pin_host_tensors) and move by DMA alone."""
     from oracle import reference as R
     masters, grads = config1_inputs()
     cpu = [m.clone() for m in masters]
+    if pinned:
+        pin_host_tensors(cpu)
     dev = [m.to(DEV) for m in masters]
     groups = lambda ps: [dict(params=[p for p in ps if p.ndim == 2], weight_decay=CONFIG1["wd_2d"]),
                          dict(params=[p for p in ps if p.ndim == 1], weight_decay=0.0)]
@@ -188,15 +249,18 @@ class Uneven(nn.Module):
         self.lm_head = nn.Linear(33, 16, bias=False)
 
 
-@pytest.mark.parametrize("model_cls", [Tiny, Uneven])
-def test_hybrid_on_cpu_masters_equals_device_masters(model_cls):
+@pytest.mark.parametrize("model_cls,pinned", [(Tiny, False), (Uneven, False), (Tiny, True),
+                                              (Uneven, True)])
+def test_hybrid_on_cpu_masters_equals_device_masters(model_cls, pinned):
     """Per-matrix streamed updates (each staging chunk one whole matrix, updated as it
     arrives) and the whole-batch fallback (uneven sizes, 5000-element chunks that cut
     matrices) both equal the device-resident optimizer bit for bit over three steps,
-    masters and momenta."""
+    masters and momenta, with pageable and with pinned (pin_host_tensors) masters."""
     torch.manual_seed(4)
     cpu_model = model_cls()
     dev_model = copy.deepcopy(cpu_model).to(DEV)
+    if pinned:
+        pin_host_tensors(cpu_model.parameters())
     opt_c = HybridMuonAdamW(cpu_model, lr=.003, muon_lr=.02)
     opt_d = HybridMuonAdamW(dev_model, lr=.003, muon_lr=.02)
     idx = list(range(len(opt_c.muon)))
