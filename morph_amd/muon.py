@@ -101,6 +101,11 @@ class Workspaces:
         entry["streams"].add(stream)
         return entry["buf"]
 
+    def note_stream(self, stream):
+        """Record that `stream` uses the workspaces too (kept alive for its queued work)."""
+        for entry in self._ws.values():
+            entry["streams"].add(stream)
+
 
 _WORKSPACES = Workspaces()  # for the free functions; each HybridMuonAdamW owns its own
 
@@ -181,13 +186,11 @@ def _finish_range(batch, first, n, stream):
                                         stream_handle(stream)))
 
 
-def _complete(batches, stream, timer=None, finish=None):
-    """Newton-Schulz chains, then the finish of every batch _prepare enqueued.
+def _chains(batches, stream, timer=None):
+    """The Newton-Schulz chain of every batch _prepare enqueued.
 
     timer: optional list; (start_event, end_event, dense flops, executed flops) around
-    each NS chain.  finish: optional callable(batches, stream) run once every chain is
-    enqueued, in place of the finish passes (it enqueues them itself, e.g. per
-    matrix as the parameters arrive, with _finish_range).
+    each NS chain.
     """
     L = lib()
     sh = stream_handle(stream)
@@ -202,9 +205,13 @@ def _complete(batches, stream, timer=None, finish=None):
             e1.record(s)
             timer.append((e0, e1, ns_flops(rows, cols, count, hp.ns_steps),
                           ns_executed_flops(rows, cols, count, hp.ns_steps)))
-    if finish is not None:
-        finish(batches, stream)
-        return
+
+
+def _complete(batches, stream, timer=None):
+    """Newton-Schulz chains, then the finish of every batch _prepare enqueued."""
+    _chains(batches, stream, timer)
+    L = lib()
+    sh = stream_handle(stream)
     for arr, count, rows, cols, hp, orth_only, ws in batches:
         check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), int(orth_only),
                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), sh))
@@ -237,21 +244,16 @@ def orthogonalize(gradients, steps=NS_STEPS, stream=None, workspaces=_WORKSPACES
     return outs[0] if single else outs
 
 
-def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=None,
-              workspaces=_WORKSPACES, timer=None, momenta_out=None, found_inf=None, gate=None,
-              finish=None):
-    """The Muon loop body of optimizer.py:55-61 for every (param, grad, momentum) triple.
+def _step_hp(rows, cols, lr, weight_decay, steps=NS_STEPS):
+    """Constants of one Muon step for the [rows, cols] batch (optimizer.py:60-61): decay
+    1 - lr * weight_decay, alpha -lr, update scale sqrt(max(1, rows / cols)) and, for the
+    transposed members, sqrt(max(1, cols / rows))."""
+    return _hp(update_scale=max(1, rows / cols) ** .5, decay=1 - lr * weight_decay,
+               neg_lr=-lr, steps=steps, update_scale_transposed=max(1, cols / rows) ** .5)
 
-    In place on params and momenta.  Scalars follow the reference: decay
-    1 - lr * weight_decay, update scale sqrt(max(1, rows / cols)), alpha -lr.
-    momenta_out: optional separate buffers that receive the updated momenta
-    (momenta are then only read).  found_inf: optional device flag set when a
-    gradient is non-finite, tested in the momentum pass.  gate: optional
-    callable run after that pass and before anything the caller keeps is
-    mutated (with momenta_out); it may raise to drop the step.  finish: optional
-    callable(batches, stream) that enqueues the parameter updates itself once the
-    Newton-Schulz chains are enqueued (the params are not read before that).
-    """
+
+def _check_items(params, grads, momenta, momenta_out):
+    """(param, grad, momentum, momentum_out) tuples, validated."""
     items = []
     outs = momenta_out if momenta_out is not None else [None] * len(params)
     for p, g, m, mo in zip(params, grads, momenta, outs):
@@ -264,15 +266,29 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
             if mo.shape != m.shape or mo.data_ptr() == m.data_ptr():
                 raise ValueError("momentum_out must be a separate buffer of the momentum's shape")
         items.append((p, g, m, mo))
+    return items
+
+
+def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=None,
+              workspaces=_WORKSPACES, timer=None, momenta_out=None, found_inf=None, gate=None):
+    """The Muon loop body of optimizer.py:55-61 for every (param, grad, momentum) triple.
+
+    In place on params and momenta.  Scalars follow the reference: decay
+    1 - lr * weight_decay, update scale sqrt(max(1, rows / cols)), alpha -lr.
+    momenta_out: optional separate buffers that receive the updated momenta
+    (momenta are then only read).  found_inf: optional device flag set when a
+    gradient is non-finite, tested in the momentum pass.  gate: optional
+    callable run after that pass and before anything the caller keeps is
+    mutated (with momenta_out); it may raise to drop the step.
+    """
+    items = _check_items(params, grads, momenta, momenta_out)
     batches = []
     for (rows, cols), group in _by_shape(items).items():
-        hp = _hp(update_scale=max(1, rows / cols) ** .5, decay=1 - lr * weight_decay,
-                 neg_lr=-lr, steps=steps, update_scale_transposed=max(1, cols / rows) ** .5)
-        batches += _prepare(group, rows, cols, hp, False, stream, workspaces, found_inf,
-                            first=len(batches))
+        batches += _prepare(group, rows, cols, _step_hp(rows, cols, lr, weight_decay, steps),
+                            False, stream, workspaces, found_inf, first=len(batches))
     if gate is not None:
         gate()
-    _complete(batches, stream, timer, finish)
+    _complete(batches, stream, timer)
 
 
 def _host_grad(p):
@@ -327,7 +343,7 @@ class HybridMuonAdamW:
             shapes = [p.shape for p in self.muon]
             sizes = {p.numel() for p in self.muon}
             # one matrix per staging chunk when they are all the same size, so each
-            # can be updated as soon as it is on the device (_streamed_finish)
+            # can be updated as soon as it is on the device (_host_step)
             chunk = sizes.pop() if len(sizes) == 1 else 1 << 22
             self._muon_masters = HostStaging(shapes, torch.float32, dev, chunk_elements=chunk)
             self._muon_grads = HostStaging(shapes, torch.float32, dev)
@@ -335,6 +351,12 @@ class HybridMuonAdamW:
         else:
             self._muon_dev = list(self.muon)
         self.ns_timer = None  # optional list: HIP events around each Newton-Schulz chain
+        # CPU masters: the Muon matrices go through the step in this many parts
+        # (uploads, momentum pass and Newton-Schulz chain per part), so that the
+        # first parts' chains run while later gradients cross PCIe and their
+        # updated masters come back while later masters go up
+        self.stream_parts = 2
+        self._ns_stream = None
         self._workspaces = Workspaces()
         self.lr = lr if muon_lr is None else muon_lr
         self.weight_decay = weight_decay
@@ -361,25 +383,20 @@ class HybridMuonAdamW:
         """The gate of optimizer.py:49-51 covers every gradient: the AdamW group's
         by the detector, the Muon matrices' inside their momentum pass (which
         writes only scratch buffers until the gate has passed).  With CPU masters
-        every gradient and master is uploaded before the gate, and nothing is
-        written back to the CPU until it has passed."""
+        every gradient is uploaded before the gate, and the masters go up and
+        come back only after it has passed (_host_step)."""
         live = [(i, p) for i, p in enumerate(self.muon) if p.grad is not None]
         adam_params = [p for g in (self.adam.param_groups if self.adam else []) for p in g["params"]]
         adam_present = [k for k, p in enumerate(adam_params) if p.grad is not None]
         if not live and not adam_present:
             return
         idx = [i for i, _ in live]
-        finish = None
+        if self.host and live:
+            return self._host_step(live, idx, adam_params, adam_present)
         if self.host:
-            device = self._muon_dev[0].device if self.muon else self.adam.device
-            if live:
-                self._muon_grads.upload([_host_grad(p) for _, p in live], idx)
-                masters = [p for _, p in live]
-                self._muon_masters._check(masters, idx)  # fail before anything is enqueued
-                finish = self._streamed_finish(masters, idx)
-            muon_grads = [self._muon_grads.views[i] for i in idx]
-            adam_grads = (self.adam._stage_in([p.grad for p in adam_params], adam_present)
-                          if adam_present else None)
+            device = self.adam.device
+            muon_grads = []
+            adam_grads = self.adam._stage_in([p.grad for p in adam_params], adam_present)
         else:
             device = (live[0][1] if live else adam_params[adam_present[0]]).device
             muon_grads = [p.grad for _, p in live]
@@ -395,57 +412,141 @@ class HybridMuonAdamW:
                 raise FloatingPointError('nonfinite gradient; optimizer not updated')
 
         if live:
-            for i in idx:
-                if i not in self.momentum:
-                    self.momentum[i] = torch.zeros_like(self._muon_dev[i])
-                if i not in self._momentum_next:
-                    self._momentum_next[i] = torch.empty_like(self._muon_dev[i])
+            self._ensure_momenta(idx)
             muon_step([self._muon_dev[i] for i in idx], muon_grads,
                       [self.momentum[i] for i in idx], self.lr, self.weight_decay,
                       workspaces=self._workspaces, timer=self.ns_timer,
                       momenta_out=[self._momentum_next[i] for i in idx],
-                      found_inf=self._flag, gate=gate, finish=finish)
-            for i in idx:
-                self.momentum[i], self._momentum_next[i] = self._momentum_next[i], self.momentum[i]
+                      found_inf=self._flag, gate=gate)
+            self._swap_momenta(idx)
         else:
             gate()
+        self._adam_after_gate(adam_grads, adam_present)
+
+    def _ensure_momenta(self, idx):
+        for i in idx:
+            if i not in self.momentum:
+                self.momentum[i] = torch.zeros_like(self._muon_dev[i])
+            if i not in self._momentum_next:
+                self._momentum_next[i] = torch.empty_like(self._muon_dev[i])
+
+    def _swap_momenta(self, idx):
+        for i in idx:
+            self.momentum[i], self._momentum_next[i] = self._momentum_next[i], self.momentum[i]
+
+    def _adam_after_gate(self, adam_grads, adam_present):
         if not adam_present:
-            pass
-        elif self.host:
+            return
+        if self.host:
             self.adam._enqueue(adam_grads, adam_present, None, False)
             self.adam._stage_out(adam_present)
         else:
             self.adam.step()
 
-    def _streamed_finish(self, masters, idx):
-        """The finish of a step with CPU masters.  Only the update reads the masters,
-        so they cross PCIe while the Newton-Schulz chains run: nothing queued touches
-        the mirrors (the last step's write-back has finished), so the uploads need not
-        wait for the chains.  When every staging chunk holds whole matrices, each
-        matrix is updated as soon as it has arrived and sent back while the next ones
-        arrive; otherwise all are uploaded, updated and sent back in turn."""
+    def _host_step(self, live, idx, adam_params, adam_present):
+        """step() with CPU masters.  The Muon matrices go through in stream_parts
+        parts: each part's gradients go up, then its momentum pass (which writes
+        only scratch buffers and the non-finite flag) and its Newton-Schulz chain
+        are enqueued while the next part's gradients go up; the chains run on a
+        second stream, so that a part's updates wait only for its own chain.
+        Once every gradient has passed the gate (optimizer.py:49-51), the masters
+        stream through the updates: each matrix goes up, is updated as soon as it
+        and its part's chain are done (morph_muon_finish_range) and comes back
+        while the next ones go up.  Returns with the new masters in the CPU
+        tensors."""
+        device = self._muon_dev[0].device
+        stream = torch.cuda.current_stream(device)
+        masters = [p for _, p in live]
+        grads = [_host_grad(p) for _, p in live]
+        self._muon_masters._check(masters, idx)  # fail before anything is enqueued
+        self._ensure_momenta(idx)
+        if self._flag is None:
+            self._flag = kernels.new_flag(device)
+        if self._ns_stream is None:
+            self._ns_stream = torch.cuda.Stream(device)
+        ns = self._ns_stream
+        kernels.flag_clear(self._flag, stream)
+        parts = []
+        try:
+            self._host_step_on(live, idx, masters, grads, adam_params, adam_present, stream, ns,
+                               parts)
+        except BaseException:
+            # The chains already ran, possibly on non-finite values, which turn the
+            # workspaces' zero padding into NaN (0 * inf): restore it, after them, so
+            # the next step starts from the state the kernels rely on.
+            stream.wait_stream(ns)
+            for batches in parts:
+                for batch in batches:
+                    batch[-1].zero_()
+            raise
+        finally:
+            # later work on `stream` (the next step's momentum pass) follows the chains
+            stream.wait_stream(ns)
+
+    def _host_step_on(self, live, idx, masters, grads, adam_params, adam_present, stream, ns,
+                      parts):
+        nparts = max(1, min(int(self.stream_parts), len(live)))
+        bounds = [len(live) * k // nparts for k in range(nparts + 1)]
+        ready, nbatch = [], 0
+        for k in range(nparts):
+            pos = range(bounds[k], bounds[k + 1])
+            part = [idx[j] for j in pos]
+            # wait=False: nothing queued reads the gradient mirrors (the last step's
+            # momentum passes finished before its masters came back)
+            self._muon_grads.upload([grads[j] for j in pos], part, stream, wait=False)
+            items = [(self._muon_dev[i], self._muon_grads.views[i], self.momentum[i],
+                      self._momentum_next[i]) for i in part]
+            batches = []
+            for (rows, cols), group in _by_shape(items).items():
+                batches += _prepare(group, rows, cols,
+                                    _step_hp(rows, cols, self.lr, self.weight_decay), False,
+                                    stream, self._workspaces, self._flag,
+                                    first=nbatch + len(batches))
+            nbatch += len(batches)
+            ns.wait_stream(stream)
+            self._workspaces.note_stream(ns)
+            parts.append(batches)
+            _chains(batches, ns, self.ns_timer)
+            done = torch.cuda.Event()
+            done.record(ns)
+            ready.append(done)
+        adam_grads = (self.adam._stage_in([p.grad for p in adam_params], adam_present)
+                      if adam_present else None)
+        if adam_present:
+            kernels.nonfinite_or([adam_grads[k] for k in adam_present], self._flag)
+        if self._flag.item():
+            raise FloatingPointError('nonfinite gradient; optimizer not updated')
+        where = {}
+        for k, batches in enumerate(parts):
+            for b, batch in enumerate(batches):
+                arr, count = batch[0], batch[1]
+                for j in range(count):
+                    where[arr[j].param] = (k, b, j)
         staging = self._muon_masters
+        waited = set()
 
-        def run(batches, stream):
-            if staging.whole_tensor_chunks(idx):
-                where = {}
-                for b, batch in enumerate(batches):
-                    arr, count = batch[0], batch[1]
-                    for j in range(count):
-                        where[arr[j].param] = (b, j)
+        def after_chain(k, st):
+            if k not in waited:
+                st.wait_event(ready[k])
+                waited.add(k)
 
-                def launch(lo, hi, pieces, st):
-                    for i, _, _ in pieces:
-                        b, j = where[self._muon_dev[i].data_ptr()]
-                        _finish_range(batches[b], j, 1, st)
+        if staging.whole_tensor_chunks(idx):
+            def launch(lo, hi, pieces, st):
+                for i, _, _ in pieces:
+                    k, b, j = where[self._muon_dev[i].data_ptr()]
+                    after_chain(k, st)
+                    _finish_range(parts[k][b], j, 1, st)
 
-                staging.pipeline(masters, idx, launch, stream, wait=False)
-            else:
-                staging.upload(masters, idx, stream, wait=False)
+            staging.pipeline(masters, idx, launch, stream, wait=False)
+        else:
+            staging.upload(masters, idx, stream, wait=False)
+            for k, batches in enumerate(parts):
+                after_chain(k, stream)
                 for batch in batches:
                     _finish_range(batch, 0, batch[1], stream)
-                staging.download([p.data for p in masters], idx, stream)
-        return run
+            staging.download([p.data for p in masters], idx, stream)
+        self._swap_momenta(idx)
+        self._adam_after_gate(adam_grads, adam_present)
 
     def state_dict(self):
         """{momentum, adam, lr, weight_decay} as optimizer.py:64-65.  The momentum

@@ -249,19 +249,23 @@ class Uneven(nn.Module):
         self.lm_head = nn.Linear(33, 16, bias=False)
 
 
-@pytest.mark.parametrize("model_cls,pinned", [(Tiny, False), (Uneven, False), (Tiny, True),
-                                              (Uneven, True)])
-def test_hybrid_on_cpu_masters_equals_device_masters(model_cls, pinned):
+@pytest.mark.parametrize("model_cls,pinned,parts", [(Tiny, False, 2), (Uneven, False, 2),
+                                                    (Tiny, True, 2), (Uneven, True, 2),
+                                                    (Tiny, False, 1), (Uneven, False, 3),
+                                                    (Tiny, True, 5)])
+def test_hybrid_on_cpu_masters_equals_device_masters(model_cls, pinned, parts):
     """Per-matrix streamed updates (each staging chunk one whole matrix, updated as it
     arrives) and the whole-batch fallback (uneven sizes, 5000-element chunks that cut
     matrices) both equal the device-resident optimizer bit for bit over three steps,
-    masters and momenta, with pageable and with pinned (pin_host_tensors) masters."""
+    masters and momenta, with pageable and with pinned (pin_host_tensors) masters, and
+    with the matrices in 1, 2, 3 or more parts (more parts than matrices: one each)."""
     torch.manual_seed(4)
     cpu_model = model_cls()
     dev_model = copy.deepcopy(cpu_model).to(DEV)
     if pinned:
         pin_host_tensors(cpu_model.parameters())
     opt_c = HybridMuonAdamW(cpu_model, lr=.003, muon_lr=.02)
+    opt_c.stream_parts = parts
     opt_d = HybridMuonAdamW(dev_model, lr=.003, muon_lr=.02)
     idx = list(range(len(opt_c.muon)))
     if model_cls is Uneven:
