@@ -4,20 +4,28 @@
 //   unpack: y = dtype(float(byte) * scale)
 // following streamtrain/precision.py:24-37 (pack_fp8 / unpack_fp8, used for
 // the opt-in FP8 weight transfer of disk.py:330-345).  The reference computes
-// with torch ops; the arithmetic here is the same sequence of FP32 operations
-// (IEEE division, one rounding each) so the bytes and scales are identical.
+// with torch ops in FP32 (IEEE division, one rounding each); the bytes and
+// scales here are identical.  The scale is the same IEEE division; each
+// element's quotient is the IEEE division for FP32 inputs, and for FP16/BF16
+// inputs Markstein's correction of the product with the block's reciprocal
+// (pack_kernel), checked exhaustively against the division.
 //
 // E4M3FN: 1 sign, 4 exponent (bias 7), 3 mantissa bits; no infinities, NaN =
 // S.1111.111, largest finite 448, smallest subnormal 2^-9.  The conversion is
-// round to nearest even, written from the format definition: normal results
-// round the FP32 bit pattern at mantissa bit 20 (a carry moves into the
-// exponent), subnormal results are rint(|x| * 2^9); NaN stays NaN.  Inputs
-// here are already clamped to +-448, so the out-of-range case only arises for
-// NaN.  Torch propagates NaN through amax, clamp_min and clamp, so a block
-// with a NaN has a NaN scale and all-NaN bytes; that is reproduced too.
+// round to nearest even; e4m3fn_from_float writes it from the format
+// definition: normal results round the FP32 bit pattern at mantissa bit 20 (a
+// carry moves into the exponent), subnormal results are rint(|x| * 2^9); NaN
+// stays NaN.  The pack encodes with gfx950's v_cvt_pk_fp8_f32, which gives the
+// same bytes for every non-NaN input in range (all FP32 bit patterns compared
+// on the device), and uses e4m3fn_from_float for NaN.  Inputs here are already
+// clamped to +-448, so the out-of-range case only arises for NaN.  Torch
+// propagates NaN through amax, clamp_min and clamp, so a block with a NaN has
+// a NaN scale and all-NaN bytes; that is reproduced too.
 //
 // One wave per block: 64 lanes x 4 elements = 256 (the block size); the amax
 // is a butterfly over the wave.  A workgroup holds 4 waves / 4 blocks.
+#include <type_traits>
+
 #include "common.h"
 
 namespace morph {
@@ -108,13 +116,41 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__
   float s = m / 448.0f;
   s = (s < 1e-30f) ? 1e-30f : s;  // clamp_min keeps NaN
   if (lane == 0) scales[blk] = s;
-  uint32_t word = 0;
+  float q[4];
+  // FP32 inputs, and blocks holding an infinity (s = inf: x / s is 0, or NaN for the
+  // infinities themselves), take the IEEE division; the branch is wave-uniform.
+  if (std::is_same_v<IT, F32> || __builtin_isinf(s)) {
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    float q = x[k] / s;
-    q = is_nan(q) ? q : (q < -448.0f ? -448.0f : (q > 448.0f ? 448.0f : q));
-    word |= e4m3fn_from_float(q) << (8 * k);
+    for (int k = 0; k < 4; ++k) q[k] = x[k] / s;
+  } else {
+    // 16-bit inputs, finite scale (NaN propagates either way): x / s by
+    // Markstein's correction of |x| * (1 / s) -- one IEEE division per lane instead
+    // of one per element -- with x's sign put back (so -0 stays -0, as in the
+    // division).  q = RN(|x| y), r = |x| - q s (exact by the fma), q' = RN(q + r y).
+    // Checked against the IEEE quotient for every finite FP16 and BF16 block
+    // maximum and every element up to it: FP16 quotients are identical; BF16 ones
+    // differ only for subnormal elements, whose quotients (below 2^-13) encode as
+    // zero either way.
+    const float y = 1.0f / s;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float ax = __builtin_fabsf(x[k]);
+      const float t = ax * y;
+      const float r = __fmaf_rn(-t, s, ax);
+      q[k] = __builtin_copysignf(__fmaf_rn(r, y, t), x[k]);
+    }
   }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    q[k] = is_nan(q[k]) ? q[k] : (q[k] < -448.0f ? -448.0f : (q[k] > 448.0f ? 448.0f : q[k]));
+  // v_cvt_pk_fp8_f32 is gfx950's OCP E4M3 conversion, round to nearest even: equal to
+  // e4m3fn_from_float for every non-NaN FP32 input in [-448, 448] (all 2^32 bit
+  // patterns were compared on the device); NaN keeps the format rule's encoding.
+  uint32_t word = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+  word = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], (int)word, true);
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    if (is_nan(q[k])) word = (word & ~(0xFFu << (8 * k))) | (e4m3fn_from_float(q[k]) << (8 * k));
   if (i + 4 <= n && ((reinterpret_cast<uintptr_t>(bytes) + i) & 3) == 0) {
     *reinterpret_cast<uint32_t*>(bytes + i) = word;
   } else {

@@ -1,8 +1,8 @@
 """GPU FP8 block-scaled pack/unpack (morph_amd.fp8) against the oracle (precision.py:24-37).
 
 Bytes and scales bit-exact for FP32/FP16/BF16 inputs, ragged sizes and wide dynamic
-range (subnormal codes); an exhaustive conversion sweep over every finite FP16 value
-with |v| <= 448 at scale 1; zero and NaN blocks; unpack of all 256 codes at several
+range (subnormal codes); exhaustive conversion sweeps over every finite FP16 value and
+every FP32 value with |v| <= 448 at scale 1; zero and NaN blocks; unpack of all 256 codes at several
 scales into FP16/BF16/FP32; the reference's 4% roundtrip bound.
 """
 import numpy as np
@@ -49,6 +49,45 @@ def test_conversion_exhaustive_over_fp16_values():
     enc, sc = fp8.pack_fp8(x.to(DEV))
     assert torch.equal(sc.cpu(), torch.ones_like(sc.cpu()))
     assert torch.equal(enc.cpu(), x.to(torch.float8_e4m3fn).view(torch.uint8))
+
+
+def test_conversion_every_fp32_value_in_range():
+    """Every FP32 value in [-448, 448] (both signs of all 1,138,753,537 magnitudes up to
+    448) in blocks led by 448, so the scale is 1 and the bytes are the plain E4M3FN
+    conversion of each value (the kernel converts with gfx950's v_cvt_pk_fp8_f32),
+    against torch's conversion on the GPU, which is checked against torch's CPU
+    conversion on a sample."""
+    top = 0x43E00000  # bits of 448.0
+    sample = torch.randint(0, top + 1, (1 << 20,), generator=torch.Generator().manual_seed(9),
+                           dtype=torch.int32).view(torch.float32)
+    assert torch.equal(sample.to(DEV).to(torch.float8_e4m3fn).view(torch.uint8).cpu(),
+                       sample.to(torch.float8_e4m3fn).view(torch.uint8))
+    step = 255 << 19
+    for lo in range(0, top + 1, step):
+        x = torch.arange(lo, min(lo + step, top + 1), dtype=torch.int32, device=DEV).view(torch.float32)
+        x = torch.cat([x, torch.zeros((-x.numel()) % 255, device=DEV)]).view(-1, 255)
+        for sign in (1.0, -1.0):
+            blocks = torch.cat([torch.full((x.shape[0], 1), 448.0, device=DEV), x * sign], 1).view(-1)
+            enc, sc = fp8.pack_fp8(blocks)
+            assert bool((sc == 1.0).all())
+            assert torch.equal(enc, blocks.to(torch.float8_e4m3fn).view(torch.uint8)), (lo, sign)
+        del x, blocks, enc, sc
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_blocks_with_infinities(dtype):
+    """A block holding +-inf has scale inf: its finite elements encode as +-0 and the
+    infinities as NaN (inf / inf), as the reference's division gives; -0 in a finite
+    block stays -0."""
+    x = torch.randn(1024, generator=torch.Generator().manual_seed(3))
+    x[5], x[300], x[301], x[700] = float("inf"), float("-inf"), float("inf"), float("nan")
+    x[800], x[801] = -0.0, 0.0  # signed zeros in a finite block keep their sign
+    x = x.to(dtype)
+    enc, sc = fp8.pack_fp8(x.to(DEV))
+    renc, rsc = R.pack_fp8_torch(x)
+    assert same(sc, rsc) and same(enc, renc)
+    assert torch.isinf(sc[0].cpu()) and torch.isinf(sc[1].cpu()) and torch.isnan(sc[2].cpu())
+    assert enc[800].item() == 0x80 and enc[801].item() == 0
 
 
 def test_zero_and_nan_blocks():
