@@ -463,7 +463,8 @@ class HybridMuonAdamW:
         if self._flag is None:
             self._flag = kernels.new_flag(device)
         if self._ns_stream is None:
-            self._ns_stream = torch.cuda.Stream(device)
+            from .staging import shared_stream
+            self._ns_stream = shared_stream(device, "side")
         ns = self._ns_stream
         kernels.flag_clear(self._flag, stream)
         parts = []
