@@ -24,6 +24,7 @@ import torch
 
 from . import kernels
 from .hyper import disk_constants
+from .staging import shared_stream
 
 
 class _Staging:
@@ -60,7 +61,7 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
     hp = disk_constants(step=step, lr=lr, clip=clip)
     chunk = min(chunk_elements, max(size, 1))
     compute = torch.cuda.current_stream(device)
-    copy_in = torch.cuda.Stream(device)
+    copy_in = shared_stream(device, "up")  # one copy stream per device (HW queues)
     slots = [_Staging(chunk, device) for _ in range(2)]
     # The staging tensors come from the caching allocator on the compute stream, which may hand
     # out memory whose last reader is still queued there, and a device gradient may still be in

@@ -36,6 +36,7 @@ import torch
 from . import kernels
 from ._lib import check, dtype_code, lib, stream_handle
 from .hyper import disk_constants
+from .staging import shared_stream
 
 
 def _fsync(path):
@@ -80,7 +81,7 @@ class ResidentWindow:
         self.timing = dict(file_read=0.0, d2h_wait=0.0, file_write=0.0, fsync=0.0)  # seconds
         self.kernel_timer = None  # optional list: (start, end) HIP events around each update launch
         self.dispatch_timer = None  # optional kernels.DispatchTimer: stamps each update launch
-        self._copy = torch.cuda.Stream(self.device)
+        self._copy = shared_stream(self.device, "up")  # one copy stream per device (HW queues)
         self._staging = None
         self.dropped_on_error = set()  # dropped by a failed update(); ahead of their files
 
