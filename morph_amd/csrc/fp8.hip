@@ -23,7 +23,7 @@
 // a NaN scale and all-NaN bytes; that is reproduced too.
 //
 // One wave per block: 64 lanes x 4 elements = 256 (the block size); the amax
-// is a butterfly over the wave.  A workgroup holds 4 waves / 4 blocks.
+// is a reduction over the wave (wave_max_bits).  A workgroup holds 4 waves / 4 blocks.
 #include <type_traits>
 
 #include "common.h"
@@ -38,9 +38,21 @@ static_assert(kBlockElems == 256, "one wave x 4 elements per block");
 
 __device__ __forceinline__ bool is_nan(float x) { return x != x; }
 
-// torch.amax: NaN if any element is NaN
-__device__ __forceinline__ float nan_max(float a, float b) {
-  return (is_nan(a) || is_nan(b)) ? __builtin_nanf("") : (a > b ? a : b);
+// torch.amax of |x| over the wave: the bit patterns of non-negative floats order
+// like the values, and every NaN pattern (above 0x7F800000) above +inf, so an
+// unsigned maximum of |x|'s bits is the amax, NaN if any element is NaN.
+// Within each row of 16 lanes by DPP (quad swaps, half-row and row mirrors),
+// then across rows with gfx950's v_permlane16_swap and v_permlane32_swap; no
+// LDS round trips.
+__device__ __forceinline__ uint32_t wave_max_bits(uint32_t x) {
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false));  // row_mirror
+  const auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = max((uint32_t)r16[0], (uint32_t)r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return max((uint32_t)r32[0], (uint32_t)r32[1]);
 }
 
 __device__ __forceinline__ uint32_t e4m3fn_from_float(float x) {
@@ -109,10 +121,9 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__
   const int64_t i = blk * kBlockElems + lane * 4;
   float x[4];
   load4<IT>(src, i, n, x);
-  float m = nan_max(nan_max(__builtin_fabsf(x[0]), __builtin_fabsf(x[1])),
-                    nan_max(__builtin_fabsf(x[2]), __builtin_fabsf(x[3])));
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = nan_max(m, __shfl_xor(m, o));
+  auto mag = [](float v) { return __builtin_bit_cast(uint32_t, v) & 0x7FFFFFFFu; };
+  const float m = __builtin_bit_cast(
+      float, wave_max_bits(max(max(mag(x[0]), mag(x[1])), max(mag(x[2]), mag(x[3])))));
   float s = m / 448.0f;
   s = (s < 1e-30f) ? 1e-30f : s;  // clamp_min keeps NaN
   if (lane == 0) scales[blk] = s;
