@@ -16,7 +16,8 @@ same calls run with the state resident in HBM (morph_amd.staging):
   * the non-finite gate: raise with CPU masters, momenta and moments untouched;
   * HostStaging round trips with small chunks, subsets and odd sizes, with pageable,
     pinned (direct DMA) and mixed host tensors; pinned masters (pin_host_tensors) give
-    the same bits as pageable ones through both optimizers.
+    the same bits as pageable ones through both optimizers;
+  * two optimizers interleaved over the shared per-device copy and side streams.
 """
 import copy
 
@@ -281,6 +282,32 @@ def test_hybrid_on_cpu_masters_equals_device_masters(model_cls, pinned, parts):
         assert torch.equal(pc.detach(), pd.detach().cpu()), n
     for i, m in opt_d.momentum.items():
         assert torch.equal(opt_c.momentum[i].cpu(), m.cpu()), i
+
+
+def test_optimizers_sharing_the_copy_streams_interleave():
+    """Every staging object and the Muon side stream use one stream per role and device
+    (staging.shared_stream).  Two CPU-master optimizers stepped alternately through those
+    shared streams equal device-resident twins bit for bit, masters and momenta."""
+    torch.manual_seed(7)
+    cpu = [Tiny(), Uneven()]
+    dev = [copy.deepcopy(m).to(DEV) for m in cpu]
+    opt_c = [HybridMuonAdamW(m, lr=.003, muon_lr=.02) for m in cpu]
+    opt_d = [HybridMuonAdamW(m, lr=.003, muon_lr=.02) for m in dev]
+    assert opt_c[0]._muon_masters._copy is opt_c[1]._muon_grads._copy
+    assert opt_c[0]._muon_masters._copy is opt_c[1].adam._staging._copy
+    for step in range(3):
+        for k, (cm, dm) in enumerate(zip(cpu, dev)):
+            _engine_grads(cm, 20 + 10 * k + step)
+            for (_, pc), (_, pd) in zip(cm.named_parameters(), dm.named_parameters()):
+                pd.grad = pc.grad.to(DEV)
+        for o in opt_c + opt_d:
+            o.step()
+    assert opt_c[0]._ns_stream is opt_c[1]._ns_stream
+    for cm, dm, oc, od in zip(cpu, dev, opt_c, opt_d):
+        for (n, pc), (_, pd) in zip(cm.named_parameters(), dm.named_parameters()):
+            assert torch.equal(pc.detach(), pd.detach().cpu()), n
+        for i, m in od.momentum.items():
+            assert torch.equal(oc.momentum[i].cpu(), m.cpu()), i
 
 
 @pytest.mark.parametrize("poisoned", ["norm.weight", "up.weight", "down.weight"])
