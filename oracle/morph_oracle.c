@@ -17,7 +17,8 @@
  *   Tensor.addcdiv_(a, b, value=c)   -> self + (c * a) / b
  *   Tensor / python_float            -> true division by (float)scalar
  *   Tensor.mul_(python_float)        -> self * (float)scalar
- *   Tensor.add_(x, alpha=c)          -> fmaf(x, c, self)   (pinned in tests)
+ *   Tensor.add_(x, alpha=c)          -> fmaf(x, c, self)   (pinned by
+ *                                       tests/test_oracle_muon.py, the Muon update)
  */
 #include <math.h>
 #include <stdint.h>
