@@ -754,7 +754,7 @@ def embedding_main(args):
     print(json.dumps(line), flush=True)
 
 
-def time_streamed(steps, warmup, muon=False, pinned=False):
+def time_streamed(steps, warmup, muon=False, pinned=False, resident=False):
     """The streamed engines' layout (runner.py:41-46, engine.py:75-88): FP32 masters and
     FP32 (already unscaled) gradients in pageable CPU memory, optimizer state resident in
     HBM.  A step uploads every gradient and master through pinned staging, runs the
@@ -763,7 +763,8 @@ def time_streamed(steps, warmup, muon=False, pinned=False):
     muon=True: HybridMuonAdamW over config 5 (42 matrices + the AdamW vectors).
     pinned=True: the masters are moved into page-locked memory first (pin_host_tensors),
     so they cross PCIe by DMA alone; the gradients stay pageable, as the engine leaves
-    them."""
+    them.  resident=True: the optimizers keep the masters' device mirrors between steps
+    (resident_masters), so only the gradients go up and the masters come back."""
     from morph_amd import FusedAdamW, pin_host_tensors
     from morph_amd.muon import HybridMuonAdamW
     cpus = host_cpus()  # the host copies run on torch's intra-op threads
@@ -774,7 +775,7 @@ def time_streamed(steps, warmup, muon=False, pinned=False):
             p.grad = torch.randn(p.shape, generator=gen) * 1e-3
         if pinned:
             pin_host_tensors(model.parameters())
-        opt = HybridMuonAdamW(model, lr=3e-4, muon_lr=0.02)
+        opt = HybridMuonAdamW(model, lr=3e-4, muon_lr=0.02, resident_masters=resident)
         params = list(model.parameters())
         stagings = [opt._muon_masters, opt._muon_grads, opt.adam._staging]
     else:
@@ -783,7 +784,7 @@ def time_streamed(steps, warmup, muon=False, pinned=False):
             p.grad = g.float() / LOSS_SCALE
         if pinned:
             pin_host_tensors(params)
-        opt = FusedAdamW(params, **HYPER)
+        opt = FusedAdamW(params, **HYPER, resident_masters=resident)
         stagings = [opt._staging]
     for _ in range(warmup):
         opt.step()
@@ -805,7 +806,7 @@ def time_streamed(steps, warmup, muon=False, pinned=False):
 
 
 def streamed_main(args, muon=False):
-    r = time_streamed(args.steps, args.warmup, muon, args.pinned)
+    r = time_streamed(args.steps, args.warmup, muon, args.pinned, args.resident_masters)
     n, t = r["n"], r["elapsed"] / args.steps
     line = {
         "metric": ("HybridMuonAdamW step" if muon else "AdamW step") + " with CPU FP32 masters "
@@ -818,9 +819,13 @@ def streamed_main(args, muon=False):
                                (" with FP32 masters in pinned and FP32 gradients in pageable CPU "
                                 "memory (pin_host_tensors); " if args.pinned else
                                 " with FP32 masters and FP32 gradients in pageable CPU memory; ") +
-                               "state resident in HBM; step = upload gradients and masters, "
-                               "device step, masters back into the CPU tensors",
-                   "params": n, "masters": "pinned" if args.pinned else "pageable"},
+                               "state resident in HBM; step = upload gradients" +
+                               (" (masters' device mirrors kept between steps, "
+                                "resident_masters)" if args.resident_masters else
+                                " and masters") +
+                               ", device step, masters back into the CPU tensors",
+                   "params": n, "masters": "pinned" if args.pinned else "pageable",
+                   "resident_masters": bool(args.resident_masters)},
         "pcie": {"h2d_bytes_per_step": int(r["h2d"]), "d2h_bytes_per_step": int(r["d2h"]),
                  "h2d_plus_d2h_gb_per_s": round((r["h2d"] + r["d2h"]) / t / 1e9, 2),
                  "host_threads": r["cpus"]["threads"]},
@@ -996,6 +1001,9 @@ def main():
     ap.add_argument("--pinned", action="store_true",
                     help="streamed / streamed_muon: masters in page-locked host memory "
                          "(pin_host_tensors), moved by DMA alone")
+    ap.add_argument("--resident-masters", action="store_true",
+                    help="streamed / streamed_muon: keep the masters' device mirrors between "
+                         "steps (resident_masters=True), so only gradients cross PCIe upward")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()

@@ -327,7 +327,8 @@ class HybridMuonAdamW:
     so the engine's next stage load (engine.py:109-115) reads the new weights.
     """
 
-    def __init__(self, model, lr=1e-3, muon_lr=None, weight_decay=.01):
+    def __init__(self, model, lr=1e-3, muon_lr=None, weight_decay=.01, *,
+                 resident_masters=False):
         self.muon, adam = partition(model)
         kinds = {p.device.type for p in self.muon + adam}
         if len(kinds) > 1 or not kinds <= {"cpu", "cuda"}:
@@ -369,8 +370,30 @@ class HybridMuonAdamW:
         # own: the one wait per step is the gate's.  Host mirrors of its step counts
         # refresh on resolve(), which state_dict() and load_state_dict() call.
         self.adam = FusedAdamW(adam, lr=lr, weight_decay=weight_decay, betas=(.9, .95),
-                               sync=False) if adam else None
+                               sync=False, resident_masters=resident_masters) if adam else None
+        # CPU masters: keep the Muon masters' device mirrors as the working copies
+        # between steps (FusedAdamW's resident_masters, same rule)
+        self.resident_masters = bool(resident_masters)
+        self._host_marks = {}  # Muon index -> (storage, version) its mirror holds
         self._flag = None
+
+    def invalidate_masters(self):
+        """resident_masters: upload every master again at its next step (after host
+        writes the parameters' version counters cannot see, e.g. through `p.data`)."""
+        self._host_marks.clear()
+        if self.adam is not None:
+            self.adam.invalidate_masters()
+
+    def _current_muon_masters(self, idx):
+        """The Muon indices whose mirrors still hold their host masters' values; their
+        marks are dropped until the step has written the masters back."""
+        current = set()
+        for i in idx:
+            mark = self._host_marks.pop(i, None)
+            p = self.muon[i]
+            if self.resident_masters and mark == (p.data_ptr(), p._version):
+                current.add(i)
+        return current
 
     def zero_grad(self, set_to_none=True):
         for p in self.muon:
@@ -531,6 +554,7 @@ class HybridMuonAdamW:
                 st.wait_event(ready[k])
                 waited.add(k)
 
+        current = self._current_muon_masters(idx)
         if staging.whole_tensor_chunks(idx):
             def launch(lo, hi, pieces, st):
                 for i, _, _ in pieces:
@@ -538,14 +562,17 @@ class HybridMuonAdamW:
                     after_chain(k, st)
                     _finish_range(parts[k][b], j, 1, st)
 
-            staging.pipeline(masters, idx, launch, stream, wait=False)
+            staging.pipeline(masters, idx, launch, stream, wait=False, current=current)
         else:
-            staging.upload(masters, idx, stream, wait=False)
+            staging.upload(masters, idx, stream, wait=False, current=current)
             for k, batches in enumerate(parts):
                 after_chain(k, stream)
                 for batch in batches:
                     _finish_range(batch, 0, batch[1], stream)
             staging.download([p.data for p in masters], idx, stream)
+        for i in idx:
+            p = self.muon[i]
+            self._host_marks[i] = (p.data_ptr(), p._version)
         self._swap_momenta(idx)
         self._adam_after_gate(adam_grads, adam_present)
 

@@ -70,11 +70,19 @@ class FusedAdamW:
       window holds its state; each parameter's `.data` is moved there (its
       values copied), so views of a parameter taken before construction stop
       aliasing it.  Parameters must be distinct, non-overlapping tensors.
+    resident_masters: CPU masters only.  Keep each master's device mirror as
+      the working copy between steps and upload a master again only when its
+      host tensor may have changed since its last step: a new storage
+      (`p.data` rebound) or a bumped version counter (an in-place op on the
+      parameter itself, as optimizer steps and `model.load_state_dict` make).
+      Writes the counter cannot see -- through `p.data`, a NumPy view or raw
+      memory -- must be followed by invalidate_masters().  Each step then moves
+      the masters one way (down) instead of both.
     """
 
     def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2, *,
                  loss_scale=None, export_dtype=None, on_overflow="skip", sync=False,
-                 arena=False):
+                 arena=False, resident_masters=False):
         if on_overflow not in _OVERFLOW_POLICIES:
             raise ValueError(f"on_overflow must be one of {_OVERFLOW_POLICIES}")
         if not 0.0 <= lr:
@@ -102,6 +110,8 @@ class FusedAdamW:
             device = p.device
         self._staging = None   # HostStaging of CPU masters (None: masters on the GPU)
         self._grad_staging = None
+        self.resident_masters = bool(resident_masters)
+        self._host_marks = {}  # index -> (storage, version) of the host master its mirror holds
         self._chunk_cache = None  # per-chunk descriptor batches of the CPU-master pipeline
         if device.type == "cpu":
             for _, p in flat:
@@ -114,6 +124,7 @@ class FusedAdamW:
             self._staging = HostStaging([p.shape for _, p in flat], torch.float32, device)
             self._dev = self._staging.views
             self._staging.upload([p for _, p in flat])  # for the initial export copies
+            self._mark_masters(range(len(flat)))
         else:
             for _, p in flat:
                 kernels.require_device_tensor(p, "param")
@@ -295,6 +306,31 @@ class FusedAdamW:
         dev_grads = self._stage_in(grads, present, stream, masters=False)
         return self._enqueue(dev_grads, present, stream, checked, pipeline=True)
 
+    def _mark_masters(self, which):
+        """Record that the mirrors of `which` now hold their host masters' values."""
+        flat = self._flat()
+        for i in which:
+            p = flat[i][1]
+            self._host_marks[i] = (p.data_ptr(), p._version)
+
+    def _current_masters(self, which):
+        """resident_masters: the indices of `which` whose mirrors still hold their host
+        masters' values (same storage, same version since the last step); their
+        marks are dropped until the caller marks them again after its step."""
+        flat = self._flat()
+        current = set()
+        for i in which:
+            mark = self._host_marks.pop(i, None)
+            p = flat[i][1]
+            if self.resident_masters and mark == (p.data_ptr(), p._version):
+                current.add(i)
+        return current
+
+    def invalidate_masters(self):
+        """resident_masters: upload every master again at its next step (after host
+        writes its version counter cannot see, e.g. through `p.data` or NumPy)."""
+        self._host_marks.clear()
+
     def _stage_in(self, grads, present, stream=None, masters=True):
         """CPU masters: upload the host gradients (and with `masters` the listed
         masters); returns the per-parameter device gradients (None where absent)."""
@@ -320,13 +356,15 @@ class FusedAdamW:
             for i in host:
                 dev[i] = self._grad_staging.views[i]
         if masters:
-            self._staging.upload([flat[i][1] for i in present], present, stream)
+            self._staging.upload([flat[i][1] for i in present], present, stream,
+                                 current=self._current_masters(present))
         return dev
 
     def _stage_out(self, present, stream=None):
         """CPU masters: copy the listed device masters back into the CPU tensors."""
         flat = self._flat()
         self._staging.download([flat[i][1].data for i in present], present, stream)
+        self._mark_masters(present)
 
     def _chunk_batches(self, grads, present, hp_of):
         """One descriptor batch per staging chunk of the listed tensors (CPU masters):
@@ -396,7 +434,8 @@ class FusedAdamW:
                 [flat[i][1].data for i in present], present,
                 lambda lo, hi, pieces, st: next(launches).launch_dev(hps, scheds, ctl.clocks,
                                                                      ctl.state, slot, st, None),
-                s)
+                s, current=self._current_masters(present))
+            self._mark_masters(present)
         elif self.kernel_timer is not None:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)

@@ -179,12 +179,14 @@ class HostStaging:
             host[i][s:e].copy_(self.flat[at:at + e - s], non_blocking=True)
             self.bytes_d2h += (e - s) * self.flat.element_size()
 
-    def upload(self, tensors, which=None, stream=None, wait=True):
+    def upload(self, tensors, which=None, stream=None, wait=True, current=()):
         """views[which[k]] <- tensors[k] (host, contiguous).
 
         wait=False: the copies do not wait for the work already queued on
         `stream`; only for a caller that knows no queued work reads or writes
-        these mirrors (later work on `stream` still waits for the copies)."""
+        these mirrors (later work on `stream` still waits for the copies).
+        current: indices whose mirrors already hold their host tensors' values;
+        a chunk made of such tensors only is not copied."""
         which = list(range(len(self.numels))) if which is None else list(which)
         tensors = list(tensors)
         self._check(tensors, which)
@@ -195,7 +197,10 @@ class HostStaging:
             self._copy.wait_stream(stream)  # earlier kernels may still read the mirrors
         bufs = None
         staged = 0
+        current = set(current)
         for lo, hi, pieces in self._chunks(which):
+            if self._direct(pieces, current):
+                continue
             if self._direct(pieces, pinned):
                 with torch.cuda.stream(self._copy):
                     self._up_direct(pieces, src)
@@ -259,7 +264,7 @@ class HostStaging:
             self._copy.synchronize()  # the host tensors hold the data on return
         stream.wait_stream(self._copy)
 
-    def pipeline(self, tensors, which, launch, stream=None, wait=True):
+    def pipeline(self, tensors, which, launch, stream=None, wait=True, current=()):
         """Per chunk of the listed mirrors: upload it from the host tensors, run
         launch(lo, hi, pieces, stream) (device work on those elements, enqueued on
         `stream`), then download it back into the same host tensors.  Uploads go
@@ -271,7 +276,9 @@ class HostStaging:
         the uploads do not wait for the work already queued on `stream` (for a
         caller that knows none of it touches these mirrors; the launches still
         follow it).  pieces: (index, start, end) of each listed tensor's elements
-        in the chunk."""
+        in the chunk.  current: indices whose mirrors already hold their host
+        tensors' values (kept resident since the last pass); a chunk made of such
+        tensors only is launched without its upload and still comes back."""
         which = list(which)
         tensors = list(tensors)
         self._check(tensors, which)
@@ -318,29 +325,33 @@ class HostStaging:
                 inflight.append((lo, hi, pieces, slot))
 
         staged = 0
+        current = set(current)
         for lo, hi, pieces in chunks:
+            resident = self._direct(pieces, current)
             if self._direct(pieces, pinned):
                 # pinned host tensors: DMA up, the launch, DMA back, nothing for the host
-                with torch.cuda.stream(self._copy):
-                    self._up_direct(pieces, host)
-                stream.wait_stream(self._copy)
+                if not resident:
+                    with torch.cuda.stream(self._copy):
+                        self._up_direct(pieces, host)
+                    stream.wait_stream(self._copy)
                 launch(lo, hi, pieces, stream)
                 self._copy_down.wait_stream(stream)
                 with torch.cuda.stream(self._copy_down):
                     self._down_direct(pieces, host)
                 service(block=False)
                 continue
-            slot = up[staged % 2]
-            staged += 1
-            slot["event"].synchronize()  # the upload that last read this buffer is done
-            for i, s, e in pieces:
-                at = self.offsets[i] + s - lo
-                slot["buf"][at:at + e - s].copy_(host[i][s:e])
-            with torch.cuda.stream(self._copy):
-                self.flat[lo:hi].copy_(slot["buf"][:hi - lo], non_blocking=True)
-                slot["event"].record(self._copy)
-            self.bytes_h2d += (hi - lo) * size
-            stream.wait_stream(self._copy)
+            if not resident:
+                slot = up[staged % 2]
+                staged += 1
+                slot["event"].synchronize()  # the upload that last read this buffer is done
+                for i, s, e in pieces:
+                    at = self.offsets[i] + s - lo
+                    slot["buf"][at:at + e - s].copy_(host[i][s:e])
+                with torch.cuda.stream(self._copy):
+                    self.flat[lo:hi].copy_(slot["buf"][:hi - lo], non_blocking=True)
+                    slot["event"].record(self._copy)
+                self.bytes_h2d += (hi - lo) * size
+                stream.wait_stream(self._copy)
             launch(lo, hi, pieces, stream)
             launched.append((lo, hi, pieces))
             service(block=False)

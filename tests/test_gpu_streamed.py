@@ -17,7 +17,10 @@ same calls run with the state resident in HBM (morph_amd.staging):
   * HostStaging round trips with small chunks, subsets and odd sizes, with pageable,
     pinned (direct DMA) and mixed host tensors; pinned masters (pin_host_tensors) give
     the same bits as pageable ones through both optimizers;
-  * two optimizers interleaved over the shared per-device copy and side streams.
+  * two optimizers interleaved over the shared per-device copy and side streams;
+  * resident_masters=True: the masters' mirrors stay in HBM between steps and only
+    changed host masters go up again (in-place ops, rebound storage, load_state_dict,
+    and writes through .data with invalidate_masters()), bit-exact.
 """
 import copy
 
@@ -379,3 +382,95 @@ def test_mixed_devices_are_rejected():
         HybridMuonAdamW(model)
     with pytest.raises(ValueError, match="one device"):
         FusedAdamW([torch.zeros(4), torch.zeros(4, device=DEV)])
+
+
+@pytest.mark.parametrize("chunk,pinned", [(None, False), (5000, False), (None, True)])
+def test_fused_adamw_resident_masters(chunk, pinned):
+    """resident_masters=True: after its first step the optimizer keeps the masters' device
+    mirrors and uploads only the gradients (the masters come back as before), bit-exact
+    with the device-resident optimizer; a master modified in place on the host between
+    steps (its version counter moves) is uploaded again."""
+    masters, grads = config1_inputs()
+    cpu = [m.clone() for m in masters]
+    if pinned:
+        pin_host_tensors(cpu)
+    dev = [m.to(DEV) for m in masters]
+    groups = lambda ps: [dict(params=[p for p in ps if p.ndim == 2], weight_decay=CONFIG1["wd_2d"]),
+                         dict(params=[p for p in ps if p.ndim == 1], weight_decay=0.0)]
+    kw = dict(lr=CONFIG1["lr"], betas=CONFIG1["betas"], eps=CONFIG1["eps"])
+    opt_c = FusedAdamW(groups(cpu), resident_masters=True, **kw)
+    opt_d = FusedAdamW(groups(dev), **kw)
+    if chunk is not None:
+        opt_c._staging.chunk = chunk
+    flat_c = [p for g in opt_c.param_groups for p in g["params"]]
+    flat_d = [p for g in opt_d.param_groups for p in g["params"]]
+    index = {id(p): i for i, p in enumerate(cpu)}
+    nbytes = 4 * sum(p.numel() for p in flat_c)
+    for t in range(1, 7):
+        gs = grads(t)
+        for p in flat_c:
+            p.grad = gs[index[id(p)]].clone()
+        for pc, pd in zip(flat_c, flat_d):
+            pd.grad = pc.grad.to(DEV)
+        if t == 4:  # the host changes two masters in place: they must go up again
+            with torch.no_grad():
+                for k in (0, 4):
+                    flat_c[k].mul_(.5)
+                    flat_d[k].mul_(.5)
+        up0 = opt_c._staging.bytes_h2d
+        opt_c.step()
+        opt_d.step()
+        up = opt_c._staging.bytes_h2d - up0
+        if t == 4:
+            assert up > 0
+            if chunk is not None:  # only the chunks holding the two changed masters
+                assert up < nbytes
+        else:
+            assert up == 0  # masters stayed resident (the initial upload is the constructor's)
+        for pc, pd in zip(flat_c, flat_d):
+            assert torch.equal(pc, pd.cpu()), t
+
+
+def test_hybrid_resident_masters_follow_host_changes():
+    """HybridMuonAdamW(resident_masters=True) on CPU masters against a device-resident twin
+    over 7 steps, bit-exact, with host changes between steps that the optimizer must see:
+    an in-place op on a parameter, a parameter's .data rebound to new storage,
+    model.load_state_dict, and a write through .data followed by invalidate_masters()."""
+    torch.manual_seed(11)
+    cpu_model = Tiny()
+    dev_model = copy.deepcopy(cpu_model).to(DEV)
+    opt_c = HybridMuonAdamW(cpu_model, lr=.003, muon_lr=.02, resident_masters=True)
+    opt_d = HybridMuonAdamW(dev_model, lr=.003, muon_lr=.02)
+    pc = dict(cpu_model.named_parameters())
+    pd = dict(dev_model.named_parameters())
+    muon_up = []
+    for step in range(7):
+        with torch.no_grad():
+            if step == 2:  # in place on the parameter: its version counter moves
+                pc["up.weight"].mul_(.5); pd["up.weight"].mul_(.5)
+                pc["norm.weight"].add_(.25); pd["norm.weight"].add_(.25)
+            if step == 3:  # new storage
+                pc["down.weight"].data = pc["down.weight"].data * 2
+                pd["down.weight"].data = pd["down.weight"].data * 2
+            if step == 4:  # a checkpoint restore
+                state = {k: v * 1.5 for k, v in cpu_model.state_dict().items()}
+                cpu_model.load_state_dict(state)
+                dev_model.load_state_dict({k: v.to(DEV) for k, v in state.items()})
+            if step == 5:  # invisible to the version counter: the caller invalidates
+                pc["gate.weight"].data.add_(.125); pd["gate.weight"].add_(.125)
+                pc["lm_head.weight"].data.mul_(.75); pd["lm_head.weight"].mul_(.75)
+                opt_c.invalidate_masters()
+        _engine_grads(cpu_model, 40 + step)
+        for n, p in cpu_model.named_parameters():
+            pd[n].grad = p.grad.to(DEV)
+        up0 = opt_c._muon_masters.bytes_h2d
+        opt_c.step()
+        opt_d.step()
+        muon_up.append(opt_c._muon_masters.bytes_h2d - up0)
+        for n, p in cpu_model.named_parameters():
+            assert torch.equal(p.detach(), pd[n].detach().cpu()), (step, n)
+    muon_bytes = 4 * sum(p.numel() for p in opt_c.muon)
+    assert muon_up[0] == muon_bytes                  # first step: every master goes up
+    assert muon_up[1] == 0 and muon_up[6] == 0       # untouched: none
+    assert 0 < muon_up[2] < muon_bytes and 0 < muon_up[3] < muon_bytes
+    assert muon_up[4] == muon_bytes and muon_up[5] == muon_bytes
