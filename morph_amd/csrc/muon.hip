@@ -49,18 +49,24 @@ constexpr int kMaxMats = 64;
 // the 42-matrix [3072, 6144] batch, bit-identical results throughout):
 //   momentum_kernel: 256 lanes, one 128-bit access each (128 lanes: 6% slower);
 //   apply_flat_kernel: 64 lanes, one 128-bit access each (128: 2%, 256: 6% slower);
-//   transpose tiles of 64 stored rows x 128 stored columns: 512-byte row segments
-//   of the FP32 streams, 128-byte segments of X (64 x 64 tiles: 7% slower);
-//   momentum_t_kernel at 3 workgroups per CU and apply_t_kernel at 6, by a dynamic
-//   LDS reservation beside the static tile (uncapped: 7% and 4% slower; 2 per CU
-//   for momentum_t_kernel or 3 for apply_t_kernel: 5% slower).
+//   momentum_t_kernel: tiles of 64 stored rows x 128 stored columns (512-byte row
+//   segments of the FP32 streams, 128-byte segments of X), every load of a tile
+//   in flight before the first is used, 2 workgroups per CU (3: 4% slower, 6 or
+//   uncapped: 7% slower; 128 x 64 tiles: 14%, 64 x 256: 2%, tiles taken down
+//   the columns first: 6% slower);
+//   apply_t_kernel: tiles of 64 x 256 (1 KiB row segments of p, 128-byte ones of
+//   X), 2 workgroups per CU (64 x 128 tiles: 2.5% slower);
+//   the workgroups per CU set by a dynamic LDS reservation beside the static
+//   tile (160 KiB of LDS per CU).
 constexpr int kFlat = 256;
 constexpr int kFlatApply = 64;
 constexpr int kElemsPerBlock = kFlat * 4;
-constexpr int kTR = 64;   // stored rows per transpose tile
-constexpr int kTC = 128;  // stored columns per transpose tile
-constexpr size_t kMomentumTReserve = 24 * 1024;  // + 16.5 KiB tile: 3 workgroups per CU
-constexpr size_t kApplyTReserve = 6 * 1024;      // + 17 KiB tile: 6 workgroups per CU
+constexpr int kTR = 64;    // stored rows per momentum transpose tile
+constexpr int kTC = 128;   // stored columns per momentum transpose tile
+constexpr int kATR = 64;   // stored rows per apply transpose tile
+constexpr int kATC = 256;  // stored columns per apply transpose tile
+constexpr size_t kMomentumTReserve = 40 * 1024;  // + 16.5 KiB tile: 2 workgroups per CU
+constexpr size_t kApplyTReserve = 24 * 1024;     // + 34 KiB tile: 2 workgroups per CU
 constexpr int64_t kRowPad = 64;                 // bf16 elements appended to every X/A/B row
 
 // The matrices one launch covers, by slot (blockIdx.y of the elementwise passes):
@@ -80,7 +86,8 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 struct Layout {
   int64_t rows, cols, m, n, mp, np, count, numel;
   int64_t blocks;  // flat blocks per matrix (momentum_kernel)
-  int64_t tiles;   // transpose tiles per matrix (momentum_t_kernel, apply_t_kernel)
+  int64_t tiles;   // transpose tiles per matrix (momentum_t_kernel)
+  int64_t atiles;  // transpose tiles per matrix (apply_t_kernel)
   int64_t parts;   // partial sums per matrix: max(blocks, tiles)
   int64_t ldn, ldm;  // row lengths of X ([Mp][ldn]) and of A, B ([Mp][ldm])
   size_t off_part, off_scale, off_x0, off_x1, off_a, off_b, total;
@@ -101,6 +108,7 @@ Layout make_layout(int64_t rows, int64_t cols, int64_t count) {
   L.blocks = (L.numel + kElemsPerBlock - 1) / kElemsPerBlock;
   // tiles of a matrix stored with its long side as rows (the ones X transposes)
   L.tiles = ((L.n + kTR - 1) / kTR) * ((L.m + kTC - 1) / kTC);
+  L.atiles = ((L.n + kATR - 1) / kATR) * ((L.m + kATC - 1) / kATC);
   L.parts = L.blocks > L.tiles ? L.blocks : L.tiles;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -229,8 +237,8 @@ __global__ __launch_bounds__(kFlat) void momentum_kernel(MatPtrs mats, uint16_t*
   if (threadIdx.x == 0) part_all[(int64_t)mat * parts + blockIdx.x] = s;
 }
 
-// Tile geometry shared by momentum_t_kernel and apply_t_kernel: tile blockIdx.x
-// of the stored layout [pr, pc] (kTR x kTC, row-major over tiles), for the
+// Tile geometry of momentum_t_kernel and apply_t_kernel: tile blockIdx.x
+// of the stored layout [pr, pc] (TR x TC, row-major over tiles), for the
 // matrices whose X is its transpose.  `vec`: a whole tile with dimensions a
 // multiple of 4, moved 4 consecutive elements per lane access.
 struct TileGeo {
@@ -238,18 +246,19 @@ struct TileGeo {
   bool valid, vec;
 };
 
+template <int TR, int TC>
 __device__ __forceinline__ TileGeo tile_geo(const MatPtrs& mats, int slot, int64_t rows,
                                             int64_t cols) {
   TileGeo t;
   const bool tr = mats.transposed[slot] != 0;
   t.pr = tr ? cols : rows;
   t.pc = tr ? rows : cols;
-  t.tiles_c = (t.pc + kTC - 1) / kTC;
+  t.tiles_c = (t.pc + TC - 1) / TC;
   t.tile = blockIdx.x;
-  t.r0 = (t.tile / t.tiles_c) * kTR;
-  t.c0 = (t.tile % t.tiles_c) * kTC;
+  t.r0 = (t.tile / t.tiles_c) * TR;
+  t.c0 = (t.tile % t.tiles_c) * TC;
   t.valid = t.r0 < t.pr;
-  t.vec = (t.pc & 3) == 0 && (t.pr & 3) == 0 && t.r0 + kTR <= t.pr && t.c0 + kTC <= t.pc;
+  t.vec = (t.pc & 3) == 0 && (t.pr & 3) == 0 && t.r0 + TR <= t.pr && t.c0 + TC <= t.pc;
   return t;
 }
 
@@ -267,7 +276,7 @@ __global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16
   __shared__ __attribute__((aligned(8))) uint16_t tile[kTR][kTC + 4];
   __shared__ double lds[kBlock / 64];
   const int slot = blockIdx.y, mat = mats.index[slot];
-  const TileGeo t = tile_geo(mats, slot, rows, cols);
+  const TileGeo t = tile_geo<kTR, kTC>(mats, slot, rows, cols);
   if (!t.valid) return;  // block-uniform
   const float* g = mats.grad[slot];
   const float* mom = mats.mom[slot];
@@ -280,32 +289,53 @@ __global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16
                                     : 0);
   const bool vec = t.vec && (addr & 15) == 0;
   constexpr int kLPR = kTC / 4, kRPP = kBlock / kLPR;  // stored rows: lanes per row, rows per pass
+  constexpr int kPasses = kTR / kRPP;
   const int q = threadIdx.x % kLPR, w = threadIdx.x / kLPR;
   double ss = 0.0;
   bool bad = false;
+  if (vec) {
+    // every load of the tile is issued before the first is used: a lane keeps
+    // 2 x kPasses 128-bit loads in flight, which the few workgroups per CU need
+    // to cover HBM latency
+    f32x4 gv[kPasses], mv[kPasses];
 #pragma unroll
-  for (int pass = 0; pass < kTR / kRPP; ++pass) {
-    const int rr = w + pass * kRPP;
-    const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
-    uint32_t h[4] = {0, 0, 0, 0};
-    if (vec) {
-      const int64_t i = r * t.pc + c;
-      const f32x4 gv = load_stream<true>(reinterpret_cast<const f32x4*>(g + i));
-      const u32x4 gb = __builtin_bit_cast(u32x4, gv);
+    for (int pass = 0; pass < kPasses; ++pass)
+      gv[pass] = load_stream<true>(reinterpret_cast<const f32x4*>(
+          g + (t.r0 + w + pass * kRPP) * t.pc + t.c0 + 4 * q));
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      mv[pass] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kMomentum)
+        mv[pass] = load_stream<true>(reinterpret_cast<const f32x4*>(
+            mom + (t.r0 + w + pass * kRPP) * t.pc + t.c0 + 4 * q));
+    }
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int rr = w + pass * kRPP;
+      const u32x4 gb = __builtin_bit_cast(u32x4, gv[pass]);
       bad |= nonfinite_f32_bits(gb.x) | nonfinite_f32_bits(gb.y) | nonfinite_f32_bits(gb.z) |
              nonfinite_f32_bits(gb.w);
-      f32x4 mv = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (kMomentum) mv = load_stream<true>(reinterpret_cast<const f32x4*>(mom + i));
+      uint32_t h[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float m = mv[e], ui;
-        momentum_one<kMomentum>(gv[e], m, ui, mom_w, nest_w, large_m, large_n);
-        mv[e] = m;
+        float m = mv[pass][e], ui;
+        momentum_one<kMomentum>(gv[pass][e], m, ui, mom_w, nest_w, large_m, large_n);
+        mv[pass][e] = m;
         h[e] = float_to_bf16_bits(ui);
         ss += (double)ui * (double)ui;
       }
-      if constexpr (kMomentum) store_stream<true>(reinterpret_cast<f32x4*>(mom_out + i), mv);
-    } else {
+      if constexpr (kMomentum)
+        store_stream<true>(reinterpret_cast<f32x4*>(mom_out + (t.r0 + rr) * t.pc + t.c0 + 4 * q),
+                           mv[pass]);
+      *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) =
+          u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    }
+  } else {
+#pragma unroll
+    for (int pass = 0; pass < kPasses; ++pass) {
+      const int rr = w + pass * kRPP;
+      const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
+      uint32_t h[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         if (r < t.pr && c + e < t.pc) {
@@ -318,8 +348,9 @@ __global__ __launch_bounds__(kBlock) void momentum_t_kernel(MatPtrs mats, uint16
           ss += (double)ui * (double)ui;
         }
       }
+      *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) =
+          u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     }
-    *reinterpret_cast<u32x2*>(&tile[rr][4 * q]) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
   }
   flag_nonfinite(found_inf, bad);
   __syncthreads();
@@ -427,7 +458,7 @@ __global__ __launch_bounds__(kFlatApply) void apply_flat_kernel(MatPtrs mats,
   }
 }
 
-// Matrices whose X is the transpose of the stored layout: per kTR x kTC tile of p,
+// Matrices whose X is the transpose of the stored layout: per kATR x kATC tile of p,
 // the X tile is staged through LDS so that the X reads and the p accesses are both
 // coalesced rows.
 template <bool kExtract>
@@ -435,46 +466,52 @@ __global__ __launch_bounds__(kBlock) void apply_t_kernel(MatPtrs mats, const uin
                                                          int64_t rows, int64_t cols, int64_t mp,
                                                          int64_t ldn, float scale_n, float scale_t,
                                                          float decay, float neg_lr) {
-  __shared__ __attribute__((aligned(8))) uint16_t tile[kTC][kTR + 4];
+  __shared__ __attribute__((aligned(8))) uint16_t tile[kATC][kATR + 4];
   const int slot = blockIdx.y, mat = mats.index[slot];
-  const TileGeo t = tile_geo(mats, slot, rows, cols);
+  const TileGeo t = tile_geo<kATR, kATC>(mats, slot, rows, cols);
   if (!t.valid) return;  // block-uniform
   float* p = mats.param[slot];
   const float scale = mats.transposed[slot] ? scale_t : scale_n;
   const uint16_t* xm = x_all + (int64_t)mat * mp * ldn;
   const bool vec = t.vec && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
-  constexpr int kLPR = kTC / 4, kRPP = kBlock / kLPR;  // stored rows: lanes per row, rows per pass
+  constexpr int kLPR = kATC / 4, kRPP = kBlock / kLPR;  // stored rows: lanes per row, rows per pass
   const int q = threadIdx.x % kLPR, w = threadIdx.x / kLPR;
   // the p rows go out first: they do not wait for the X tile
-  f32x4 pv[kTR / kRPP];
+  f32x4 pv[kATR / kRPP];
   if (vec && !kExtract) {
 #pragma unroll
-    for (int pass = 0; pass < kTR / kRPP; ++pass)
+    for (int pass = 0; pass < kATR / kRPP; ++pass)
       pv[pass] = load_stream<true>(
           reinterpret_cast<const f32x4*>(p + (t.r0 + w + pass * kRPP) * t.pc + t.c0 + 4 * q));
   }
-  // tile[c - c0][r - r0] = X[c][r]: X rows c0 .. c0 + kTC - 1, columns r0 .. r0 + kTR - 1
-  constexpr int kXL = kTR / 4, kXRP = kBlock / kXL;
+  // tile[c - c0][r - r0] = X[c][r]: X rows c0 .. c0 + kATC - 1, columns r0 .. r0 + kATR - 1
+  constexpr int kXL = kATR / 4, kXRP = kBlock / kXL, kXPasses = kATC / kXRP;
   const int q2 = threadIdx.x % kXL, w2 = threadIdx.x / kXL;
+  if (t.vec) {
+    // all X loads in flight together, behind the p loads
+    u32x2 xv[kXPasses];
 #pragma unroll
-  for (int pass = 0; pass < kTC / kXRP; ++pass) {
-    const int cc = w2 + pass * kXRP;
-    const int64_t c = t.c0 + cc, r = t.r0 + 4 * q2;
-    u32x2 v = u32x2{0, 0};
-    if (t.vec) {
-      v = *reinterpret_cast<const u32x2*>(xm + c * ldn + r);
-    } else {
+    for (int pass = 0; pass < kXPasses; ++pass)
+      xv[pass] = *reinterpret_cast<const u32x2*>(xm + (t.c0 + w2 + pass * kXRP) * ldn + t.r0 +
+                                                 4 * q2);
+#pragma unroll
+    for (int pass = 0; pass < kXPasses; ++pass)
+      *reinterpret_cast<u32x2*>(&tile[w2 + pass * kXRP][4 * q2]) = xv[pass];
+  } else {
+#pragma unroll
+    for (int pass = 0; pass < kXPasses; ++pass) {
+      const int cc = w2 + pass * kXRP;
+      const int64_t c = t.c0 + cc, r = t.r0 + 4 * q2;
       uint32_t h[4] = {0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         if (c < t.pc && r + e < t.pr) h[e] = xm[c * ldn + r + e];
-      v = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+      *reinterpret_cast<u32x2*>(&tile[cc][4 * q2]) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
     }
-    *reinterpret_cast<u32x2*>(&tile[cc][4 * q2]) = v;
   }
   __syncthreads();
 #pragma unroll
-  for (int pass = 0; pass < kTR / kRPP; ++pass) {
+  for (int pass = 0; pass < kATR / kRPP; ++pass) {
     const int rr = w + pass * kRPP;
     const int64_t r = t.r0 + rr, c = t.c0 + 4 * q;
     uint32_t h[4];
@@ -537,7 +574,8 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   if (workspace == nullptr || workspace_bytes < L.total) return MORPH_EWORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return MORPH_EINVAL;
   // grid x of the tile passes and of apply_flat_kernel (the most blocks of the flat passes)
-  if (L.tiles > INT32_MAX || (L.numel + kFlatApply * 4 - 1) / (kFlatApply * 4) > INT32_MAX)
+  if (L.tiles > INT32_MAX || L.atiles > INT32_MAX ||
+      (L.numel + kFlatApply * 4 - 1) / (kFlatApply * 4) > INT32_MAX)
     return MORPH_ERANGE;
   char* ws = static_cast<char*>(workspace);
   out->L = L;
@@ -551,7 +589,7 @@ int setup(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
 }
 
 // The transpose tiles of `count` matrices (momentum_t_kernel, apply_t_kernel).
-dim3 tile_grid(const Layout& L, int count) { return dim3((unsigned)L.tiles, (unsigned)count); }
+dim3 tile_grid(int64_t tiles, int count) { return dim3((unsigned)tiles, (unsigned)count); }
 
 // X0 has the stored layout of a matrix when its stored rows are the shorter side.
 bool stored_is_x(const morph_muon_matrix& m, int64_t rows, int64_t cols) {
@@ -607,7 +645,7 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
     if ((rc = launch_status())) return rc;
   }
   if (n_tiled) {
-    const dim3 tg = tile_grid(L, n_tiled);
+    const dim3 tg = tile_grid(L.tiles, n_tiled);
     if (orth_only)
       hipLaunchKernelGGL(momentum_t_kernel<false>, tg, dim3(kBlock), kMomentumTReserve, s, tiled,
                          W.X[0], W.part, rows, cols, L.mp, L.ldn, L.parts, mw, nw, found_inf);
@@ -692,7 +730,7 @@ int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
     if ((rc = launch_status())) return rc;
   }
   if (n_tiled) {
-    const dim3 tg = tile_grid(L, n_tiled);
+    const dim3 tg = tile_grid(L.atiles, n_tiled);
     if (orth_only)
       hipLaunchKernelGGL(apply_t_kernel<true>, tg, dim3(kBlock), kApplyTReserve, s, tiled, x,
                          rows, cols, L.mp, L.ldn, sn, st, hp->decay, hp->neg_lr);
