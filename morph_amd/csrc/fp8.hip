@@ -5,26 +5,25 @@
 // following streamtrain/precision.py:24-37 (pack_fp8 / unpack_fp8, used for
 // the opt-in FP8 weight transfer of disk.py:330-345).  The reference computes
 // with torch ops in FP32 (IEEE division, one rounding each); the bytes and
-// scales here are identical.  The scale is the same IEEE division; each
+// the finite scales here are identical.  The scale is the same IEEE division; each
 // element's quotient is the IEEE division for FP32 inputs, and for FP16/BF16
 // inputs Markstein's correction of the product with the block's reciprocal
 // (pack_kernel), checked exhaustively against the division.
 //
 // E4M3FN: 1 sign, 4 exponent (bias 7), 3 mantissa bits; no infinities, NaN =
-// S.1111.111, largest finite 448, smallest subnormal 2^-9.  The conversion is
-// round to nearest even; e4m3fn_from_float writes it from the format
-// definition: normal results round the FP32 bit pattern at mantissa bit 20 (a
-// carry moves into the exponent), subnormal results are rint(|x| * 2^9); NaN
-// stays NaN.  The pack encodes with gfx950's v_cvt_pk_fp8_f32, which gives the
-// same bytes for every non-NaN input in range (all FP32 bit patterns compared
-// on the device), and uses e4m3fn_from_float for NaN.  Inputs here are already
-// clamped to +-448, so the out-of-range case only arises for NaN.  Torch
-// propagates NaN through amax, clamp_min and clamp, so a block with a NaN has
-// a NaN scale and all-NaN bytes; that is reproduced too.
+// S.1111.111, largest finite 448, smallest subnormal 2^-9.  The pack encodes
+// the quotients, clamped to +-448, with gfx950's v_cvt_pk_fp8_f32 (round to
+// nearest even), which equals torch's conversion for every FP32 value in
+// [-448, 448] (all compared on the device); the unpack decodes with
+// v_cvt_pk_f32_fp8, exact for every code.  Torch propagates NaN through amax,
+// clamp_min and clamp, so a block with a NaN has a NaN scale and NaN bytes, and
+// a block with an infinity an infinite scale; their bytes follow the x86 NaN
+// rules the reference's CPU ops run under (nonfinite_block_bytes8).
 //
-// One wave per 4 blocks (64 lanes x 16 elements); each block is held by 32
-// lanes (8 elements each), and its amax is a reduction over those lanes
-// (half_wave_max_bits).  A workgroup holds 4 waves / 16 blocks.
+// One wave per 4 blocks (64 lanes x 16 elements).  Pack: each block is held
+// by a row of 16 lanes (16 contiguous elements each), its amax a reduction
+// within the row (row_max_bits).  Unpack: each block by 32 lanes, 8 bytes
+// each per half of the wave's span.  A workgroup holds 4 waves / 16 blocks.
 #include <type_traits>
 
 #include "common.h"
@@ -36,50 +35,60 @@ constexpr int kBlockElems = MORPH_FP8_BLOCK;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBlocksPerWave = 4;  // 64 lanes x 16 elements
-static_assert(kBlockElems == 256, "32 lanes x 8 elements per block");
+constexpr int kParts = 2;          // unpack: 512-element parts per wave, 8 elements per lane
+static_assert(kBlockElems == 256, "16 lanes x 16 elements per block (pack), 32 x 8 (unpack)");
 
 __device__ __forceinline__ bool is_nan(float x) { return x != x; }
 
-// torch.amax of |x| over a block held by 32 lanes (lanes 0-31 or 32-63 of the
-// wave): the bit patterns of non-negative floats order like the values, and
-// every NaN pattern (above 0x7F800000) above +inf, so an unsigned maximum of
-// |x|'s bits is the amax, NaN if any element is NaN.  Within each row of 16
-// lanes by DPP (quad swaps, half-row and row mirrors), then across the two rows
-// of each half with gfx950's v_permlane16_swap; no LDS round trips.
-__device__ __forceinline__ uint32_t half_wave_max_bits(uint32_t x) {
+// torch.amax of |x| over a block held by a row of 16 lanes: the bit patterns
+// of non-negative floats order like the values, and every NaN pattern (above
+// 0x7F800000) above +inf, so an unsigned maximum of |x|'s bits is the amax,
+// NaN if any element is NaN.  By DPP within the row (quad swaps, half-row and
+// row mirrors); every lane of the row ends with the maximum.
+__device__ __forceinline__ uint32_t row_max_bits(uint32_t x) {
   x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
   x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
   x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false));  // row_half_mirror
   x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false));  // row_mirror
-  const auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);  // rows 0 <-> 1, 2 <-> 3
-  return max((uint32_t)r16[0], (uint32_t)r16[1]);
+  return x;
 }
 
-__device__ __forceinline__ uint32_t e4m3fn_from_float(float x) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, x);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t a = u & 0x7FFFFFFFu;
-  if (a > 0x7F800000u) return sign | 0x7Fu;  // NaN
-  uint32_t r;
-  if (a < 0x3C800000u) {  // below 2^-6: subnormal (or zero) result, step 2^-9
-    r = (uint32_t)__builtin_rintf(__builtin_bit_cast(float, a) * 512.0f);
+// Eight consecutive input elements as loaded: one 16-byte load of 16-bit
+// values, two of FP32.
+template <typename IT>
+struct Raw8 {
+  u32x4 v;
+};
+template <>
+struct Raw8<F32> {
+  f32x4 lo, hi;
+};
+
+// Elements i .. i + 7, all inside the input and 16-byte aligned.
+template <typename IT>
+__device__ __forceinline__ Raw8<IT> load_raw8(const void* src, int64_t i) {
+  Raw8<IT> r;
+  if constexpr (std::is_same_v<IT, F32>) {
+    r.lo = *reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + i);
+    r.hi = *reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + i + 4);
   } else {
-    r = ((a + 0x7FFFFu + ((a >> 20) & 1u)) >> 20) - (120u << 3);  // rebias 127 -> 7
-    if (r > 0x7Eu) r = 0x7Fu;  // beyond 448 after rounding: NaN (no infinities)
+    r.v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + i);
   }
-  return sign | r;
+  return r;
 }
 
-__device__ __forceinline__ float float_from_e4m3fn(uint32_t b) {
-  const uint32_t e = (b >> 3) & 0xFu, m = b & 7u;
-  float v;
-  if (e == 0)
-    v = (float)m * 0.001953125f;  // m * 2^-9, exact
-  else if (e == 0xFu && m == 7u)
-    v = __builtin_nanf("");
-  else
-    v = __builtin_bit_cast(float, ((e + 120u) << 23) | (m << 20));
-  return (b & 0x80u) ? -v : v;
+template <typename IT>
+__device__ __forceinline__ void raw8_to_float(const Raw8<IT>& r, float (&x)[8]) {
+  if constexpr (std::is_same_v<IT, F32>) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = r.lo[k], x[4 + k] = r.hi[k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      x[2 * k] = to_float<IT>(r.v[k] & 0xFFFFu);
+      x[2 * k + 1] = to_float<IT>(r.v[k] >> 16);
+    }
+  }
 }
 
 // Elements i .. i + 7 of the input as floats (zeros past n: the reference pads
@@ -89,19 +98,7 @@ template <typename IT>
 __device__ __forceinline__ void load8(const void* src, int64_t i, int64_t n, float (&x)[8]) {
   constexpr int kBytes = Fmt<IT>::bytes;
   if (i + 8 <= n && (reinterpret_cast<uintptr_t>(src) + i * kBytes) % 16 == 0) {
-    if constexpr (std::is_same_v<IT, F32>) {
-      const f32x4 v0 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + i);
-      const f32x4 v1 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + i + 4);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) x[k] = v0[k], x[4 + k] = v1[k];
-    } else {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(src) + i);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        x[2 * k] = to_float<IT>(v[k] & 0xFFFFu);
-        x[2 * k + 1] = to_float<IT>(v[k] >> 16);
-      }
-    }
+    raw8_to_float<IT>(load_raw8<IT>(src, i), x);
     return;
   }
 #pragma unroll
@@ -118,10 +115,73 @@ __device__ __forceinline__ void load8(const void* src, int64_t i, int64_t n, flo
   }
 }
 
-// One wave per kBlocksPerWave consecutive blocks: in half h (0, 1) of the
-// wave's span, lane l holds the 8 elements at 512 h + 8 l, so lanes 0-31 and
-// 32-63 each hold one whole block per half, every access is a contiguous 512 B
-// (16-bit input) per instruction, and the amax needs no cross-half exchange.
+// Eight quotients clamp(x / s, -448, 448) encoded as E4M3FN bytes (two words),
+// for a finite scale s: x and the quotients are then finite too (|x| <= 448 s).
+// For 16-bit inputs x / s is Markstein's correction of |x| * y with y = 1 / s --
+// one IEEE division per block instead of one per element -- with x's sign put
+// back (so -0 stays -0, as in the division): q = RN(|x| y), r = |x| - q s (exact
+// by the fma), q' = RN(q + r y).  Checked against the IEEE quotient for every
+// finite FP16 and BF16 block maximum and every element up to it: FP16 quotients
+// are identical; BF16 ones differ only for subnormal elements, whose quotients
+// (below 2^-13) encode as zero either way.  FP32 inputs take the IEEE division.
+// v_cvt_pk_fp8_f32 is gfx950's OCP E4M3 conversion, round to nearest even:
+// equal to e4m3fn_from_float for every FP32 input in [-448, 448] (all 2^32 bit
+// patterns were compared on the device).
+template <typename IT>
+__device__ __forceinline__ u32x2 quantize8(const float (&x)[8], float s, float y) {
+  float q[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if constexpr (std::is_same_v<IT, F32>) {
+      q[k] = x[k] / s;
+    } else {
+      const float ax = __builtin_fabsf(x[k]);
+      const float t = ax * y;
+      const float r = __fmaf_rn(-t, s, ax);
+      q[k] = __builtin_copysignf(__fmaf_rn(r, y, t), x[k]);
+    }
+    q[k] = __builtin_amdgcn_fmed3f(q[k], -448.0f, 448.0f);
+  }
+  u32x2 w;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t word = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * k], q[4 * k + 1], 0, false);
+    w[k] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * k + 2], q[4 * k + 3], (int)word, true);
+  }
+  return w;
+}
+
+// The bytes of a block whose scale is NaN (it holds a NaN) or +inf (an
+// infinity, no NaN), as the reference's CPU ops give them: x86 division
+// returns its first NaN operand, and an invalid one (inf / inf) the negative
+// default NaN; clamp keeps a NaN as it is and the E4M3FN conversion keeps its
+// sign (NaN = S.1111.111).  s is a positive NaN (the amax of |x|), so
+//   s = NaN: x's own NaN code for a NaN x, 0x7F for every other element;
+//   s = inf: +-0 (x's sign) for finite x, 0xFF for x = +-inf.
+__device__ __forceinline__ u32x2 nonfinite_block_bytes8(const float (&x)[8], float s) {
+  u32x2 w = u32x2{0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t sign = (__builtin_bit_cast(uint32_t, x[k]) >> 24) & 0x80u;
+    uint32_t b;
+    if (is_nan(x[k]))
+      b = sign | 0x7Fu;
+    else if (is_nan(s))
+      b = 0x7Fu;
+    else if (__builtin_isinf(x[k]))
+      b = 0xFFu;
+    else
+      b = sign;
+    w[k >> 2] |= b << (8 * (k & 3));
+  }
+  return w;
+}
+
+// One wave per kBlocksPerWave consecutive blocks: lane l holds the 16 elements
+// at 16 l of the wave's span, so a row of 16 lanes holds one block, its amax is
+// a reduction within the row, and each lane stores 16 contiguous bytes.  A wave
+// whose span lies inside an aligned input issues all of its loads before the
+// first is used.
 template <typename IT>
 __global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__ src, int64_t n,
                                                         uint8_t* __restrict__ bytes,
@@ -132,72 +192,45 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(const void* __restrict__
   if (first >= blocks) return;  // whole waves exit together
   const int lane = threadIdx.x & 63;
   auto mag = [](float v) { return __builtin_bit_cast(uint32_t, v) & 0x7FFFFFFFu; };
+  const int64_t i = first * kBlockElems + 16 * lane;
+  const int64_t blk = first + (lane >> 4);
+  float xa[8], xb[8];
+  if ((first + kBlocksPerWave) * kBlockElems <= n &&
+      reinterpret_cast<uintptr_t>(src) % 16 == 0) {  // wave-uniform
+    const Raw8<IT> ra = load_raw8<IT>(src, i), rb = load_raw8<IT>(src, i + 8);
+    raw8_to_float<IT>(ra, xa);
+    raw8_to_float<IT>(rb, xb);
+  } else {
+    load8<IT>(src, i, n, xa);  // zeros past n, so blocks past the end reduce harmlessly
+    load8<IT>(src, i + 8, n, xb);
+  }
+  uint32_t mb = 0;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int64_t blk = first + 2 * h + (lane >> 5);
-    const int64_t i = first * kBlockElems + 512 * h + 8 * lane;
-    float x[8];
-    load8<IT>(src, i, n, x);  // zeros past n, so blocks past the end reduce harmlessly
-    uint32_t mb = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) mb = max(mb, mag(x[k]));
-    const float m = __builtin_bit_cast(float, half_wave_max_bits(mb));
-    float s = m / 448.0f;
-    s = (s < 1e-30f) ? 1e-30f : s;  // clamp_min keeps NaN
-    if ((lane & 31) == 0 && blk < blocks) scales[blk] = s;
-    float q[8];
-    // FP32 inputs, and blocks holding an infinity (s = inf: x / s is 0, or NaN for the
-    // infinities themselves), take the IEEE division.
-    if (std::is_same_v<IT, F32> || __builtin_isinf(s)) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) q[k] = x[k] / s;
-    } else {
-      // 16-bit inputs, finite scale (NaN propagates either way): x / s by
-      // Markstein's correction of |x| * (1 / s) -- one IEEE division per block
-      // instead of one per element -- with x's sign put back (so -0 stays -0, as
-      // in the division).  q = RN(|x| y), r = |x| - q s (exact by the fma), q' =
-      // RN(q + r y).  Checked against the IEEE quotient for every finite FP16 and
-      // BF16 block maximum and every element up to it: FP16 quotients are
-      // identical; BF16 ones differ only for subnormal elements, whose quotients
-      // (below 2^-13) encode as zero either way.
-      const float y = 1.0f / s;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float ax = __builtin_fabsf(x[k]);
-        const float t = ax * y;
-        const float r = __fmaf_rn(-t, s, ax);
-        q[k] = __builtin_copysignf(__fmaf_rn(r, y, t), x[k]);
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      q[k] = is_nan(q[k]) ? q[k] : (q[k] < -448.0f ? -448.0f : (q[k] > 448.0f ? 448.0f : q[k]));
-    // v_cvt_pk_fp8_f32 is gfx950's OCP E4M3 conversion, round to nearest even:
-    // equal to e4m3fn_from_float for every non-NaN FP32 input in [-448, 448] (all
-    // 2^32 bit patterns were compared on the device); NaN keeps the format rule's
-    // encoding.
-    u32x2 w;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      uint32_t word = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * k], q[4 * k + 1], 0, false);
-      word = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[4 * k + 2], q[4 * k + 3], (int)word, true);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (is_nan(q[4 * k + e]))
-          word = (word & ~(0xFFu << (8 * e))) | (e4m3fn_from_float(q[4 * k + e]) << (8 * e));
-      w[k] = word;
-    }
-    if (i + 8 <= n && ((reinterpret_cast<uintptr_t>(bytes) + i) & 7) == 0) {
-      *reinterpret_cast<u32x2*>(bytes + i) = w;
-    } else {
-      for (int k = 0; k < 8; ++k)
-        if (i + k < n) bytes[i + k] = (uint8_t)(w[k >> 2] >> (8 * (k & 3)));
-    }
+  for (int k = 0; k < 8; ++k) mb = max(mb, max(mag(xa[k]), mag(xb[k])));
+  const float m = __builtin_bit_cast(float, row_max_bits(mb));
+  float s = m / 448.0f;
+  s = (s < 1e-30f) ? 1e-30f : s;  // clamp_min keeps NaN
+  if ((lane & 15) == 0 && blk < blocks) scales[blk] = s;
+  u32x2 wa, wb;
+  if (__builtin_isfinite(s)) {
+    const float y = std::is_same_v<IT, F32> ? 0.0f : 1.0f / s;
+    wa = quantize8<IT>(xa, s, y);
+    wb = quantize8<IT>(xb, s, y);
+  } else {
+    wa = nonfinite_block_bytes8(xa, s);
+    wb = nonfinite_block_bytes8(xb, s);
+  }
+  if (i + 16 <= n && ((reinterpret_cast<uintptr_t>(bytes) + i) & 15) == 0) {
+    *reinterpret_cast<u32x4*>(bytes + i) = u32x4{wa[0], wa[1], wb[0], wb[1]};
+  } else {
+    for (int k = 0; k < 16; ++k)
+      if (i + k < n) bytes[i + k] = (uint8_t)((k < 8 ? wa[k >> 2] : wb[(k - 8) >> 2]) >> (8 * (k & 3)));
   }
 }
 
-// The same layout as pack_kernel: in half h of the wave's span, lane l turns
-// the 8 bytes at 512 h + 8 l into 8 outputs with its block's scale.
+// The same layout as pack_kernel: in part h of the wave's span, lane l turns
+// the 8 bytes at 512 h + 8 l into 8 outputs with its block's scale; a wave
+// whose span lies inside aligned bytes loads all of its bytes and scales first.
 template <typename OT>
 __global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restrict__ bytes,
                                                           const float* __restrict__ scales,
@@ -207,21 +240,48 @@ __global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t* __restr
   const int64_t first = wave * kBlocksPerWave;
   if (first >= blocks) return;
   const int lane = threadIdx.x & 63;
+  const int64_t base = first * kBlockElems + 8 * lane;
+  const bool whole = (first + kBlocksPerWave) * kBlockElems <= n &&
+                     (reinterpret_cast<uintptr_t>(bytes) & 7) == 0;  // wave-uniform
+  u32x2 wv[kParts];
+  float sv[kParts];
+  if (whole) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int64_t i = first * kBlockElems + 512 * h + 8 * lane;
-    if (i >= n) continue;  // no cross-lane work here: lanes may leave on their own
-    const float s = scales[first + 2 * h + (lane >> 5)];
-    u32x2 w = u32x2{0u, 0u};
-    if (i + 8 <= n && ((reinterpret_cast<uintptr_t>(bytes) + i) & 7) == 0) {
-      w = *reinterpret_cast<const u32x2*>(bytes + i);
-    } else {
-      for (int k = 0; k < 8; ++k)
-        if (i + k < n) w[k >> 2] |= (uint32_t)bytes[i + k] << (8 * (k & 3));
+    for (int h = 0; h < kParts; ++h) {
+      wv[h] = *reinterpret_cast<const u32x2*>(bytes + base + 512 * h);
+      sv[h] = scales[first + 2 * h + (lane >> 5)];
     }
+  }
+#pragma unroll
+  for (int h = 0; h < kParts; ++h) {
+    const int64_t i = base + 512 * h;
+    float s;
+    u32x2 w = u32x2{0u, 0u};
+    if (whole) {
+      s = sv[h];
+      w = wv[h];
+    } else {
+      if (i >= n) continue;  // no cross-lane work here: lanes may leave on their own
+      s = scales[first + 2 * h + (lane >> 5)];
+      if (i + 8 <= n && ((reinterpret_cast<uintptr_t>(bytes) + i) & 7) == 0) {
+        w = *reinterpret_cast<const u32x2*>(bytes + i);
+      } else {
+        for (int k = 0; k < 8; ++k)
+          if (i + k < n) w[k >> 2] |= (uint32_t)bytes[i + k] << (8 * (k & 3));
+      }
+    }
+    // gfx950's v_cvt_pk_f32_fp8 decodes two OCP E4M3 bytes (word_sel: the high
+    // pair) exactly; every finite code is an FP32 value, and the NaN codes give NaN.
     float y[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) y[k] = float_from_e4m3fn((w[k >> 2] >> (8 * (k & 3))) & 0xFFu) * s;
+    for (int k = 0; k < 2; ++k) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);
+      y[4 * k] = lo[0] * s;
+      y[4 * k + 1] = lo[1] * s;
+      y[4 * k + 2] = hi[0] * s;
+      y[4 * k + 3] = hi[1] * s;
+    }
     constexpr int kBytes = Fmt<OT>::bytes;
     if (i + 8 <= n && (reinterpret_cast<uintptr_t>(dst) + i * kBytes) % 16 == 0) {
       if constexpr (std::is_same_v<OT, F32>) {

@@ -1,7 +1,7 @@
 """GPU FP8 block-scaled pack/unpack (morph_amd.fp8) against the oracle (precision.py:24-37).
 
-Bytes and scales bit-exact for FP32/FP16/BF16 inputs, ragged sizes and wide dynamic
-range (subnormal codes); exhaustive conversion sweeps over every finite FP16 value and
+Bytes (NaN codes included) and scales bit-exact for FP32/FP16/BF16 inputs, ragged sizes
+and wide dynamic range (subnormal codes); exhaustive conversion sweeps over every finite FP16 value and
 every FP32 value with |v| <= 448 at scale 1; zero and NaN blocks; unpack of all 256 codes at several
 scales into FP16/BF16/FP32; the reference's 4% roundtrip bound.
 """
@@ -17,11 +17,11 @@ DEV = torch.device("cuda", 0)
 
 
 def same(a, b):
-    """Bitwise equality, with any NaN equal to any NaN."""
+    """Bitwise equality: exact for E4M3FN bytes (NaN codes and their signs included);
+    for floats, with any NaN equal to any NaN (scales and unpacked values)."""
     a, b = a.cpu(), b.cpu()
     if a.dtype == torch.uint8:
-        nan = lambda t: (t & 0x7F) == 0x7F
-        return torch.equal(nan(a), nan(b)) and torch.equal(a[~nan(a)], b[~nan(b)])
+        return torch.equal(a, b)
     an, bn = torch.isnan(a.float()), torch.isnan(b.float())
     view = {torch.float32: torch.int32, torch.float16: torch.int16, torch.bfloat16: torch.int16}[a.dtype]
     return torch.equal(an, bn) and torch.equal(a[~an].view(view), b[~bn].view(view))
@@ -88,16 +88,28 @@ def test_blocks_with_infinities(dtype):
     assert same(sc, rsc) and same(enc, renc)
     assert torch.isinf(sc[0].cpu()) and torch.isinf(sc[1].cpu()) and torch.isnan(sc[2].cpu())
     assert enc[800].item() == 0x80 and enc[801].item() == 0
+    assert enc[5].item() == enc[300].item() == 0xFF  # inf / inf: the negative default NaN
 
 
-def test_zero_and_nan_blocks():
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_zero_and_nan_blocks(dtype):
+    """A zero block has scale 1e-30; a block with a NaN has a NaN scale and NaN bytes
+    whose signs follow the reference's ops: 0x7F for every element but a NaN one,
+    which keeps its own sign (x86 division returns its first NaN operand)."""
     x = torch.zeros(1024)
-    x[300] = float("nan")
+    x[256:512] = torch.linspace(-1, 1, 256)
+    x[300], x[301] = float("nan"), -float("nan")
     x[600:700] = torch.linspace(-1, 1, 100)
+    x[900] = -float("nan")
+    x = x.to(dtype)
     enc, sc = fp8.pack_fp8(x.to(DEV))
     renc, rsc = R.pack_fp8_torch(x)
     assert same(sc, rsc) and same(enc, renc)
     assert sc[0].item() == np.float32(1e-30) and torch.isnan(sc[1].cpu())
+    bits = x.float().view(torch.int32)  # the NaNs' signs after the cast to dtype
+    assert enc[256].item() == 0x7F
+    for i in (300, 301, 900):
+        assert enc[i].item() == (0xFF if bits[i] < 0 else 0x7F)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
