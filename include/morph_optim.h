@@ -332,7 +332,10 @@ int morph_convert_f32(const float* src, void* dst, int dst_dtype, int64_t n,
 
 /* scales[b] = max(amax(|src block b|) / 448, 1e-30) (NaN if the block holds a
  * NaN); bytes[i] = e4m3fn(clamp(src[i] / scale, -448, 448)), round to nearest
- * even.  bytes: n entries; scales: ceil(n / 256) entries. */
+ * even.  bytes: n entries; scales: ceil(n / 256) entries.  A block with a NaN
+ * or an infinity gets the bytes of the reference's x86 CPU ops: 0x7F for every
+ * non-NaN element of a NaN block and a NaN element's own NaN code (sign kept);
+ * in a block with an infinity +-0 for finite elements and 0xFF for +-inf. */
 int morph_fp8_pack(const void* src, int src_dtype, int64_t n, uint8_t* bytes, float* scales,
                    void* stream);
 /* dst[i] = dst_dtype(float(e4m3fn bytes[i]) * scales[i / 256]). */
