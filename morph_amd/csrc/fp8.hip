@@ -125,8 +125,8 @@ __device__ __forceinline__ void load8(const void* src, int64_t i, int64_t n, flo
 // are identical; BF16 ones differ only for subnormal elements, whose quotients
 // (below 2^-13) encode as zero either way.  FP32 inputs take the IEEE division.
 // v_cvt_pk_fp8_f32 is gfx950's OCP E4M3 conversion, round to nearest even:
-// equal to e4m3fn_from_float for every FP32 input in [-448, 448] (all 2^32 bit
-// patterns were compared on the device).
+// equal to torch's E4M3FN conversion for every FP32 value in [-448, 448] (all
+// compared on the device).
 template <typename IT>
 __device__ __forceinline__ u32x2 quantize8(const float (&x)[8], float s, float y) {
   float q[8];
