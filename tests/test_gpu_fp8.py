@@ -112,6 +112,23 @@ def test_zero_and_nan_blocks(dtype):
         assert enc[i].item() == (0xFF if bits[i] < 0 else 0x7F)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("offset", [1, 3, 8])
+def test_unaligned_views(dtype, offset):
+    """Views that start off a 16-byte boundary take the element-wise loads (source) and
+    byte-wise loads (encoded); bytes, scales and decoded values still equal the reference's."""
+    gen = torch.Generator().manual_seed(offset)
+    base = (torch.randn(5000 + offset, generator=gen) * 3).to(dtype)
+    x = base[offset:]
+    enc, sc = fp8.pack_fp8(base.to(DEV)[offset:])
+    renc, rsc = R.pack_fp8_torch(x)
+    assert same(sc, rsc) and same(enc, renc)
+    padded = torch.cat([torch.zeros(offset, dtype=torch.uint8), renc]).to(DEV)
+    for out in (torch.float16, torch.bfloat16, torch.float32):
+        got = fp8.unpack_fp8(padded[offset:], rsc.to(DEV), out)
+        assert same(got, R.unpack_fp8_torch(renc, rsc, out))
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_unpack_all_codes_bitexact(dtype):
     codes = torch.arange(256, dtype=torch.uint8).repeat(5)
