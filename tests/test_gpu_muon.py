@@ -180,22 +180,34 @@ def test_orthogonalize_without_iterations_is_the_normalised_input(shape):
     assert bool(((out - ref).abs() <= ref.abs() * 2 ** -7).all())
 
 
-@pytest.mark.parametrize("shape", [(128, 256), (100, 300), (45, 70), (96, 96), (1, 300),
-                                   (300, 100), (70, 45), (300, 1), (4100, 1024)])
-def test_muon_step_elementwise_bitexact(shape):
+def on_device(t, offset):
+    """t on the GPU, `offset` elements past the start of a fresh allocation."""
+    buf = torch.zeros(t.numel() + offset, dtype=t.dtype, device=DEV)
+    buf[offset:] = t.reshape(-1).to(DEV)
+    return buf[offset:].view(t.shape)
+
+
+@pytest.mark.parametrize("shape,offset", [
+    ((128, 256), 0), ((100, 300), 0), ((45, 70), 0), ((96, 96), 0), ((1, 300), 0),
+    ((300, 100), 0), ((70, 45), 0), ((300, 1), 0), ((4100, 1024), 0), ((4096, 640), 0),
+    ((256, 640), 1), ((640, 256), 1), ((640, 256), 2)])
+def test_muon_step_elementwise_bitexact(shape, offset):
     """momentum/Nesterov and the master update match the oracle bit for bit: the flat
     passes (X in the stored layout: (128, 256) whole blocks, (100, 300) a partial last
     block, (45, 70) rows not a multiple of 4, (96, 96) square, (1, 300) a single row) and
     the transposing tile passes ((300, 100) and (70, 45) partial tiles only, (300, 1) a
-    single column, (4100, 1024) whole tiles and a partial last band)."""
+    single column, (4100, 1024) whole tiles and a partial last band, (4096, 640) whole
+    momentum tiles and a partial last column of apply tiles); with `offset`, parameter,
+    momentum and gradient start off a 16-byte boundary, so every pass takes its
+    element-wise path."""
     from oracle import reference as R
     gen = torch.Generator().manual_seed(7)
     p0 = torch.randn(shape, generator=gen) * .02
     m0 = torch.randn(shape, generator=gen) * 1e-3
     g = torch.randn(shape, generator=gen) * 1e-3
     lr, wd = .02, .01
-    p, m = p0.to(DEV), m0.to(DEV)
-    muon.muon_step([p], [g.to(DEV)], [m], lr, wd)
+    p, m = on_device(p0, offset), on_device(m0, offset)
+    muon.muon_step([p], [on_device(g, offset)], [m], lr, wd)
     om = m0.numpy().copy()
     u = R.muon_momentum(g.numpy(), om)  # momentum in place, returns the Nesterov blend
     assert_same_bits(m.cpu().numpy(), om, "momentum")
