@@ -62,6 +62,30 @@ def test_accumulate_bitexact_vs_reference_ops(dtype, scale):
     assert abs(window.norm_squared() - ref) <= 1e-12 * ref
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_unaligned_gradient_views(dtype):
+    """Gradients that start off a 16-byte boundary (views one element into their
+    allocation) take the lane-strided path; the window, flag and norm are unchanged."""
+    def on_device(g):
+        if g is None:
+            return None
+        buf = torch.zeros(g.numel() + 1, dtype=g.dtype, device=DEV)
+        buf[1:] = g.reshape(-1).to(DEV)
+        return buf[1:].view(g.shape)
+
+    mbs = micro_batches(dtype, 3, 5, 65536.0)
+    window = G.StageGradients(SHAPES, DEV)
+    window.zero_()
+    for k, grads in enumerate(mbs):
+        window.accumulate([on_device(g) for g in grads], 65536.0, final=(k == len(mbs) - 1))
+    expect = oracle_window(mbs, 65536.0)
+    for got, exp in zip(window.views, expect):
+        assert_same_bits(got.cpu().numpy(), exp.numpy(), "window")
+    assert not window.found_inf()
+    ref = R.norm_squared_torch(expect)
+    assert abs(window.norm_squared() - ref) <= 1e-12 * ref
+
+
 def test_first_pass_turns_negative_zero_into_positive_zero():
     window = G.StageGradients([(5,)], DEV).zero_()
     g = torch.tensor([-0.0, 0.0, -0.0, 1.0, -0.0], dtype=torch.float16, device=DEV)
