@@ -33,6 +33,23 @@ def test_single_poison_anywhere(dtype, n):
             assert detect([h]), (pos, bad)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("offset", [1, 3])
+def test_unaligned_views(dtype, offset):
+    """A gradient view that starts off a 16-byte boundary takes the element path: a
+    non-finite value is found at either end and in the middle, and a finite view
+    (with a poisoned element just before it, outside the view) is not flagged."""
+    n = 10001
+    base = torch.randn(n + offset, generator=torch.Generator().manual_seed(offset)).to(dtype)
+    base[offset - 1] = float("nan")  # outside the view
+    dev = base.cuda()
+    assert not detect([dev[offset:]])
+    for pos in (0, n // 2, n - 1):
+        h = dev.clone()
+        h[offset + pos] = float("inf")
+        assert detect([h[offset:]]), pos
+
+
 def test_finite_extremes_never_flag():
     f16 = torch.tensor([65504., -65504., 6e-8, -6e-8, 0., -0.] * 1000, dtype=torch.float16)
     bf16 = torch.tensor([3.38e38, -3.38e38, 1e-38, 0.] * 1000, dtype=torch.bfloat16)
