@@ -325,6 +325,11 @@ class HybridMuonAdamW:
     uploads the gradients and masters, runs the same kernels on device mirrors,
     and writes the updated masters back into the CPU tensors before returning,
     so the engine's next stage load (engine.py:109-115) reads the new weights.
+    resident_masters=True (CPU masters only) keeps the masters' device mirrors
+    between steps and uploads a master again only when its CPU tensor's storage
+    or version counter changed since the step wrote it back; writes the counter
+    cannot see (through `p.data`, a NumPy view, raw memory) must be followed by
+    invalidate_masters().
     """
 
     def __init__(self, model, lr=1e-3, muon_lr=None, weight_decay=.01, *,
