@@ -424,8 +424,9 @@ size_t morph_muon_workspace_bytes(int64_t rows, int64_t cols, int count);
  * (transposed back when p has more rows than columns, optimizer.py:15-17, 22)
  * and scale = update_scale or update_scale_transposed by the matrix's
  * orientation.  The workspace must be
- * 256-byte aligned and zero-filled once before first use (its zero padding is
- * kept by every call).  Replaces optimizer.py:13-22 and 52-61.
+ * 256-byte aligned; its contents need no initialisation (every call writes
+ * what it reads, zero padding included, so a call on non-finite values leaves
+ * nothing behind).  Replaces optimizer.py:13-22 and 52-61.
  */
 int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
                     const morph_muon_hp* hp, void* workspace, size_t workspace_bytes,

@@ -122,6 +122,19 @@ class StepControl:
     def scaler_changed(self):
         return self._scale_fields()[:3] != self._mirrored
 
+    def host_fields(self):
+        """The host scaler's (scale, good_steps) as the caller last set them."""
+        return self._scale_fields()[:2]
+
+    def restore_host_fields(self, fields):
+        """Put back host scaler fields that a mirror() overwrote (dynamic scalers only)."""
+        s = self.loss_scale
+        scale, good = fields
+        if isinstance(s, DynamicLossScale):
+            s._scale, s._good_steps = scale, good
+        elif hasattr(s, "overflow") and hasattr(s, "success"):
+            s.scale, s.good_steps = scale, good
+
     def read(self):
         """Synchronously copy the state block to the host."""
         self._host.copy_(self.state)

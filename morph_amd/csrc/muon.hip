@@ -24,11 +24,13 @@
 // to B's diagonal before its bf16 rounding; measured against the FP32
 // reference this is as accurate as the separate a X term or more).
 //
-// Workspace (caller-allocated, zero-filled once; morph_muon_workspace_bytes):
+// Workspace (caller-allocated, morph_muon_workspace_bytes; no initial contents needed):
 // per-block partial sums f64; per-matrix 1/den, 1/den^2, den f32;
 // X0/X1 [count][Mp][Np] (iterations alternate: X' = B' X reads all of X as its
 // [K, N] operand, so it cannot overwrite it), A and B' [count][Mp][Mp], bf16,
-// with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.  The
+// with m = min(rows, cols), n = max, Mp/Np rounded up to the GEMM tile.  prepare
+// writes X0 including its zero padding (pad_zero_kernel) and every product
+// rewrites its whole padded output, so no call depends on an earlier one.  The
 // zero padding is exact for Newton-Schulz: padded rows of X give zero rows and
 // columns of A, and of B' apart from its diagonal (a on every diagonal
 // element), so a padded row of X' is a times the padded row of X: zero again.
@@ -396,6 +398,28 @@ __global__ __launch_bounds__(kBlock) void norm_kernel(MatPtrs mats, const double
   }
 }
 
+// Zero padding of X0: columns n .. np - 1 of rows 0 .. m - 1 and all np columns
+// of rows m .. mp - 1, per matrix (blockIdx.y).  Every product rewrites its
+// whole padded output from its inputs, so X0's padding is the only one a call
+// inherits; the chain writes X0 in its second iteration, and a non-finite
+// input leaves NaN there (0 * NaN), so every prepare restores the zeros.
+__global__ __launch_bounds__(kBlock) void pad_zero_kernel(uint16_t* x_all, int64_t m, int64_t n,
+                                                          int64_t mp, int64_t np, int64_t ldn) {
+  uint16_t* xm = x_all + (int64_t)blockIdx.y * mp * ldn;
+  const int64_t tail = np - n, per_row = tail > 0 ? tail : 0;
+  const int64_t total = m * per_row + (mp - m) * np;
+  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kBlock) {
+    if (i < m * per_row) {
+      const int64_t r = i / per_row;
+      xm[r * ldn + n + (i - r * per_row)] = 0;
+    } else {
+      const int64_t j = i - m * per_row, r = m + j / np;
+      xm[r * ldn + (j - (r - m) * np)] = 0;
+    }
+  }
+}
+
 // Without Newton-Schulz iterations X itself is the result: X = bf16(X0 / den)
 // over the whole padded buffer (zero padding stays zero).
 __global__ __launch_bounds__(kBlock) void rescale_kernel(uint16_t* x_all, const float* den,
@@ -634,6 +658,13 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
   const MatPtrs flat = pointers(mats, count, rows, cols, Orient::kStored, &n_flat);
   const MatPtrs tiled = pointers(mats, count, rows, cols, Orient::kTransposed, &n_tiled);
   const float mw = hp->momentum_weight, nw = hp->nesterov_weight;
+  if (L.mp != L.m || L.np != L.n) {
+    const int64_t pad = L.m * (L.np - L.n) + (L.mp - L.m) * L.np;
+    const int64_t bx = std::min<int64_t>((pad + kBlock - 1) / kBlock, 1024);
+    hipLaunchKernelGGL(pad_zero_kernel, dim3((unsigned)bx, count), dim3(kBlock), 0, s, W.X[0],
+                       L.m, L.n, L.mp, L.np, L.ldn);
+    if ((rc = launch_status())) return rc;
+  }
   if (n_flat) {
     const dim3 ew((unsigned)L.blocks, n_flat);
     if (orth_only)
@@ -768,6 +799,7 @@ extern "C" int morph_muon_finish_range(const morph_muon_matrix* mats, int count,
                                        int64_t cols, const morph_muon_hp* hp,
                                        int orthogonalize_only, int first, int n, void* workspace,
                                        size_t workspace_bytes, void* stream) {
+  if (first < 0 || n < 0) return MORPH_EINVAL;  // n = -1 ("the rest") is internal only
   return finish(mats, count, rows, cols, hp, workspace, workspace_bytes, orthogonalize_only != 0,
                 stream, first, n);
 }

@@ -186,6 +186,12 @@ def export_fp16(state_dir, output, chunk_elements=1048576, lock_held=False, *, m
         encoder = _Encoder(device, chunk_elements, segment_elements)
         slots = threading.Semaphore(max(1, hash_threads))
         writers = []
+
+        def failed():
+            # a writer's error ends production: the reference's serial loop stops at its
+            # first error, so no shard is started, and no segment encoded, after one
+            return any(w.error is not None for _, _, w in writers)
+
         try:
             for name, entry in entries.items():
                 size = entry["size"]
@@ -194,12 +200,18 @@ def export_fp16(state_dir, output, chunk_elements=1048576, lock_held=False, *, m
                 mapped = None if resident else np.memmap(
                     state_dir / entry["file"], dtype=np.float32, mode="r", shape=(3, size))
                 slots.acquire()
+                if failed():
+                    slots.release()
+                    break
                 writer = _ShardWriter(output / entry["file"], chunk_elements, slots)
                 writer.start()
                 writers.append((name, entry, writer))
                 bad = False
                 try:
                     for lo in range(0, size, encoder.segment):
+                        if failed():
+                            bad = True
+                            break
                         hi = min(lo + encoder.segment, size)
                         encoded, flags = encoder.encode(
                             lo, hi, mapped_row=None if resident else mapped[0], row_dev=row_dev)

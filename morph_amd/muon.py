@@ -68,12 +68,11 @@ class Workspaces:
     """Device workspaces of the Muon batches, one per (shape, device, batch index), each
     sized for the largest matrix count it has served.
 
-    The workspace layout depends on the batch's matrix count, and the kernels rely
-    on its zero padding (zero-filled once, then kept by every call of the same
-    layout).  A call with another count than the workspace's last is therefore
-    preceded by a zero fill of the part it uses, on the call's stream.  Streams
-    that used a workspace are recorded, so that a workspace replaced by a larger
-    one stays allocated until their queued work is done.
+    A call needs no particular contents: morph_muon_prepare writes the Newton-Schulz
+    operand with its zero padding every time and each product rewrites its whole
+    output, so a call on non-finite values leaves nothing behind for the next.
+    Streams that used a workspace are recorded, so that a workspace replaced by a
+    larger one stays allocated until their queued work is done.
     """
 
     def __init__(self):
@@ -91,13 +90,9 @@ class Workspaces:
                 for s in entry["streams"]:
                     entry["buf"].record_stream(s)
             with torch.cuda.stream(stream):
-                entry = dict(buf=torch.zeros(nbytes, dtype=torch.uint8, device=device),
-                             count=count, streams=set())
+                entry = dict(buf=torch.empty(nbytes, dtype=torch.uint8, device=device),
+                             streams=set())
             self._ws[key] = entry
-        elif entry["count"] != count:
-            with torch.cuda.stream(stream):
-                entry["buf"][:nbytes].zero_()
-            entry["count"] = count
         entry["streams"].add(stream)
         return entry["buf"]
 
@@ -291,12 +286,18 @@ def muon_step(params, grads, momenta, lr, weight_decay, steps=NS_STEPS, stream=N
     _complete(batches, stream, timer)
 
 
-def _host_grad(p):
-    g = p.grad
-    if g.device.type != "cpu" or g.dtype != torch.float32 or g.shape != p.shape:
-        raise ValueError("with CPU masters the Muon gradients are CPU float32 tensors of the "
+def _muon_grad(g, p, device):
+    """A Muon gradient of a CPU master: a float32 tensor of the parameter's shape, in CPU
+    memory (uploaded through the staging) or on the optimizer's GPU (read in place)."""
+    if g.dtype != torch.float32 or g.shape != p.shape:
+        raise ValueError("with CPU masters the Muon gradients are float32 tensors of the "
                          "parameter's shape")
-    return g.contiguous()
+    if g.device.type == "cpu":
+        return g.contiguous()
+    if g.device != device:
+        raise ValueError(f"a Muon gradient is on {g.device}; the optimizer works on {device}")
+    _check_matrix(g, "gradient")
+    return g
 
 
 def partition(model):
@@ -407,28 +408,38 @@ class HybridMuonAdamW:
             self.adam.zero_grad(set_to_none=set_to_none)
 
     @torch.no_grad()
-    def step(self):
+    def step(self, grads=None):
         """The gate of optimizer.py:49-51 covers every gradient: the AdamW group's
         by the detector, the Muon matrices' inside their momentum pass (which
         writes only scratch buffers until the gate has passed).  With CPU masters
         every gradient is uploaded before the gate, and the masters go up and
-        come back only after it has passed (_host_step)."""
-        live = [(i, p) for i, p in enumerate(self.muon) if p.grad is not None]
+        come back only after it has passed (_host_step).
+
+        grads: optional {parameter: gradient} used instead of p.grad (a parameter
+        missing from it has no gradient this step).  With CPU masters a gradient
+        may be a float32 tensor on the GPU -- an engine's device stage buffer
+        (Slot.grad_device, engine.py:67) before its flush to p.grad
+        (engine.py:75-88) -- which the step reads where it is, with no upload."""
+        if grads is None:
+            grad_of = lambda p: p.grad  # noqa: E731
+        else:
+            grad_of = grads.get
+        live = [(i, p) for i, p in enumerate(self.muon) if grad_of(p) is not None]
         adam_params = [p for g in (self.adam.param_groups if self.adam else []) for p in g["params"]]
-        adam_present = [k for k, p in enumerate(adam_params) if p.grad is not None]
+        adam_grads = [grad_of(p) for p in adam_params]
+        adam_present = [k for k, g in enumerate(adam_grads) if g is not None]
         if not live and not adam_present:
             return
         idx = [i for i, _ in live]
         if self.host and live:
-            return self._host_step(live, idx, adam_params, adam_present)
+            return self._host_step(live, idx, adam_params, adam_grads, adam_present, grad_of)
         if self.host:
             device = self.adam.device
             muon_grads = []
-            adam_grads = self.adam._stage_in([p.grad for p in adam_params], adam_present)
+            adam_grads = self.adam._stage_in(adam_grads, adam_present)
         else:
             device = (live[0][1] if live else adam_params[adam_present[0]]).device
-            muon_grads = [p.grad for _, p in live]
-            adam_grads = [p.grad for p in adam_params]
+            muon_grads = [grad_of(p) for _, p in live]
         if self._flag is None:
             self._flag = kernels.new_flag(device)
         kernels.flag_clear(self._flag)
@@ -463,15 +474,19 @@ class HybridMuonAdamW:
             self.momentum[i], self._momentum_next[i] = self._momentum_next[i], self.momentum[i]
 
     def _adam_after_gate(self, adam_grads, adam_present):
+        """The AdamW group's step.  The gate's detector has already seen every one of
+        its gradients finite (the flag it read covers them), and the group has no loss
+        scale, so the step's found_inf word stays clear: checked=True runs the fused
+        pass without a second detector scan."""
         if not adam_present:
             return
         if self.host:
-            self.adam._enqueue(adam_grads, adam_present, None, False)
+            self.adam._enqueue(adam_grads, adam_present, None, True)
             self.adam._stage_out(adam_present)
         else:
-            self.adam.step()
+            self.adam.step(adam_grads, checked=True)
 
-    def _host_step(self, live, idx, adam_params, adam_present):
+    def _host_step(self, live, idx, adam_params, adam_grads, adam_present, grad_of):
         """step() with CPU masters.  The Muon matrices go through in stream_parts
         parts: each part's gradients go up, then its momentum pass (which writes
         only scratch buffers and the non-finite flag) and its Newton-Schulz chain
@@ -485,7 +500,7 @@ class HybridMuonAdamW:
         device = self._muon_dev[0].device
         stream = torch.cuda.current_stream(device)
         masters = [p for _, p in live]
-        grads = [_host_grad(p) for _, p in live]
+        grads = [_muon_grad(grad_of(p), p, device) for _, p in live]
         self._muon_masters._check(masters, idx)  # fail before anything is enqueued
         self._ensure_momenta(idx)
         if self._flag is None:
@@ -497,22 +512,15 @@ class HybridMuonAdamW:
         kernels.flag_clear(self._flag, stream)
         parts = []
         try:
-            self._host_step_on(live, idx, masters, grads, adam_params, adam_present, stream, ns,
+            # the chains may run on non-finite values before the gate raises; the next
+            # step's prepare rewrites everything of the workspaces that its chains read
+            self._host_step_on(live, idx, masters, grads, adam_grads, adam_present, stream, ns,
                                parts)
-        except BaseException:
-            # The chains already ran, possibly on non-finite values, which turn the
-            # workspaces' zero padding into NaN (0 * inf): restore it, after them, so
-            # the next step starts from the state the kernels rely on.
-            stream.wait_stream(ns)
-            for batches in parts:
-                for batch in batches:
-                    batch[-1].zero_()
-            raise
         finally:
             # later work on `stream` (the next step's momentum pass) follows the chains
             stream.wait_stream(ns)
 
-    def _host_step_on(self, live, idx, masters, grads, adam_params, adam_present, stream, ns,
+    def _host_step_on(self, live, idx, masters, grads, adam_grads, adam_present, stream, ns,
                       parts):
         nparts = max(1, min(int(self.stream_parts), len(live)))
         bounds = [len(live) * k // nparts for k in range(nparts + 1)]
@@ -520,11 +528,16 @@ class HybridMuonAdamW:
         for k in range(nparts):
             pos = range(bounds[k], bounds[k + 1])
             part = [idx[j] for j in pos]
-            # wait=False: nothing queued reads the gradient mirrors (the last step's
-            # momentum passes finished before its masters came back)
-            self._muon_grads.upload([grads[j] for j in pos], part, stream, wait=False)
-            items = [(self._muon_dev[i], self._muon_grads.views[i], self.momentum[i],
-                      self._momentum_next[i]) for i in part]
+            # CPU gradients go up (device ones are read in place).  wait=False: nothing
+            # queued reads the gradient mirrors (the last step's momentum passes
+            # finished before its masters came back)
+            up = [j for j in pos if grads[j].device.type == "cpu"]
+            if up:
+                self._muon_grads.upload([grads[j] for j in up], [idx[j] for j in up], stream,
+                                        wait=False)
+            items = [(self._muon_dev[idx[j]],
+                      self._muon_grads.views[idx[j]] if grads[j].device.type == "cpu" else grads[j],
+                      self.momentum[idx[j]], self._momentum_next[idx[j]]) for j in pos]
             batches = []
             for (rows, cols), group in _by_shape(items).items():
                 batches += _prepare(group, rows, cols,
@@ -539,8 +552,7 @@ class HybridMuonAdamW:
             done = torch.cuda.Event()
             done.record(ns)
             ready.append(done)
-        adam_grads = (self.adam._stage_in([p.grad for p in adam_params], adam_present)
-                      if adam_present else None)
+        adam_grads = self.adam._stage_in(adam_grads, adam_present) if adam_present else None
         if adam_present:
             kernels.nonfinite_or([adam_grads[k] for k in adam_present], self._flag)
         if self._flag.item():

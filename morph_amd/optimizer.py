@@ -398,8 +398,15 @@ class FusedAdamW:
         masters, streamed through the update by HostStaging.pipeline (the launch
         timers do not apply)."""
         flat = self._flat()
-        if self._ctl.scaler_changed():  # the caller edited the scaler: resync the device copy
-            self.resolve()
+        if self._ctl.scaler_changed():
+            # the caller set the scaler (scale, good_steps, load_state_dict) since the last
+            # step: wait for the queued steps, then the caller's values replace what they
+            # left on the device (the wait's mirror() would otherwise overwrite them)
+            fields = self._ctl.host_fields()
+            try:
+                self.resolve()
+            finally:
+                self._ctl.restore_host_fields(fields)
             self._ctl.push_scale()
         batch, clock_list, hps, scheds = self._prepare(grads, present)
         # everything that can fail is done before the first launch is enqueued

@@ -44,6 +44,9 @@ class DynamicLossScale:
 
     @scale.setter
     def scale(self, value):
+        # the owner's queued steps come first in program order: settle them, then
+        # the assignment wins (the owner pushes it to the device at its next step)
+        self._settle()
         self._scale = value
 
     @property
@@ -53,6 +56,7 @@ class DynamicLossScale:
 
     @good_steps.setter
     def good_steps(self, value):
+        self._settle()
         self._good_steps = value
 
     def attach(self, owner):

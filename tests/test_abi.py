@@ -121,6 +121,23 @@ def test_muon_matrix_flags_are_validated():
                                    1 << 40, None) == -1
 
 
+@no_gpu_visible
+def test_muon_finish_range_rejects_ranges_outside_the_batch():
+    """0 <= first, 0 <= n, first + n <= count: n = -1 is not "the rest of the batch"."""
+    from morph_amd import _lib
+    lib = _lib.lib()
+    p = 0x10000
+    hp = _lib.MuonHP()
+    hp.ns_steps = 5
+    arr = (_lib.MuonMatrix * 2)()
+    for i in range(2):
+        arr[i].grad, arr[i].momentum, arr[i].param = p, p, p
+    fin = lambda first, n: lib.morph_muon_finish_range(arr, 2, 256, 512, ctypes.byref(hp), 0,
+                                                       first, n, ctypes.c_void_p(p), 1 << 40, None)
+    for first, n in ((0, -1), (-1, 1), (1, 2), (3, 0), (0, 3)):
+        assert fin(first, n) == -1, (first, n)
+
+
 # (ctypes class, C type) pairs whose layouts must agree field by field
 STRUCTS = [("AdamwHP", "morph_adamw_hp"), ("AdamwTensor", "morph_adamw_tensor"),
            ("StepState", "morph_step_state"), ("AdamwSched", "morph_adamw_sched"),

@@ -133,3 +133,27 @@ def test_export_from_resident_window_equals_file_export(tmp_path):
                 segment_elements=600)
     R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, 300)
     same_dirs(tmp_path / "win", tmp_path / "cpu")
+
+
+def test_a_failed_shard_write_stops_the_export(tmp_path, monkeypatch):
+    """The reference's serial loop (export.py:26-36) stops at its first I/O error, so the
+    output holds the shards up to the failing one.  With one shard writer at a time the
+    GPU export ends the same way: the first shard's fsync fails, the error propagates,
+    and no later shard is started."""
+    import os as os_mod
+    from morph_amd import export as export_mod
+    model = Tiny()
+    make_state(tmp_path / "run" / "state", model)
+    real_fsync = os_mod.fsync
+    calls = []
+
+    def failing_fsync(fd):
+        calls.append(fd)
+        if len(calls) == 1:
+            raise OSError(5, "injected I/O error")
+        return real_fsync(fd)
+
+    monkeypatch.setattr(export_mod.os, "fsync", failing_fsync)
+    with pytest.raises(OSError, match="injected"):
+        export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", 100, model=model, hash_threads=1)
+    assert sorted(p.name for p in (tmp_path / "gpu").iterdir()) == ["00000.bin"]

@@ -287,6 +287,50 @@ def test_hybrid_on_cpu_masters_equals_device_masters(model_cls, pinned, parts):
         assert torch.equal(opt_c.momentum[i].cpu(), m.cpu()), i
 
 
+@pytest.mark.parametrize("model_cls,which", [(Tiny, "all"), (Tiny, "some"), (Uneven, "all"),
+                                             (Uneven, "muon")])
+def test_hybrid_on_cpu_masters_takes_device_gradients(model_cls, which):
+    """step({p: g}) with gradients on the GPU (an engine's device stage buffers,
+    engine.py:67, before Slot.flush copies them to CPU p.grad, :75-88): no gradient
+    upload for those, and the same bits as the CPU-gradient step over three steps --
+    masters, momenta, AdamW moments -- with every gradient on the device, every other
+    one, or only the Muon ones.  A parameter missing from the mapping is not stepped."""
+    torch.manual_seed(5)
+    model_a = model_cls()
+    model_b = copy.deepcopy(model_a)
+    opt_a = HybridMuonAdamW(model_a, lr=.003, muon_lr=.02)
+    opt_b = HybridMuonAdamW(model_b, lr=.003, muon_lr=.02)
+    muon_ids = {id(p) for p in opt_b.muon}
+    names = [n for n, _ in model_a.named_parameters()]
+    for step in range(3):
+        _engine_grads(model_a, 20 + step)
+        skip = names[-1] if step == 1 else None   # absent from the mapping this step
+        grads = {}
+        for k, ((n, pa), (_, pb)) in enumerate(zip(model_a.named_parameters(),
+                                                   model_b.named_parameters())):
+            if n == skip:
+                pa.grad = None
+                continue
+            on_device = (which == "all" or (which == "some" and k % 2 == 0)
+                         or (which == "muon" and id(pb) in muon_ids))
+            grads[pb] = pa.grad.to(DEV) if on_device else pa.grad.clone()
+        before = opt_b._muon_grads.bytes_h2d
+        opt_a.step()
+        opt_b.step(grads)
+        if which in ("all", "muon"):
+            assert opt_b._muon_grads.bytes_h2d == before  # no Muon gradient went up
+        assert all(p.grad is None for p in model_b.parameters())
+    for (n, pa), (_, pb) in zip(model_a.named_parameters(), model_b.named_parameters()):
+        assert pb.device.type == "cpu"
+        assert torch.equal(pa.detach(), pb.detach()), n
+    for i, m in opt_a.momentum.items():
+        assert torch.equal(m.cpu(), opt_b.momentum[i].cpu()), i
+    sa, sb = opt_a.state_dict()["adam"]["state"], opt_b.state_dict()["adam"]["state"]
+    for k in sa:
+        for key in ("exp_avg", "exp_avg_sq", "step"):
+            assert torch.equal(sa[k][key], sb[k][key]), (k, key)
+
+
 def test_optimizers_sharing_the_copy_streams_interleave():
     """Every staging object and the Muon side stream use one stream per role and device
     (staging.shared_stream).  Two CPU-master optimizers stepped alternately through those
