@@ -33,7 +33,7 @@ import time
 
 import torch
 
-from . import kernels
+from . import arena, kernels
 from ._lib import check, dtype_code, lib, stream_handle
 from .hyper import disk_constants
 from .staging import shared_stream
@@ -104,7 +104,7 @@ class ResidentWindow:
         slots = self._slots()
         for name in (self.names if names is None else names):
             size = int(self.store.entries[name]["size"])
-            dev = torch.empty((3, size), dtype=torch.float32, device=self.device)
+            dev = _state_rows(size, self.device)
             # allocated on the compute stream, which may still have work queued on this memory
             self._copy.wait_stream(compute)
             fd = os.open(self._path(name), os.O_RDONLY)
@@ -217,6 +217,24 @@ class ResidentWindow:
         finally:
             self._copy.synchronize()
             os.close(fd)
+
+
+def _state_rows(size, device):
+    """A [3, size] float32 device view (weight, exp_avg, exp_avg_sq: the file's rows) laid
+    out like a FusedAdamW arena (morph_amd.arena): when a row is 2 MiB or more, row k starts
+    at a 2 MiB boundary + k * 64 KiB.  One plain [3, size] tensor puts the rows exactly
+    size * 4 bytes apart -- for the config-2 matrices 36 x 2 MiB, every stream on the same
+    2 MiB phase, the placement the fused pass streams slowest from."""
+    nbytes = 4 * size
+    if nbytes >= arena.ALIGN_LARGE:
+        stride = (arena._align(nbytes, arena.ALIGN_LARGE) + arena.STAGGER) // 4
+    else:
+        stride = arena._align(max(nbytes, 4), arena.ALIGN_SMALL) // 4
+    # room to move the first row up to the next 2 MiB boundary
+    storage = torch.empty(2 * stride + size + arena.ALIGN_LARGE // 4, dtype=torch.float32,
+                          device=device)
+    base = ((-storage.data_ptr()) % arena.ALIGN_LARGE) // 4
+    return storage.as_strided((3, size), (stride, 1), base)
 
 
 def _read_exact(fd, out, offset):

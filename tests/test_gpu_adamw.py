@@ -136,6 +136,36 @@ def test_multi_tensor_launch_splits_and_mixes_constants():
         assert_same_bits(export_bits(o), oo, f"export[{i}]")
 
 
+def test_launch_larger_than_the_infinity_cache_runs_descending_bit_exact():
+    """A launch whose gradients exceed 256 MB runs its chunks in descending order (it reads
+    the gradient lines the detector left in the Infinity Cache first).  Elementwise, so the
+    bits are the ascending order's: three FP32-gradient tensors (288 MB of gradients in
+    one launch) with ragged sizes, one of them an unaligned view (scalar path), against
+    the oracle over two steps with different constants."""
+    from oracle import reference as R
+    sizes = [40_000_003, 31_999_997, 5]
+    offsets = [0, 1, 0]
+    cases = [make_case(n, torch.float32, 300 + i, offset=o)
+             for i, (n, o) in enumerate(zip(sizes, offsets))]
+    assert sum(4 * n for n in sizes) > 256 << 20
+    views = [[t.to(DEV)[o:] for t in c] for c, o in zip(cases, offsets)]
+    outs = [torch.empty(n, dtype=torch.float16, device=DEV) for n in sizes]
+    batch = kernels.AdamwBatch([v[0] for v in views], [v[1] for v in views],
+                               [v[2] for v in views], [v[3] for v in views], outs)
+    ora = [[to_oracle(t[o:]).copy() for t in c] for c, o in zip(cases, offsets)]
+    for step in (1, 2):
+        batch.launch([hyper.adamw_constants(lr=3e-4 * step, beta1=.9, beta2=.95, eps=1e-8,
+                                            weight_decay=.1, step=step)])
+        ohp = R.torch_adamw_hp(3e-4 * step, .9, .95, 1e-8, .1, step)
+        oouts = [R.adamw(o[3], o[0], o[1], o[2], ohp, out_dtype=R.DTYPE_F16) for o in ora]
+    torch.cuda.synchronize()
+    for i, (v, o, out, oo) in enumerate(zip(views, ora, outs, oouts)):
+        assert_same_bits(v[0].cpu().numpy(), o[0], f"master[{i}]")
+        assert_same_bits(v[1].cpu().numpy(), o[1], f"exp_avg[{i}]")
+        assert_same_bits(v[2].cpu().numpy(), o[2], f"exp_avg_sq[{i}]")
+        assert_same_bits(export_bits(out), oo.view(np.uint16), f"export[{i}]")
+
+
 def test_special_values_in_masters_and_grads():
     """Subnormal, zero, huge and export-overflowing values round like the oracle."""
     from oracle import reference as R
