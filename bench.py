@@ -754,7 +754,7 @@ def embedding_main(args):
     print(json.dumps(line), flush=True)
 
 
-def time_streamed(steps, warmup, muon=False, pinned=False, resident=False):
+def time_streamed(steps, warmup, muon=False, pinned=False, resident=False, device_grads=False):
     """The streamed engines' layout (runner.py:41-46, engine.py:75-88): FP32 masters and
     FP32 (already unscaled) gradients in pageable CPU memory, optimizer state resident in
     HBM.  A step uploads every gradient and master through pinned staging, runs the
@@ -764,7 +764,10 @@ def time_streamed(steps, warmup, muon=False, pinned=False, resident=False):
     pinned=True: the masters are moved into page-locked memory first (pin_host_tensors),
     so they cross PCIe by DMA alone; the gradients stay pageable, as the engine leaves
     them.  resident=True: the optimizers keep the masters' device mirrors between steps
-    (resident_masters), so only the gradients go up and the masters come back."""
+    (resident_masters), so only the gradients go up and the masters come back.
+    device_grads=True: the gradients are handed to step() as FP32 tensors on the GPU (the
+    engine's device stage buffers, engine.py:67, before Slot.flush copies them to CPU
+    p.grad), so no gradient crosses PCIe."""
     from morph_amd import FusedAdamW, pin_host_tensors
     from morph_amd.muon import HybridMuonAdamW
     cpus = host_cpus()  # the host copies run on torch's intra-op threads
@@ -786,18 +789,24 @@ def time_streamed(steps, warmup, muon=False, pinned=False, resident=False):
             pin_host_tensors(params)
         opt = FusedAdamW(params, **HYPER, resident_masters=resident)
         stagings = [opt._staging]
-    for _ in range(warmup):
-        opt.step()
-    if not muon:
-        stagings.append(opt._grad_staging)
+    if device_grads:
+        device = torch.device("cuda", torch.cuda.current_device())
+        dev = [p.grad.to(device) for p in params]
+        hand = dict(zip(params, dev)) if muon else dev
+        step = lambda: opt.step(hand)  # noqa: E731
     else:
-        stagings.append(opt.adam._grad_staging)
+        step = opt.step
+    for _ in range(warmup):
+        step()
+    grad_staging = opt.adam._grad_staging if muon else opt._grad_staging
+    if grad_staging is not None:
+        stagings.append(grad_staging)
     torch.cuda.synchronize()
     h2d0 = sum(st.bytes_h2d for st in stagings)
     d2h0 = sum(st.bytes_d2h for st in stagings)
     t0 = time.perf_counter()
     for _ in range(steps):
-        opt.step()  # returns with the new masters in the CPU tensors
+        step()  # returns with the new masters in the CPU tensors
     elapsed = time.perf_counter() - t0
     torch.cuda.synchronize()
     return dict(elapsed=elapsed, n=sum(p.numel() for p in params), cpus=cpus,
@@ -806,7 +815,8 @@ def time_streamed(steps, warmup, muon=False, pinned=False, resident=False):
 
 
 def streamed_main(args, muon=False):
-    r = time_streamed(args.steps, args.warmup, muon, args.pinned, args.resident_masters)
+    r = time_streamed(args.steps, args.warmup, muon, args.pinned, args.resident_masters,
+                      args.device_grads)
     n, t = r["n"], r["elapsed"] / args.steps
     line = {
         "metric": ("HybridMuonAdamW step" if muon else "AdamW step") + " with CPU FP32 masters "
@@ -816,15 +826,21 @@ def streamed_main(args, muon=False):
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": ("config 5 (42 x [3072, 6144] Muon + 326 AdamW vectors)" if muon
                                 else "config-2 window (N = 56,623,104)") +
-                               (" with FP32 masters in pinned and FP32 gradients in pageable CPU "
-                                "memory (pin_host_tensors); " if args.pinned else
-                                " with FP32 masters and FP32 gradients in pageable CPU memory; ") +
-                               "state resident in HBM; step = upload gradients" +
-                               (" (masters' device mirrors kept between steps, "
-                                "resident_masters)" if args.resident_masters else
-                                " and masters") +
-                               ", device step, masters back into the CPU tensors",
+                               (" with FP32 masters in pinned" if args.pinned else
+                                " with FP32 masters in pageable") +
+                               (" CPU memory (pin_host_tensors)" if args.pinned else " CPU memory") +
+                               (" and FP32 gradients on the GPU (step(grads): the engine's device "
+                                "stage buffers); " if args.device_grads else
+                                " and FP32 gradients in pageable CPU memory; ") +
+                               "state resident in HBM; step = " +
+                               ", ".join(
+                                   (["upload gradients"] if not args.device_grads else []) +
+                                   (["upload masters"] if not args.resident_masters else
+                                    ["masters' device mirrors kept between steps "
+                                     "(resident_masters)"]) +
+                                   ["device step", "masters back into the CPU tensors"]),
                    "params": n, "masters": "pinned" if args.pinned else "pageable",
+                   "gradients": "device" if args.device_grads else "pageable",
                    "resident_masters": bool(args.resident_masters)},
         "pcie": {"h2d_bytes_per_step": int(r["h2d"]), "d2h_bytes_per_step": int(r["d2h"]),
                  "h2d_plus_d2h_gb_per_s": round((r["h2d"] + r["d2h"]) / t / 1e9, 2),
@@ -1004,6 +1020,9 @@ def main():
     ap.add_argument("--resident-masters", action="store_true",
                     help="streamed / streamed_muon: keep the masters' device mirrors between "
                          "steps (resident_masters=True), so only gradients cross PCIe upward")
+    ap.add_argument("--device-grads", action="store_true",
+                    help="streamed / streamed_muon: hand the gradients to step() as FP32 tensors "
+                         "on the GPU (the engine's device stage buffers): no gradient upload")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()
