@@ -337,13 +337,15 @@ def muon_main(args):
                                "Muon (5 NS iterations, bf16 MFMA, lr .02, momentum .95) + "
                                f"{r['n_adam']} AdamW params", "muon_params": r["n_muon"]},
         "ns_ms_per_step": round(r["ns_s"] * 1e3, 3),
+        "ns_includes": "the FP32 master update, which the last X' = B' X launch applies in its "
+                       "epilogue (morph_muon_newton_schulz_finish); no separate finish pass",
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic(TRAFFIC_PROFILE_MUON),
                      "traffic_source": TRAFFIC_SOURCE % TRAFFIC_PROFILE_MUON.name
                      + "; the mean over the three products' launches",
-                     "kernel": "gemm_kernel (3 launches per Newton-Schulz iteration, all 42 "
-                               "matrices batched)",
+                     "kernel": "gemm_kernel / gemm_apply_kernel (3 launches per Newton-Schulz "
+                               "iteration, all 42 matrices batched; the last carries the update)",
                      "flops_per_step": r["executed"],
                      "flops_counted": "executed by the MFMAs: the symmetric products A and B' "
                                       "compute 78 of 144 tiles per matrix",

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 7
+#define MORPH_ABI_VERSION 8
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -476,6 +476,21 @@ int morph_muon_finish(const morph_muon_matrix* mats, int count, int64_t rows, in
 int morph_muon_finish_range(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
                             const morph_muon_hp* hp, int orthogonalize_only, int first, int n,
                             void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * morph_muon_newton_schulz followed by morph_muon_finish (the master update,
+ * not orthogonalize_only), after morph_muon_prepare, with the same bits.  When
+ * the batch's operand has no padding (min(rows, cols) and max(rows, cols)
+ * multiples of 256) and every param is 16-byte aligned, the last product
+ * X' = B' X updates the parameters in its epilogue instead of storing X' (the
+ * update runs while other tiles still compute, and the finish pass's reads of
+ * X and p become the epilogue's reads of p); the last iteration's X is then not
+ * written to the workspace.  Otherwise the two phases run as they are.
+ * morph_muon_step uses it.  Replaces optimizer.py:19-22 and 60-61 for a batch.
+ */
+int morph_muon_newton_schulz_finish(const morph_muon_matrix* mats, int count, int64_t rows,
+                                    int64_t cols, const morph_muon_hp* hp, void* workspace,
+                                    size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

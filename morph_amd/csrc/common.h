@@ -56,6 +56,17 @@ __device__ __forceinline__ uint32_t float_to_bf16_bits(float f) {
   return (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
 }
 
+// The Muon master update of one element (streamtrain/optimizer.py:60-61):
+// update = U * scale with U the bf16 Newton-Schulz result, then
+// p.mul_(1 - lr * wd).add_(update, alpha=-lr), which torch's CPU kernels round
+// as fma(update, -lr, p * decay).  Shared by the finish pass and the epilogue
+// of the last Newton-Schulz product, so both give the same bits.
+__device__ __forceinline__ float muon_update_element(float p, uint32_t u16, float scale,
+                                                     float decay, float neg_lr) {
+  const float upd = bf16_bits_to_float(u16) * scale;
+  return __fmaf_rn(upd, neg_lr, p * decay);
+}
+
 // Tag types for the element formats of gradients and export copies.
 struct F32 {};
 struct F16 {};

@@ -74,6 +74,12 @@
 // A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32] for i < 8; output
 // register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
 //
+// The last product of a Muon step's chain can carry the FP32 master update
+// instead of storing X' (gemm_apply_kernel, gemm_kn_apply): the epilogue stages
+// bf16(X') through the LDS tile exactly as for the store, then updates the
+// parameter tile (p rows = tile rows, or = tile columns through transposing LDS
+// reads for a parameter stored transposed) with the finish pass's arithmetic.
+//
 // Dimensions must be multiples of the tile (M, N of 256, K of 64): callers pad
 // with zeros, which is exact for Newton-Schulz (zero rows stay zero).
 #include "common.h"
@@ -313,10 +319,9 @@ __device__ __forceinline__ void store_tile_t(const uint16_t* E, uint16_t* dst, u
 // registers, so D and C move through the row-major LDS tile with one 64-bit access
 // per four values (T, the transposed copy, with transposing reads).
 template <int kDMode, bool kScaled, bool kDiag = false>
-__device__ __forceinline__ void epilogue_rows(const GemmArgs& g, float alpha, float beta,
-                                              f32x16 (&acc)[4][4], uint16_t* smem,
-                                              const uint16_t* D, uint16_t* C, uint16_t* T,
-                                              int64_t ldt, bool diag_tile = false) {
+__device__ __forceinline__ void stage_rows(const GemmArgs& g, float alpha, float beta,
+                                           f32x16 (&acc)[4][4], uint16_t* smem,
+                                           const uint16_t* D, bool diag_tile = false) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = (wave >> 1) * 128, wc = (wave & 1) * 128;
   const int fr = lane & 31, fh = lane >> 5;
@@ -376,15 +381,113 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& g, float alpha, fl
             u32x2{pack_bf16x2(x[4 * q], x[4 * q + 1]), pack_bf16x2(x[4 * q + 2], x[4 * q + 3])};
     }
   }
+}
+
+template <int kDMode, bool kScaled, bool kDiag = false>
+__device__ __forceinline__ void epilogue_rows(const GemmArgs& g, float alpha, float beta,
+                                              f32x16 (&acc)[4][4], uint16_t* smem,
+                                              const uint16_t* D, uint16_t* C, uint16_t* T,
+                                              int64_t ldt, bool diag_tile = false) {
+  stage_rows<kDMode, kScaled, kDiag>(g, alpha, beta, acc, smem, D, diag_tile);
   __syncthreads();
-  store_tile(E, C, (uint32_t)g.ldc);
-  if (T) store_tile_t(E, T, (uint32_t)ldt);
+  store_tile(smem, C, (uint32_t)g.ldc);
+  if (T) store_tile_t(smem, T, (uint32_t)ldt);
+}
+
+// The Muon update of eight consecutive parameters p[0..7] (lo, hi) from eight
+// bf16 results u (two per word, the lower element in the low half).
+__device__ __forceinline__ void update8(const u32x4 u, f32x4& lo, f32x4& hi, float scale,
+                                        float decay, float neg_lr) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t w = u[e >> 1];
+    const uint32_t h = (e & 1) ? (w >> 16) : (w & 0xFFFFu);
+    if (e < 4) lo[e] = muon_update_element(lo[e], h, scale, decay, neg_lr);
+    else hi[e - 4] = muon_update_element(hi[e - 4], h, scale, decay, neg_lr);
+  }
+}
+
+// The Muon update in place of the store of C (gemm_apply_kernel).  Chunk i
+// (0..31) of a lane is 8 consecutive parameters of one p row and the 8 bf16
+// results that update them.  kCols = false: p holds the tile (p rows = tile
+// rows), in store_tile's geometry (a wave covers two 1 KiB row segments per
+// chunk).  kCols = true: p holds the transposed tile, p[c][r] = tile[r][c]; the
+// transposing LDS reads of store_tile_t give each lane 8 consecutive elements
+// of one p row (16 rows per 16-lane group, the four groups' 32-byte pieces
+// adjacent in each row).
+template <bool kCols>
+__device__ __forceinline__ uint32_t apply_offset(int i, uint32_t ld) {
+  const int tid = threadIdx.x;
+  if constexpr (!kCols) {
+    const int c = tid + i * kThreads;
+    return (uint32_t)(c / (BN / 8)) * ld + (c % (BN / 8)) * 8;
+  } else {
+    const int lane = tid & 63, item = (tid >> 6) * 32 + i;
+    const int c0 = (item >> 3) * 16, rb = (item & 7) * 32 + (lane >> 4) * 8;
+    return (uint32_t)(c0 + (lane & 15)) * ld + rb;
+  }
+}
+
+template <bool kCols>
+__device__ __forceinline__ u32x4 apply_source(const uint16_t* E, int i) {
+  const int tid = threadIdx.x;
+  if constexpr (!kCols) {
+    const int c = tid + i * kThreads;
+    return *reinterpret_cast<const u32x4*>(E + (c / (BN / 8)) * LDE + (c % (BN / 8)) * 8);
+  } else {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+    auto tr = [](const uint16_t* at) {
+      return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+          (lds_bf16x4*)(__attribute__((address_space(3))) uint16_t*)at));
+    };
+    const int lane = tid & 63, j = lane & 15, item = (tid >> 6) * 32 + i;
+    const int c0 = (item >> 3) * 16, rb = (item & 7) * 32 + (lane >> 4) * 8;
+    const uint16_t* e = E + (rb + (j >> 2)) * LDE + c0 + 4 * (j & 3);
+    const u32x2 a = tr(e), b = tr(e + 4 * LDE);
+    return u32x4{a.x, a.y, b.x, b.y};
+  }
+}
+
+// The whole epilogue of one tile: the accumulators go through the LDS tile as
+// bf16 (the values the store of X' would write), then the parameters are
+// updated in two batches of 16 chunks, every load of a batch in flight before
+// its first update.  Measured against the separate finish pass on the config-5
+// batch (Muon step, round-robin on one box): 39.14 -> 38.77 ms per step; a
+// rolling look-ahead of 16 chunks (a load issued with every update) gave 38.84,
+// and issuing the first loads before the staging spilled registers.
+template <bool kScaled, bool kCols>
+__device__ __forceinline__ void epilogue_apply(const GemmArgs& g, float alpha, f32x16 (&acc)[4][4],
+                                               uint16_t* smem, float* p, uint32_t ld, float scale,
+                                               float decay, float neg_lr) {
+  constexpr int kChunks = 32, kBatch = 16;
+  stage_rows<kNoD, kScaled>(g, alpha, 0.0f, acc, smem, nullptr);
+  __syncthreads();
+#pragma unroll
+  for (int b0 = 0; b0 < kChunks; b0 += kBatch) {
+    f32x4 lo[kBatch], hi[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const float* at = p + apply_offset<kCols>(b0 + i, ld);
+      lo[i] = load_stream<true>(reinterpret_cast<const f32x4*>(at));
+      hi[i] = load_stream<true>(reinterpret_cast<const f32x4*>(at + 4));
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      update8(apply_source<kCols>(smem, b0 + i), lo[i], hi[i], scale, decay, neg_lr);
+      float* at = p + apply_offset<kCols>(b0 + i, ld);
+      store_stream<true>(reinterpret_cast<f32x4*>(at), lo[i]);
+      store_stream<true>(reinterpret_cast<f32x4*>(at + 4), hi[i]);
+    }
+  }
 }
 
 // kQKN: Q is stored [K, N] (row-major, N contiguous) instead of [N, K]; its
-// fragments come from the LDS through transposing reads.
-template <bool kQKN, int kDMode, bool kScaled, bool kDiag>
-__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
+// fragments come from the LDS through transposing reads.  kApply (with kQKN):
+// the Muon update of GemmApply in place of the store of C.
+template <bool kQKN, int kDMode, bool kScaled, bool kDiag, bool kApply>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, const GemmApply* ap) {
+  static_assert(!kApply || (kQKN && kDMode == kNoD && !kDiag), "the update rides on X' = B' X");
   __shared__ __attribute__((aligned(16))) uint16_t smem[kSmemElems];
 
   // XCD-aware numbering: the grid is a multiple of 8; XCD x = id % 8 runs the
@@ -639,6 +742,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
   __syncthreads();  // all fragment reads and trailing loads done before the epilogue reuses the LDS
 
   // ---- epilogue ------------------------------------------------------------
+  if constexpr (kApply) {
+    float alpha = g.alpha;
+    if (g.bscale != nullptr) alpha *= g.bscale[b];
+    if (ap->transposed[b] == 0)  // p [m, n]: the tile's rows are p rows
+      epilogue_apply<kScaled, false>(g, alpha, acc, smem, ap->p[b] + row0 * ap->n + col0,
+                                     (uint32_t)ap->n, ap->scale[b], ap->decay, ap->neg_lr);
+    else  // p [n, m]: the tile's columns are p rows
+      epilogue_apply<kScaled, true>(g, alpha, acc, smem, ap->p[b] + col0 * ap->m + row0,
+                                    (uint32_t)ap->m, ap->scale[b], ap->decay, ap->neg_lr);
+    return;
+  }
   const uint16_t* D = nullptr;
   if (g.D) D = g.D + b * g.sd + row0 * g.ldd + col0;
   uint16_t* T = nullptr;  // transposed destination: Ct, or the mirror tile
@@ -670,6 +784,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
     epilogue<kDMode, kScaled, true>(g, alpha, beta, acc, smem, D, C, T, ldt);
   else
     epilogue<kDMode, kScaled, false>(g, alpha, beta, acc, smem, D, C, T, ldt);
+}
+
+template <bool kQKN, int kDMode, bool kScaled, bool kDiag>
+__global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs g) {
+  gemm_tile<kQKN, kDMode, kScaled, kDiag, false>(g, nullptr);
+}
+
+template <bool kScaled>
+__global__ __launch_bounds__(kThreads, 1) void gemm_apply_kernel(const GemmArgs g,
+                                                                 const GemmApply ap) {
+  gemm_tile<true, kNoD, kScaled, false, true>(g, &ap);
 }
 
 }  // namespace
@@ -761,6 +886,38 @@ int morph::gemm_nt_bf16_scaled(const uint16_t* P, const uint16_t* Q, const uint1
     else MORPH_GEMM_LAUNCH(false, kNoD, false, false);
   }
 #undef MORPH_GEMM_LAUNCH
+  return launch_status();
+}
+
+int morph::gemm_kn_apply(const uint16_t* P, const uint16_t* Q, int64_t M, int64_t N, int64_t K,
+                         int64_t batch, int64_t ldp, int64_t ldq, int64_t stride_p,
+                         int64_t stride_q, const float* bscale, const GemmApply& ap,
+                         void* stream) {
+  if (P == nullptr || Q == nullptr || M <= 0 || N <= 0 || K <= 0 || batch <= 0 ||
+      batch > kGemmMaxApply)
+    return MORPH_EINVAL;
+  if (M % BM || N % BN || K % MORPH_GEMM_TILE_K) return MORPH_ERANGE;
+  if (ap.m != M || ap.n != N || ldp < K || ldq < N || (ldp | ldq | stride_p | stride_q) % 8)
+    return MORPH_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(P) | reinterpret_cast<uintptr_t>(Q)) % 16) return MORPH_EINVAL;
+  for (int64_t b = 0; b < batch; ++b)
+    if (ap.p[b] == nullptr || reinterpret_cast<uintptr_t>(ap.p[b]) % 16 ||
+        (ap.transposed[b] != 0 && ap.transposed[b] != 1))
+      return MORPH_EINVAL;
+  // 32-bit offsets inside a tile: 255 rows of the widest row length
+  constexpr int64_t kMaxLd = int64_t(1) << 23;
+  if (ldp > kMaxLd || ldq > kMaxLd || M > kMaxLd || N > kMaxLd) return MORPH_ERANGE;
+  const int64_t tm = M / BM, tn = N / BN, per = tm * tn, total = batch * per;
+  const int64_t grid = (total + 7) / 8 * 8;
+  if (grid > (int64_t(1) << 31) - 1) return MORPH_ERANGE;
+  GemmArgs g{P, Q, nullptr, nullptr, nullptr, K, ldp, ldq, 0, 0, 0,
+             stride_p, stride_q, 0, 0, 0, 1.0f, 0.0f, bscale, 0.0f,
+             (int32_t)tm, (int32_t)tn, (int32_t)per, MORPH_GEMM_Q_KN, total};
+  hipStream_t s = as_stream(stream);
+  if (bscale != nullptr)
+    hipLaunchKernelGGL(gemm_apply_kernel<true>, dim3((unsigned)grid), dim3(kThreads), 0, s, g, ap);
+  else
+    hipLaunchKernelGGL(gemm_apply_kernel<false>, dim3((unsigned)grid), dim3(kThreads), 0, s, g, ap);
   return launch_status();
 }
 

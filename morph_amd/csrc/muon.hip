@@ -22,7 +22,10 @@
 // The quintic's linear term rides on B's diagonal: X' = a X + B X = (B + a I) X,
 // so the last product of an iteration reads no third operand (a is added in fp32
 // to B's diagonal before its bf16 rounding; measured against the FP32
-// reference this is as accurate as the separate a X term or more).
+// reference this is as accurate as the separate a X term or more).  A Muon
+// step's master update rides on the chain's last product where the operand has
+// no padding (newton_schulz_finish, gemm_kn_apply): its epilogue updates p from
+// the bf16 values it would have stored, so X is not written back and read again.
 //
 // Workspace (caller-allocated, morph_muon_workspace_bytes; no initial contents needed):
 // per-block partial sums f64; per-matrix 1/den, 1/den^2, den f32;
@@ -441,8 +444,7 @@ __device__ __forceinline__ float apply_one(float p, uint32_t u16, float scale, f
   if constexpr (kExtract) {
     return bf16_bits_to_float(u16);
   } else {
-    const float upd = bf16_bits_to_float(u16) * scale;
-    return __fmaf_rn(upd, neg_lr, p * decay);
+    return muon_update_element(p, u16, scale, decay, neg_lr);
   }
 }
 
@@ -698,8 +700,20 @@ int prepare(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols
   return rc;
 }
 
+// Whether the last product can carry the parameter update (gemm_kn_apply): the
+// operands have no padding and every parameter is 16-byte aligned.
+bool can_fuse_update(const morph_muon_matrix* mats, int count, const Layout& L) {
+  if (L.mp != L.m || L.np != L.n) return false;
+  for (int i = 0; i < count; ++i)
+    if (reinterpret_cast<uintptr_t>(mats[i].param) % 16) return false;
+  return true;
+}
+
+// fuse: the batch's matrices, whose parameter update the last product carries in
+// place of writing X (can_fuse_update must hold); nullptr: X is written.
 int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp,
-                  void* workspace, size_t workspace_bytes, void* stream) {
+                  void* workspace, size_t workspace_bytes, void* stream,
+                  const morph_muon_matrix* fuse = nullptr) {
   Bufs W;
   int rc = setup(nullptr, count, rows, cols, hp, workspace, workspace_bytes, false, false, &W);
   if (rc || count == 0) return rc;
@@ -723,6 +737,23 @@ int newton_schulz(int count, int64_t rows, int64_t cols, const morph_muon_hp* hp
                              ss, ss, ss, ss, 0, hp->c, hp->b, nullptr, hp->a, MORPH_GEMM_SYMMETRIC,
                              stream);
     if (rc) return rc;
+    if (fuse != nullptr && it == hp->ns_steps - 1) {
+      // the last X' = B' X updates the parameters instead of being stored: the
+      // finish pass's arithmetic (muon_update_element) on the same bf16 values
+      GemmApply ap;
+      for (int i = 0; i < count; ++i) {
+        ap.p[i] = fuse[i].param;
+        ap.transposed[i] = stored_is_x(fuse[i], rows, cols) ? 0 : 1;
+        ap.scale[i] = fuse[i].transposed ? hp->update_scale_transposed : hp->update_scale;
+      }
+      ap.m = L.m;
+      ap.n = L.n;
+      ap.decay = hp->decay;
+      ap.neg_lr = hp->neg_lr;
+      rc = gemm_kn_apply(W.B, X, L.mp, L.np, L.mp, count, m, n, ss, sx, inv_den, ap, stream);
+      if (rc) return rc;
+      break;
+    }
     // X' = B' X: X as the [K, N] operand (transposing LDS reads), into the other buffer
     rc = gemm_nt_bf16_scaled(W.B, X, nullptr, W.X[cur ^ 1], nullptr, L.mp, L.np, L.mp, count, m,
                              n, 0, n, 0, ss, sx, 0, sx, 0, 1.0f, 0.0f, inv_den, 0.0f,
@@ -772,6 +803,21 @@ int finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
   return launch_status();
 }
 
+// newton_schulz, then the parameter update of finish: carried by the last product
+// when the shape allows (can_fuse_update), else the finish pass after the chain.
+int newton_schulz_finish(const morph_muon_matrix* mats, int count, int64_t rows, int64_t cols,
+                         const morph_muon_hp* hp, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  Bufs W;
+  int rc = setup(mats, count, rows, cols, hp, workspace, workspace_bytes, true, false, &W);
+  if (rc || count == 0) return rc;
+  if (hp->ns_steps >= 1 && can_fuse_update(mats, count, W.L))
+    return newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream, mats);
+  rc = newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream);
+  if (!rc) rc = finish(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
+  return rc;
+}
+
 }  // namespace
 
 extern "C" int morph_muon_prepare(const morph_muon_matrix* mats, int count, int64_t rows,
@@ -804,12 +850,18 @@ extern "C" int morph_muon_finish_range(const morph_muon_matrix* mats, int count,
                 stream, first, n);
 }
 
+extern "C" int morph_muon_newton_schulz_finish(const morph_muon_matrix* mats, int count,
+                                               int64_t rows, int64_t cols,
+                                               const morph_muon_hp* hp, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+  return newton_schulz_finish(mats, count, rows, cols, hp, workspace, workspace_bytes, stream);
+}
+
 extern "C" int morph_muon_step(const morph_muon_matrix* mats, int count, int64_t rows,
                                int64_t cols, const morph_muon_hp* hp, void* workspace,
                                size_t workspace_bytes, void* stream) {
   int rc = prepare(mats, count, rows, cols, hp, workspace, workspace_bytes, false, nullptr, stream);
-  if (!rc) rc = newton_schulz(count, rows, cols, hp, workspace, workspace_bytes, stream);
-  if (!rc) rc = finish(mats, count, rows, cols, hp, workspace, workspace_bytes, false, stream);
+  if (!rc) rc = newton_schulz_finish(mats, count, rows, cols, hp, workspace, workspace_bytes, stream);
   return rc;
 }
 

@@ -181,11 +181,13 @@ def _finish_range(batch, first, n, stream):
                                         stream_handle(stream)))
 
 
-def _chains(batches, stream, timer=None):
+def _chains(batches, stream, timer=None, with_update=False):
     """The Newton-Schulz chain of every batch _prepare enqueued.
 
     timer: optional list; (start_event, end_event, dense flops, executed flops) around
-    each NS chain.
+    each NS chain.  with_update: the chain of a Muon-step batch also applies the
+    parameter update (morph_muon_newton_schulz_finish: in its last product's epilogue
+    where the shape allows), so no finish follows; orthogonalize batches are chains only.
     """
     L = lib()
     sh = stream_handle(stream)
@@ -195,7 +197,11 @@ def _chains(batches, stream, timer=None):
             s = stream or torch.cuda.current_stream()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
-        check(L.morph_muon_newton_schulz(count, rows, cols, ctypes.byref(hp), wsp, wsn, sh))
+        if with_update and not orth_only:
+            check(L.morph_muon_newton_schulz_finish(arr, count, rows, cols, ctypes.byref(hp), wsp,
+                                                    wsn, sh))
+        else:
+            check(L.morph_muon_newton_schulz(count, rows, cols, ctypes.byref(hp), wsp, wsn, sh))
         if timer is not None:
             e1.record(s)
             timer.append((e0, e1, ns_flops(rows, cols, count, hp.ns_steps),
@@ -203,13 +209,16 @@ def _chains(batches, stream, timer=None):
 
 
 def _complete(batches, stream, timer=None):
-    """Newton-Schulz chains, then the finish of every batch _prepare enqueued."""
-    _chains(batches, stream, timer)
+    """Newton-Schulz chains and the finish of every batch _prepare enqueued: a Muon
+    step's update rides on its chain (morph_muon_newton_schulz_finish), orthogonalize's
+    U goes into param by the finish pass."""
+    _chains(batches, stream, timer, with_update=True)
     L = lib()
     sh = stream_handle(stream)
     for arr, count, rows, cols, hp, orth_only, ws in batches:
-        check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), int(orth_only),
-                                  ctypes.c_void_p(ws.data_ptr()), ws.numel(), sh))
+        if orth_only:
+            check(L.morph_muon_finish(arr, count, rows, cols, ctypes.byref(hp), 1,
+                                      ctypes.c_void_p(ws.data_ptr()), ws.numel(), sh))
 
 
 def _check_matrix(t, name):

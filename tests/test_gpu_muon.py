@@ -233,7 +233,7 @@ def on_device(t, offset):
 @pytest.mark.parametrize("shape,offset", [
     ((128, 256), 0), ((100, 300), 0), ((45, 70), 0), ((96, 96), 0), ((1, 300), 0),
     ((300, 100), 0), ((70, 45), 0), ((300, 1), 0), ((4100, 1024), 0), ((4096, 640), 0),
-    ((256, 640), 1), ((640, 256), 1), ((640, 256), 2)])
+    ((256, 640), 1), ((640, 256), 1), ((640, 256), 2), ((512, 768), 0), ((768, 512), 0)])
 def test_muon_step_elementwise_bitexact(shape, offset):
     """momentum/Nesterov and the master update match the oracle bit for bit: the flat
     passes (X in the stored layout: (128, 256) whole blocks, (100, 300) a partial last
@@ -242,7 +242,8 @@ def test_muon_step_elementwise_bitexact(shape, offset):
     single column, (4100, 1024) whole tiles and a partial last band, (4096, 640) whole
     momentum tiles and a partial last column of apply tiles); with `offset`, parameter,
     momentum and gradient start off a 16-byte boundary, so every pass takes its
-    element-wise path."""
+    element-wise path.  (512, 768) and (768, 512) have no operand padding: their update
+    rides on the last Newton-Schulz product's epilogue (morph_muon_newton_schulz_finish)."""
     from oracle import reference as R
     gen = torch.Generator().manual_seed(7)
     p0 = torch.randn(shape, generator=gen) * .02
@@ -436,8 +437,56 @@ def test_hybrid_state_dict_roundtrip():
         assert torch.equal(p, q), n
 
 
+@pytest.mark.parametrize("rows,cols,steps", [(256, 512, 5), (512, 256, 5), (512, 768, 2),
+                                             (768, 512, 1), (192, 320, 5), (320, 192, 1)])
+def test_update_in_the_last_product_equals_the_finish_pass(rows, cols, steps):
+    """morph_muon_newton_schulz_finish carries the master update in the last X' = B' X
+    product's epilogue when the operand has no padding -- both orientations in one batch,
+    so the epilogue writes p rows from the tile's rows and from its columns, scale
+    sqrt(max(1, r/c)) per matrix; with steps == 1 the last product is also the first,
+    which carries 1/den -- and falls back to the finish pass otherwise ((192, 320),
+    (320, 192)).  Either way parameters and momenta are bit-identical to
+    prepare + newton_schulz + finish."""
+    import ctypes
+    from morph_amd import _lib
+    L = _lib.lib()
+    gen = torch.Generator().manual_seed(rows + cols + steps)
+    shapes = [(rows, cols), (cols, rows), (rows, cols), (cols, rows)]
+    p0 = [torch.randn(s, generator=gen) * .02 for s in shapes]
+    m0 = [torch.randn(s, generator=gen) * 1e-3 for s in shapes]
+    g = [(torch.randn(s, generator=gen) * 1e-3).to(DEV) for s in shapes]
+    hp = muon._step_hp(rows, cols, .02, .01, steps)
+    results = []
+    for fused in (True, False):
+        p, m = [t.to(DEV) for t in p0], [t.to(DEV) for t in m0]
+        ws = torch.zeros(L.morph_muon_workspace_bytes(rows, cols, 4), dtype=torch.uint8,
+                         device=DEV)
+        wsp, sh = ctypes.c_void_p(ws.data_ptr()), _lib.stream_handle()
+        arr = (_lib.MuonMatrix * 4)()
+        for i in range(4):
+            arr[i].grad, arr[i].momentum, arr[i].param = (g[i].data_ptr(), m[i].data_ptr(),
+                                                          p[i].data_ptr())
+            arr[i].transposed = int(shapes[i] != (rows, cols))
+        _lib.check(L.morph_muon_prepare(arr, 4, rows, cols, ctypes.byref(hp), 0, wsp, ws.numel(),
+                                        None, sh))
+        if fused:
+            _lib.check(L.morph_muon_newton_schulz_finish(arr, 4, rows, cols, ctypes.byref(hp), wsp,
+                                                         ws.numel(), sh))
+        else:
+            _lib.check(L.morph_muon_newton_schulz(4, rows, cols, ctypes.byref(hp), wsp, ws.numel(),
+                                                  sh))
+            _lib.check(L.morph_muon_finish(arr, 4, rows, cols, ctypes.byref(hp), 0, wsp, ws.numel(),
+                                           sh))
+        torch.cuda.synchronize()
+        results.append((p, m))
+    for i in range(4):
+        assert torch.equal(results[0][0][i], results[1][0][i]), i
+        assert torch.equal(results[0][1][i], results[1][1][i]), i
+        assert not torch.equal(results[0][0][i].cpu(), p0[i])  # the update happened
+
+
 def test_one_call_c_entry_equals_phased_path():
-    """morph_muon_step (C convenience) == prepare/newton_schulz/finish as the Python layer runs them."""
+    """morph_muon_step (C convenience) == prepare + newton_schulz_finish as the Python layer runs them."""
     import ctypes
     from morph_amd import _lib
     gen = torch.Generator().manual_seed(9)
