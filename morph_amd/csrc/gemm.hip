@@ -394,90 +394,86 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& g, float alpha, fl
   if (T) store_tile_t(smem, T, (uint32_t)ldt);
 }
 
-// The Muon update of eight consecutive parameters p[0..7] (lo, hi) from eight
-// bf16 results u (two per word, the lower element in the low half).
-__device__ __forceinline__ void update8(const u32x4 u, f32x4& lo, f32x4& hi, float scale,
-                                        float decay, float neg_lr) {
+// The Muon update of four consecutive parameters from four bf16 results u (two
+// per word, the lower element in the low half).
+__device__ __forceinline__ void update4(const u32x2 u, f32x4& v, float scale, float decay,
+                                        float neg_lr) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
+  for (int e = 0; e < 4; ++e) {
     const uint32_t w = u[e >> 1];
-    const uint32_t h = (e & 1) ? (w >> 16) : (w & 0xFFFFu);
-    if (e < 4) lo[e] = muon_update_element(lo[e], h, scale, decay, neg_lr);
-    else hi[e - 4] = muon_update_element(hi[e - 4], h, scale, decay, neg_lr);
+    v[e] = muon_update_element(v[e], (e & 1) ? (w >> 16) : (w & 0xFFFFu), scale, decay, neg_lr);
   }
 }
 
-// The Muon update in place of the store of C (gemm_apply_kernel).  Chunk i
-// (0..31) of a lane is 8 consecutive parameters of one p row and the 8 bf16
-// results that update them.  kCols = false: p holds the tile (p rows = tile
-// rows), in store_tile's geometry (a wave covers two 1 KiB row segments per
-// chunk).  kCols = true: p holds the transposed tile, p[c][r] = tile[r][c]; the
-// transposing LDS reads of store_tile_t give each lane 8 consecutive elements
-// of one p row (16 rows per 16-lane group, the four groups' 32-byte pieces
-// adjacent in each row).
+// The Muon update in place of the store of C (gemm_apply_kernel).  Quad i
+// (0..63) of a lane is 4 consecutive parameters of one p row and the 4 bf16
+// results that update them; every access instruction covers whole contiguous
+// pieces of rows (a non-temporal access to every other 16 bytes of a line
+// fetches and writes lines twice).  kCols = false: p holds the tile (p rows =
+// tile rows); a wave's instruction covers one whole 1 KiB row.  kCols = true: p
+// holds the transposed tile, p[c][r] = tile[r][c]; a transposing LDS read gives
+// lane j of a 16-lane group the 4 consecutive elements of p row c0 + j at
+// columns t .. t + 3, and the four groups take adjacent t, so an instruction
+// covers 64 contiguous bytes of each of 16 p rows (the quad's other half the
+// next 64).
 template <bool kCols>
 __device__ __forceinline__ uint32_t apply_offset(int i, uint32_t ld) {
   const int tid = threadIdx.x;
   if constexpr (!kCols) {
-    const int c = tid + i * kThreads;
-    return (uint32_t)(c / (BN / 8)) * ld + (c % (BN / 8)) * 8;
+    const int q = tid + i * kThreads;
+    return (uint32_t)(q >> 6) * ld + (q & 63) * 4;
   } else {
-    const int lane = tid & 63, item = (tid >> 6) * 32 + i;
-    const int c0 = (item >> 3) * 16, rb = (item & 7) * 32 + (lane >> 4) * 8;
-    return (uint32_t)(c0 + (lane & 15)) * ld + rb;
+    const int lane = tid & 63, item = (tid >> 6) * 32 + (i >> 1);
+    const int c0 = (item >> 3) * 16, t = (item & 7) * 32 + 16 * (i & 1) + 4 * (lane >> 4);
+    return (uint32_t)(c0 + (lane & 15)) * ld + t;
   }
 }
 
 template <bool kCols>
-__device__ __forceinline__ u32x4 apply_source(const uint16_t* E, int i) {
+__device__ __forceinline__ u32x2 apply_source(const uint16_t* E, int i) {
   const int tid = threadIdx.x;
   if constexpr (!kCols) {
-    const int c = tid + i * kThreads;
-    return *reinterpret_cast<const u32x4*>(E + (c / (BN / 8)) * LDE + (c % (BN / 8)) * 8);
+    const int q = tid + i * kThreads;
+    return *reinterpret_cast<const u32x2*>(E + (q >> 6) * LDE + (q & 63) * 4);
   } else {
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-    auto tr = [](const uint16_t* at) {
-      return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-          (lds_bf16x4*)(__attribute__((address_space(3))) uint16_t*)at));
-    };
-    const int lane = tid & 63, j = lane & 15, item = (tid >> 6) * 32 + i;
-    const int c0 = (item >> 3) * 16, rb = (item & 7) * 32 + (lane >> 4) * 8;
-    const uint16_t* e = E + (rb + (j >> 2)) * LDE + c0 + 4 * (j & 3);
-    const u32x2 a = tr(e), b = tr(e + 4 * LDE);
-    return u32x4{a.x, a.y, b.x, b.y};
+    // lane j, slot e <- element j % 4 of source lane 4 e + j / 4 (ds_read_b64_tr_b16):
+    // source lane s reads tile row t + s / 4, columns c0 + 4 (s % 4) .. + 3, so lane j
+    // receives tile rows t .. t + 3 of column c0 + j
+    const int lane = tid & 63, j = lane & 15, item = (tid >> 6) * 32 + (i >> 1);
+    const int c0 = (item >> 3) * 16, t = (item & 7) * 32 + 16 * (i & 1) + 4 * (lane >> 4);
+    const uint16_t* e = E + (t + (j >> 2)) * LDE + c0 + 4 * (j & 3);
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4*)(__attribute__((address_space(3))) uint16_t*)e));
   }
 }
 
 // The whole epilogue of one tile: the accumulators go through the LDS tile as
 // bf16 (the values the store of X' would write), then the parameters are
-// updated in two batches of 16 chunks, every load of a batch in flight before
+// updated in four batches of 16 quads, every load of a batch in flight before
 // its first update.  Measured against the separate finish pass on the config-5
-// batch (Muon step, round-robin on one box): 39.14 -> 38.77 ms per step; a
-// rolling look-ahead of 16 chunks (a load issued with every update) gave 38.84,
-// and issuing the first loads before the staging spilled registers.
+// batch (Muon step, round-robin on one box): 39.14 -> 38.77 ms per step with
+// 32-byte chunks per lane; a rolling look-ahead (a load issued with every
+// update) gave 38.84, and issuing the first loads before the staging spilled
+// registers.
 template <bool kScaled, bool kCols>
 __device__ __forceinline__ void epilogue_apply(const GemmArgs& g, float alpha, f32x16 (&acc)[4][4],
                                                uint16_t* smem, float* p, uint32_t ld, float scale,
                                                float decay, float neg_lr) {
-  constexpr int kChunks = 32, kBatch = 16;
+  constexpr int kQuads = 64, kBatch = 16;
   stage_rows<kNoD, kScaled>(g, alpha, 0.0f, acc, smem, nullptr);
   __syncthreads();
 #pragma unroll
-  for (int b0 = 0; b0 < kChunks; b0 += kBatch) {
-    f32x4 lo[kBatch], hi[kBatch];
+  for (int b0 = 0; b0 < kQuads; b0 += kBatch) {
+    f32x4 v[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      v[i] = load_stream<true>(reinterpret_cast<const f32x4*>(p + apply_offset<kCols>(b0 + i, ld)));
 #pragma unroll
     for (int i = 0; i < kBatch; ++i) {
-      const float* at = p + apply_offset<kCols>(b0 + i, ld);
-      lo[i] = load_stream<true>(reinterpret_cast<const f32x4*>(at));
-      hi[i] = load_stream<true>(reinterpret_cast<const f32x4*>(at + 4));
-    }
-#pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
-      update8(apply_source<kCols>(smem, b0 + i), lo[i], hi[i], scale, decay, neg_lr);
-      float* at = p + apply_offset<kCols>(b0 + i, ld);
-      store_stream<true>(reinterpret_cast<f32x4*>(at), lo[i]);
-      store_stream<true>(reinterpret_cast<f32x4*>(at + 4), hi[i]);
+      update4(apply_source<kCols>(smem, b0 + i), v[i], scale, decay, neg_lr);
+      store_stream<true>(reinterpret_cast<f32x4*>(p + apply_offset<kCols>(b0 + i, ld)), v[i]);
     }
   }
 }
