@@ -756,7 +756,8 @@ def embedding_main(args):
     print(json.dumps(line), flush=True)
 
 
-def time_streamed(steps, warmup, muon=False, pinned=False, resident=False, device_grads=False):
+def time_streamed(steps, warmup, muon=False, pinned=False, resident=False, device_grads=False,
+                  stream_parts=None):
     """The streamed engines' layout (runner.py:41-46, engine.py:75-88): FP32 masters and
     FP32 (already unscaled) gradients in pageable CPU memory, optimizer state resident in
     HBM.  A step uploads every gradient and master through pinned staging, runs the
@@ -781,6 +782,8 @@ def time_streamed(steps, warmup, muon=False, pinned=False, resident=False, devic
         if pinned:
             pin_host_tensors(model.parameters())
         opt = HybridMuonAdamW(model, lr=3e-4, muon_lr=0.02, resident_masters=resident)
+        if stream_parts is not None:
+            opt.stream_parts = stream_parts
         params = list(model.parameters())
         stagings = [opt._muon_masters, opt._muon_grads, opt.adam._staging]
     else:
@@ -818,7 +821,7 @@ def time_streamed(steps, warmup, muon=False, pinned=False, resident=False, devic
 
 def streamed_main(args, muon=False):
     r = time_streamed(args.steps, args.warmup, muon, args.pinned, args.resident_masters,
-                      args.device_grads)
+                      args.device_grads, args.stream_parts)
     n, t = r["n"], r["elapsed"] / args.steps
     line = {
         "metric": ("HybridMuonAdamW step" if muon else "AdamW step") + " with CPU FP32 masters "
@@ -843,6 +846,7 @@ def streamed_main(args, muon=False):
                                    ["device step", "masters back into the CPU tensors"]),
                    "params": n, "masters": "pinned" if args.pinned else "pageable",
                    "gradients": "device" if args.device_grads else "pageable",
+                   "stream_parts": args.stream_parts,
                    "resident_masters": bool(args.resident_masters)},
         "pcie": {"h2d_bytes_per_step": int(r["h2d"]), "d2h_bytes_per_step": int(r["d2h"]),
                  "h2d_plus_d2h_gb_per_s": round((r["h2d"] + r["d2h"]) / t / 1e9, 2),
@@ -1025,6 +1029,10 @@ def main():
     ap.add_argument("--device-grads", action="store_true",
                     help="streamed / streamed_muon: hand the gradients to step() as FP32 tensors "
                          "on the GPU (the engine's device stage buffers): no gradient upload")
+    ap.add_argument("--stream-parts", type=int, default=None, metavar="K",
+                    help="streamed_muon: HybridMuonAdamW.stream_parts (the matrices go through "
+                         "the step in K parts; default: the optimizer's choice, 2 with CPU "
+                         "gradients, one per 6 matrices with device gradients)")
     ap.add_argument("--copy-calibration", type=int, metavar="MIB", default=0,
                     help="only run 5 plain device copies of MIB MiB (rocprof counter scale)")
     args = ap.parse_args()

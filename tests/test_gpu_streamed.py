@@ -287,19 +287,22 @@ def test_hybrid_on_cpu_masters_equals_device_masters(model_cls, pinned, parts):
         assert torch.equal(opt_c.momentum[i].cpu(), m.cpu()), i
 
 
-@pytest.mark.parametrize("model_cls,which", [(Tiny, "all"), (Tiny, "some"), (Uneven, "all"),
-                                             (Uneven, "muon")])
-def test_hybrid_on_cpu_masters_takes_device_gradients(model_cls, which):
+@pytest.mark.parametrize("model_cls,which,parts", [(Tiny, "all", None), (Tiny, "some", None),
+                                                   (Uneven, "all", None), (Uneven, "muon", None),
+                                                   (Tiny, "all", 3), (Uneven, "muon", 2)])
+def test_hybrid_on_cpu_masters_takes_device_gradients(model_cls, which, parts):
     """step({p: g}) with gradients on the GPU (an engine's device stage buffers,
     engine.py:67, before Slot.flush copies them to CPU p.grad, :75-88): no gradient
     upload for those, and the same bits as the CPU-gradient step over three steps --
     masters, momenta, AdamW moments -- with every gradient on the device, every other
-    one, or only the Muon ones.  A parameter missing from the mapping is not stepped."""
+    one, or only the Muon ones, in the default and in fixed numbers of streamed parts.
+    A parameter missing from the mapping is not stepped."""
     torch.manual_seed(5)
     model_a = model_cls()
     model_b = copy.deepcopy(model_a)
     opt_a = HybridMuonAdamW(model_a, lr=.003, muon_lr=.02)
     opt_b = HybridMuonAdamW(model_b, lr=.003, muon_lr=.02)
+    opt_b.stream_parts = parts  # None: one part per 6 matrices with device gradients
     muon_ids = {id(p) for p in opt_b.muon}
     names = [n for n, _ in model_a.named_parameters()]
     for step in range(3):
