@@ -10,7 +10,7 @@ previous step (skip decision, loss scale, clocks), then the fused unscale +
 AdamW + FP16 export kernel -- all on the device, with no host round trip
 between steps.  Inputs are synthetic (seeded), resident in HBM before the
 timed region.  Other workloads: embedding (config 3), overflow (config 4),
-muon (config 5), grads, window, fp8.
+muon (config 5), grads, window, fp8, export, streamed, streamed_muon.
 
 Prints one JSON line.  `value` is whole-step throughput in Gparams/s;
 `roofline` is the fused AdamW kernel's algorithmic bandwidth (28 bytes per
@@ -577,6 +577,118 @@ def window_main(args):
         shutil.rmtree(root, ignore_errors=True)
 
 
+EXPORT_BYTES = 6  # the export's conversion: read the FP32 master 4, write FP16 2 (+ one flag per chunk)
+EXPORT_CHUNK = 1 << 20  # the reference's chunk (export.py:16): one conversion launch and flag each
+
+
+class _ExportConfig:
+    def to_dict(self):
+        return dict(preset="5b", d_model=3072, d_ff=6144)
+
+
+class _ExportModel(torch.nn.Module):
+    """The config-2 window's matrices on the meta device, as the export's schema check sees a
+    model (export.py:24-25): parameter names, shapes and order, and a config with to_dict()."""
+
+    def __init__(self):
+        super().__init__()
+        self.config = _ExportConfig()
+        mk = lambda o, i: torch.nn.Linear(i, o, bias=False, device="meta")  # noqa: E731
+        self.gate, self.up, self.down = mk(6144, 3072), mk(6144, 3072), mk(3072, 6144)
+
+
+def time_export(steps, warmup, root):
+    """FP16 shard export (f3, export.py:16-43) of the config-2 window from its [3, N] state
+    files: the rows go through pinned staging, the GPU converts each 1M-element chunk with its
+    range flag, the host writes and hashes the shards (SHA-256) and fsyncs them."""
+    import shutil
+    from morph_amd import _lib
+    from morph_amd.export import export_fp16
+    device = torch.device("cuda", 0)
+    model = _ExportModel()
+    state = root / "state"
+    state.mkdir()
+    store = _FileStore(state, [(n, p.shape) for n, p in model.named_parameters()])
+    (state / "manifest.json").write_text(json.dumps(dict(
+        entries=store.entries, step=7, dirty=False, config=model.config.to_dict())))
+    times = []
+    for k in range(warmup + steps):
+        out = root / f"out{k}"
+        t0 = time.perf_counter()
+        export_fp16(state, out, model=model, device=device)
+        if k >= warmup:
+            times.append(time.perf_counter() - t0)
+        shutil.rmtree(out)
+    # the export's conversion launch: one 1M-element chunk with its range flag, back to back
+    src = torch.randn(EXPORT_CHUNK, device=device) * .02
+    dst = torch.empty(EXPORT_CHUNK, dtype=torch.float16, device=device)
+    flag = torch.zeros(1, dtype=torch.int32, device=device)
+    L, sh = _lib.lib(), _lib.stream_handle()
+    launch = lambda: _lib.check(L.morph_convert_f32(  # noqa: E731
+        ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), _lib.DTYPE_F16,
+        EXPORT_CHUNK, ctypes.c_void_p(flag.data_ptr()), sh))
+    for _ in range(20):
+        launch()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(200):
+        launch()
+    e1.record()
+    torch.cuda.synchronize()
+    return dict(n=sum(e["size"] for e in store.entries.values()), times=sorted(times),
+                launch_s=e0.elapsed_time(e1) / 1e3 / 200, state=state, model=model)
+
+
+def cpu_baseline_export(state, model, out):
+    """The reference's export (export.py:26-36: memmap rows, finite/range check, astype('<f2'),
+    write, SHA-256, fsync per shard) restated on the CPU, on the same state files."""
+    from oracle import reference as R
+    cpus = host_cpus()
+    t0 = time.perf_counter()
+    R.export_fp16_reference(state, out, model, durable=True)
+    t = time.perf_counter() - t0
+    n = sum(p.numel() for p in model.parameters())
+    return dict(value=round(n / t / 1e9, 4), unit="Gparams/s", **cpu_fields(cpus), kind="port",
+                sample=f"one export of the config-2 window's three state files: {t * 1e3:.0f} ms "
+                       "(single-threaded numpy, as the reference's loop runs)")
+
+
+def export_main(args):
+    import shutil
+    import tempfile
+    root = Path(tempfile.mkdtemp(prefix="morph_export_"))
+    try:
+        r = time_export(args.steps, args.warmup, root)
+        n, t = r["n"], r["times"][len(r["times"]) // 2]
+        achieved = EXPORT_BYTES * EXPORT_CHUNK / r["launch_s"] / 1e9
+        line = {
+            "metric": "FP16 shard export Gparams/s (morph-fp16-shards-v1: GPU encode + range check, "
+                      "SHA-256, fsync), 5B SwiGLU window, 1 MI355X",
+            "value": round(n / t / 1e9, 3), "unit": "Gparams/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 2),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+            "data": "synthetic",
+            "config": {"workload": "config 2 window as three [3, N] float32 state files -> FP16 "
+                                   "shards + manifest (one export per step; median)",
+                       "params": n, "shapes": CONFIG2_SHAPES, "chunk_elements": EXPORT_CHUNK,
+                       "state_dir": "tempfile.mkdtemp() on the GPU box"},
+            "shard_write_gbs": round(2 * n / t / 1e9, 3),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "convert_kernel<F16,true> (one 1M-element chunk with its range "
+                                   "flag, launches back to back)",
+                         "avg_launch_us": round(r["launch_s"] * 1e6, 2),
+                         "bytes_per_launch": EXPORT_BYTES * EXPORT_CHUNK},
+            "bound_by": "the host: file reads into pinned memory, SHA-256 and fsync of the shards; "
+                        "the GPU conversion is a few percent of the export",
+        }
+        line["cpu_baseline"] = None if args.no_cpu_baseline else cpu_baseline_export(
+            r["state"], r["model"], root / "cpu")
+        print(json.dumps(line), flush=True)
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+
+
 FP8_PACK_BYTES, FP8_UNPACK_BYTES = 3, 3  # FP16 in 2 + byte out 1 (+ 4 B per 256); byte in 1 + FP16 out 2
 
 
@@ -1013,12 +1125,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("adamw", "embedding", "overflow", "muon", "grads",
-                                           "window", "fp8", "streamed", "streamed_muon"),
+                                           "window", "fp8", "export", "streamed", "streamed_muon"),
                     default="adamw",
                     help="adamw: the headline config-2 step (default); embedding: config 3; "
                          "overflow: config 4's skip sequence; muon: config 5; "
                          "grads: the stage-gradient window; window: the HBM-resident [3, N] "
-                         "state; fp8: block-scaled FP8 transport encoding; streamed / "
+                         "state; fp8: block-scaled FP8 transport encoding; export: FP16 shard "
+                         "export of the window's state files; streamed / "
                          "streamed_muon: config 2 / config 5 with CPU FP32 masters, PCIe included")
     ap.add_argument("--pinned", action="store_true",
                     help="streamed / streamed_muon: masters in page-locked host memory "
@@ -1066,6 +1179,8 @@ def main():
         return streamed_main(args, muon=args.workload == "streamed_muon")
     if args.workload == "fp8":
         return fp8_main(args)
+    if args.workload == "export":
+        return export_main(args)
     r = time_gpu(args.steps, args.warmup)
     n = r["n"]
     ms_per_step = r["elapsed"] / args.steps * 1e3

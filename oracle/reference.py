@@ -384,8 +384,9 @@ def e4m3fn_value(byte):
     return sign * (1 + m / 8) * 2.0 ** (e - 7)
 
 
-def export_fp16_reference(state_dir, output, model, chunk_elements=1048576):
-    """export.py:16-43 on the CPU: same checks, encoding, hashing, manifest."""
+def export_fp16_reference(state_dir, output, model, chunk_elements=1048576, durable=False):
+    """export.py:16-43 on the CPU: same checks, encoding, hashing, manifest.  durable: flush
+    and fsync each shard as export.py:35 does (left out where only the bytes matter)."""
     import hashlib
     import json
     from pathlib import Path
@@ -411,6 +412,9 @@ def export_fp16_reference(state_dir, output, model, chunk_elements=1048576):
                 encoded = value.astype("<f2").tobytes()
                 handle.write(encoded)
                 digest.update(encoded)
+            if durable:
+                handle.flush()
+                os.fsync(handle.fileno())
         del source
         weights[name] = dict(file=path.name, shape=entry["shape"], dtype="float16",
                              sha256=digest.hexdigest())
