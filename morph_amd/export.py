@@ -32,11 +32,11 @@ import threading
 from contextlib import nullcontext
 from pathlib import Path
 
-import numpy as np
 import torch
 
 from . import _lib
 from ._lib import check, lib, stream_handle
+from .window import _read_exact
 
 FP16_ERROR = "weights cannot be represented by finite FP16"
 
@@ -84,14 +84,16 @@ class _Encoder:
         self.out_host = torch.empty(self.segment, dtype=torch.float16, pin_memory=True)
         self.flags_host = torch.empty(per, dtype=torch.int32, pin_memory=True)
 
-    def encode(self, lo, hi, mapped_row=None, row_dev=None):
-        """Encode elements [lo, hi) of a row; returns (fp16 numpy array, per-chunk flags)."""
+    def encode(self, lo, hi, fd=None, row_dev=None):
+        """Encode elements [lo, hi) of a weight row -- row 0 of the [3, N] state file open
+        as `fd` (read straight into the pinned staging), or the device tensor `row_dev` --
+        and return (fp16 numpy array, per-chunk flags)."""
         n = hi - lo
         chunks = -(-n // self.chunk)
         L, sh = lib(), stream_handle(self.stream)
         with torch.cuda.stream(self.stream):
             if row_dev is None:
-                np.copyto(self.src_host[:n].numpy(), mapped_row[lo:hi])
+                _read_exact(fd, self.src_host[:n].numpy(), 4 * lo)  # row 0 starts the file
                 self.src_dev[:n].copy_(self.src_host[:n], non_blocking=True)
                 src = self.src_dev
             else:
@@ -197,31 +199,35 @@ def export_fp16(state_dir, output, chunk_elements=1048576, lock_held=False, *, m
                 size = entry["size"]
                 resident = window is not None and name in window.state
                 row_dev = window.state[name][0] if resident else None
-                mapped = None if resident else np.memmap(
-                    state_dir / entry["file"], dtype=np.float32, mode="r", shape=(3, size))
-                slots.acquire()
-                if failed():
-                    slots.release()
-                    break
-                writer = _ShardWriter(output / entry["file"], chunk_elements, slots)
-                writer.start()
-                writers.append((name, entry, writer))
-                bad = False
+                fd = None if resident else os.open(state_dir / entry["file"], os.O_RDONLY)
                 try:
-                    for lo in range(0, size, encoder.segment):
-                        if failed():
-                            bad = True
-                            break
-                        hi = min(lo + encoder.segment, size)
-                        encoded, flags = encoder.encode(
-                            lo, hi, mapped_row=None if resident else mapped[0], row_dev=row_dev)
-                        writer.queue.put((encoded, flags))
-                        if flags.any():
-                            bad = True  # the reference stops at this parameter's first bad chunk
-                            break
+                    if fd is not None and os.fstat(fd).st_size < 12 * size:
+                        # where the reference's np.memmap of the [3, N] file refuses it
+                        raise ValueError("mmap length is greater than file size")
+                    slots.acquire()
+                    if failed():
+                        slots.release()
+                        break
+                    writer = _ShardWriter(output / entry["file"], chunk_elements, slots)
+                    writer.start()
+                    writers.append((name, entry, writer))
+                    bad = False
+                    try:
+                        for lo in range(0, size, encoder.segment):
+                            if failed():
+                                bad = True
+                                break
+                            hi = min(lo + encoder.segment, size)
+                            encoded, flags = encoder.encode(lo, hi, fd=fd, row_dev=row_dev)
+                            writer.queue.put((encoded, flags))
+                            if flags.any():
+                                bad = True  # the reference stops at this parameter's first bad chunk
+                                break
+                    finally:
+                        writer.queue.put(None)
                 finally:
-                    writer.queue.put(None)
-                    del mapped
+                    if fd is not None:
+                        os.close(fd)
                 if bad:
                     break
         finally:

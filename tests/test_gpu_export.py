@@ -157,3 +157,18 @@ def test_a_failed_shard_write_stops_the_export(tmp_path, monkeypatch):
     with pytest.raises(OSError, match="injected"):
         export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", 100, model=model, hash_threads=1)
     assert sorted(p.name for p in (tmp_path / "gpu").iterdir()) == ["00000.bin"]
+
+
+def test_a_truncated_state_file_is_refused_where_the_reference_refuses_it(tmp_path):
+    """The reference maps each [3, N] file with np.memmap before it opens that shard, so a file
+    shorter than its schema raises ValueError there and the output holds the shards before it.
+    The GPU export reads the rows with pread and checks the size at the same point."""
+    model = Tiny()
+    entries = make_state(tmp_path / "run" / "state", model)
+    victim = tmp_path / "run" / "state" / entries["gate.weight"]["file"]
+    victim.write_bytes(victim.read_bytes()[:-4])
+    with pytest.raises(ValueError, match="mmap length"):
+        export_fp16(tmp_path / "run" / "state", tmp_path / "gpu", 100, model=model)
+    with pytest.raises(ValueError, match="mmap length"):
+        R.export_fp16_reference(tmp_path / "run" / "state", tmp_path / "cpu", model, 100)
+    same_dirs(tmp_path / "gpu", tmp_path / "cpu")
