@@ -36,7 +36,7 @@ import torch
 
 from . import _lib
 from ._lib import check, lib, stream_handle
-from .window import _read_exact
+from .staging import read_exact
 
 FP16_ERROR = "weights cannot be represented by finite FP16"
 
@@ -93,7 +93,7 @@ class _Encoder:
         L, sh = lib(), stream_handle(self.stream)
         with torch.cuda.stream(self.stream):
             if row_dev is None:
-                _read_exact(fd, self.src_host[:n].numpy(), 4 * lo)  # row 0 starts the file
+                read_exact(fd, self.src_host[:n].numpy(), 4 * lo)  # row 0 starts the file
                 self.src_dev[:n].copy_(self.src_host[:n], non_blocking=True)
                 src = self.src_dev
             else:

@@ -19,6 +19,7 @@ per direction (PCIe carries both directions at once: 88 GB/s together against
 56 GB/s either way alone, measured on MI355X).
 """
 import collections
+import os
 import threading
 
 import torch
@@ -46,6 +47,26 @@ def shared_stream(device, role):
         if stream is None:
             stream = _STREAMS[key] = torch.cuda.Stream(torch.device("cuda", key[0]))
     return stream
+
+
+def read_exact(fd, out, offset):
+    """Fill the contiguous array `out` (e.g. a view of pinned staging) from the file `fd` at
+    byte `offset`, by pread; a file that ends first raises OSError."""
+    view = memoryview(out).cast("B")
+    got = 0
+    while got < len(view):
+        n = os.preadv(fd, [view[got:]], offset + got)
+        if n <= 0:
+            raise OSError(f"short read of a state file at offset {offset + got}")
+        got += n
+
+
+def write_exact(fd, data, offset):
+    """Write all of the contiguous array `data` to the file `fd` at byte `offset`, by pwrite."""
+    view = memoryview(data).cast("B")
+    put = 0
+    while put < len(view):
+        put += os.pwrite(fd, view[put:], offset + put)
 
 
 def _align(x):

@@ -36,7 +36,7 @@ import torch
 from . import arena, kernels
 from ._lib import check, dtype_code, lib, stream_handle
 from .hyper import disk_constants
-from .staging import shared_stream
+from .staging import read_exact, shared_stream, write_exact
 
 
 def _fsync(path):
@@ -117,7 +117,7 @@ class ResidentWindow:
                     t0 = time.perf_counter()
                     host = s["host"].numpy()
                     for row in range(3):  # row r of the file starts at r * N floats
-                        _read_exact(fd, host[row, :n], (row * size + start) * 4)
+                        read_exact(fd, host[row, :n], (row * size + start) * 4)
                     self.timing["file_read"] += time.perf_counter() - t0
                     with torch.cuda.stream(self._copy):
                         for row in range(3):
@@ -207,7 +207,7 @@ class ResidentWindow:
                     fetch(k + 1)  # overlaps this chunk's file write
                 t0 = time.perf_counter()
                 for row in range(3):  # the chunk's columns of all three rows, then the fault hook
-                    _write_exact(fd, hnp[k % 2, row, :end - start], (row * size + start) * 4)
+                    write_exact(fd, hnp[k % 2, row, :end - start], (row * size + start) * 4)
                 self.timing["file_write"] += time.perf_counter() - t0
                 self.transfer_bytes["d2h_state"] += 12 * (end - start)
                 self.store.fault('partial_state_write')
@@ -235,24 +235,6 @@ def _state_rows(size, device):
                           device=device)
     base = ((-storage.data_ptr()) % arena.ALIGN_LARGE) // 4
     return storage.as_strided((3, size), (stride, 1), base)
-
-
-def _read_exact(fd, out, offset):
-    """Fill the contiguous float32 array `out` from the file at byte `offset`."""
-    view = memoryview(out).cast("B")
-    got = 0
-    while got < len(view):
-        n = os.preadv(fd, [view[got:]], offset + got)
-        if n <= 0:
-            raise OSError(f"short read of a state file at offset {offset + got}")
-        got += n
-
-
-def _write_exact(fd, data, offset):
-    view = memoryview(data).cast("B")
-    put = 0
-    while put < len(view):
-        put += os.pwrite(fd, view[put:], offset + put)
 
 
 class ResidentDiskUpdate:
