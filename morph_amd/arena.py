@@ -22,7 +22,7 @@ STAGGER = 64 << 10
 ALIGN_SMALL = 256
 
 
-def _align(x, a):
+def align_up(x, a):
     return (x + a - 1) // a * a
 
 
@@ -40,13 +40,13 @@ def plan(groups):
         row = []
         for k, nbytes in enumerate(sizes):
             if large:
-                off = _align(off, ALIGN_LARGE) + k * STAGGER
+                off = align_up(off, ALIGN_LARGE) + k * STAGGER
             else:
-                off = _align(off, ALIGN_SMALL)
+                off = align_up(off, ALIGN_SMALL)
             row.append(off)
             off += nbytes
         offsets.append(row)
-    return offsets, _align(off, ALIGN_SMALL)
+    return offsets, align_up(off, ALIGN_SMALL)
 
 
 class Arena:

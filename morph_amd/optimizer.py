@@ -343,6 +343,9 @@ class FusedAdamW:
                                  f"{tuple(flat[i][1].shape)}")
             if g.device.type not in ("cpu", "cuda"):
                 raise ValueError(f"gradient {i} is on {g.device}")
+            if g.device.type == "cuda" and g.device != self.device:
+                raise ValueError(f"gradient {i} is on {g.device}, the optimizer on "
+                                 f"{self.device}")
         dev = list(grads)
         if host:
             dtypes = {grads[i].dtype for i in host}

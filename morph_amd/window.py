@@ -227,9 +227,9 @@ def _state_rows(size, device):
     2 MiB phase, the placement the fused pass streams slowest from."""
     nbytes = 4 * size
     if nbytes >= arena.ALIGN_LARGE:
-        stride = (arena._align(nbytes, arena.ALIGN_LARGE) + arena.STAGGER) // 4
+        stride = (arena.align_up(nbytes, arena.ALIGN_LARGE) + arena.STAGGER) // 4
     else:
-        stride = arena._align(max(nbytes, 4), arena.ALIGN_SMALL) // 4
+        stride = arena.align_up(max(nbytes, 4), arena.ALIGN_SMALL) // 4
     # room to move the first row up to the next 2 MiB boundary
     storage = torch.empty(2 * stride + size + arena.ALIGN_LARGE // 4, dtype=torch.float32,
                           device=device)
