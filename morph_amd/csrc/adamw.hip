@@ -56,7 +56,6 @@
 #define MORPH_ADAMW_NT 1
 #endif
 
-
 namespace morph {
 namespace {
 

@@ -50,6 +50,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kMaxMats = 64;
+static_assert(kGemmMaxApply >= kMaxMats, "a whole batch's update rides on one fused product");
 // Workgroup shapes of the elementwise passes (HBM-bound; measured round-robin on
 // the 42-matrix [3072, 6144] batch, bit-identical results throughout):
 //   momentum_kernel: 256 lanes, one 128-bit access each (128 lanes: 6% slower);
