@@ -885,7 +885,7 @@ def time_streamed(steps, warmup, muon=False, pinned=False, resident=False, devic
     p.grad), so no gradient crosses PCIe."""
     from morph_amd import FusedAdamW, pin_host_tensors
     from morph_amd.muon import HybridMuonAdamW
-    cpus = host_cpus()  # the host copies run on torch's intra-op threads
+    cpus = host_cpus()  # torch's intra-op threads; the staging copies run on the library's pool
     if muon:
         model = Config5("cpu")
         gen = torch.Generator().manual_seed(6)
@@ -926,9 +926,11 @@ def time_streamed(steps, warmup, muon=False, pinned=False, resident=False, devic
         step()  # returns with the new masters in the CPU tensors
     elapsed = time.perf_counter() - t0
     torch.cuda.synchronize()
+    from morph_amd import staging
     return dict(elapsed=elapsed, n=sum(p.numel() for p in params), cpus=cpus,
                 h2d=(sum(st.bytes_h2d for st in stagings) - h2d0) / steps,
-                d2h=(sum(st.bytes_d2h for st in stagings) - d2h0) / steps)
+                d2h=(sum(st.bytes_d2h for st in stagings) - d2h0) / steps,
+                copy_threads=staging.COPY_THREADS or staging.default_copy_threads())
 
 
 def streamed_main(args, muon=False):
@@ -962,7 +964,8 @@ def streamed_main(args, muon=False):
                    "resident_masters": bool(args.resident_masters)},
         "pcie": {"h2d_bytes_per_step": int(r["h2d"]), "d2h_bytes_per_step": int(r["d2h"]),
                  "h2d_plus_d2h_gb_per_s": round((r["h2d"] + r["d2h"]) / t / 1e9, 2),
-                 "host_threads": r["cpus"]["threads"]},
+                 "host_threads": r["cpus"]["threads"],
+                 "staging_copy_threads": r["copy_threads"]},
         "cpu_baseline": None if args.no_cpu_baseline else (
             cpu_baseline_muon() if muon else cpu_baseline()),
     }

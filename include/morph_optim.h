@@ -6,11 +6,12 @@
  * calls these entry points through ctypes; no torch type crosses the boundary.
  *
  * Conventions shared by every entry point:
- *   - Tensor pointers are device pointers owned by the caller.  The library
- *     allocates nothing and keeps no state between calls, so calls are
- *     re-entrant from several host threads.  The one exception is the
- *     library-owned partials array of morph_grad_accumulate_final_noalloc
- *     (see there).
+ *   - Tensor pointers are device pointers owned by the caller (morph_host_copy
+ *     alone takes host pointers).  The library allocates no device memory and
+ *     keeps no state between calls, so calls are re-entrant from several host
+ *     threads.  The exceptions are the library-owned partials array of
+ *     morph_grad_accumulate_final_noalloc and the host thread pool of
+ *     morph_host_copy (see there).
  *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as
  *     void*; NULL means the legacy default stream).  Ordering between calls
  *     comes only from the stream.
@@ -43,7 +44,7 @@
 extern "C" {
 #endif
 
-#define MORPH_ABI_VERSION 8
+#define MORPH_ABI_VERSION 9
 
 /* Element types of gradient / export buffers. */
 enum morph_dtype {
@@ -491,6 +492,20 @@ int morph_muon_finish_range(const morph_muon_matrix* mats, int count, int64_t ro
 int morph_muon_newton_schulz_finish(const morph_muon_matrix* mats, int count, int64_t rows,
                                     int64_t cols, const morph_muon_hp* hp, void* workspace,
                                     size_t workspace_bytes, void* stream);
+
+/* ---- Host staging copy ---------------------------------------------------
+ * dst[0, bytes) <- src[0, bytes) on the host, split over up to `threads`
+ * threads (1..64) of a pool the library keeps; the calling thread copies
+ * pieces too and the call returns when the copy is complete.  Host memory
+ * only, no GPU work: the staging of pageable host tensors (masters, gradients)
+ * through pinned buffers.  Its workers sleep when idle, so unlike an
+ * intra-op pool spinning on every core they leave cores to the HIP runtime
+ * while DMAs are in flight.  No counterpart in the reference, whose
+ * optimizer updates the CPU tensors in place (streamtrain/optimizer.py:47-62).
+ * MORPH_EINVAL for null pointers with bytes > 0, threads < 1 or overlapping
+ * ranges; MORPH_ERANGE for threads > 64.  Calls are serialized.
+ */
+int morph_host_copy(void* dst, const void* src, size_t bytes, int threads);
 
 #ifdef __cplusplus
 }

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must load the HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmorph_optim.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPE_NONE, DTYPE_F32, DTYPE_F16, DTYPE_BF16 = -1, 0, 1, 2
 HP_DIVIDE_SCALE, HP_APPLY_CLIP, HP_APPLY_DECAY, HP_LERP_LARGE = 1, 2, 4, 8
@@ -29,7 +29,7 @@ EXPORTS = (
     "morph_gemm_nt_bf16",
     "morph_muon_workspace_bytes", "morph_muon_step", "morph_muon_orthogonalize",
     "morph_muon_prepare", "morph_muon_newton_schulz", "morph_muon_finish",
-    "morph_muon_finish_range", "morph_muon_newton_schulz_finish",
+    "morph_muon_finish_range", "morph_muon_newton_schulz_finish", "morph_host_copy",
 )
 GEMM_TILE_M, GEMM_TILE_N, GEMM_TILE_K = 256, 256, 64
 GEMM_SYMMETRIC = 1
@@ -160,6 +160,7 @@ def _load():
         "morph_muon_newton_schulz_finish": ([ctypes.POINTER(MuonMatrix), i32, i64, i64,
                                              ctypes.POINTER(MuonHP), vp, ctypes.c_size_t, vp],
                                             i32),
+        "morph_host_copy": ([vp, vp, ctypes.c_size_t, i32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(handle, name)

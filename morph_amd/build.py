@@ -16,7 +16,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
-SOURCES = ["abi.hip", "adamw.hip", "nonfinite.hip", "step.hip", "grads.hip", "convert.hip", "fp8.hip", "gemm.hip", "muon.hip"]
+SOURCES = ["abi.hip", "adamw.hip", "nonfinite.hip", "step.hip", "grads.hip", "convert.hip", "fp8.hip", "gemm.hip", "muon.hip", "hostcopy.hip"]
 OUTPUT = PKG / "lib" / "libmorph_optim.so"
 ARCH = os.environ.get("MORPH_OFFLOAD_ARCH", "gfx950")
 

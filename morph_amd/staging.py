@@ -19,10 +19,13 @@ per direction (PCIe carries both directions at once: 88 GB/s together against
 56 GB/s either way alone, measured on MI355X).
 """
 import collections
+import ctypes
 import os
 import threading
 
 import torch
+
+from ._lib import check, lib
 
 ALIGN = 64  # elements of 4 bytes: mirrors start 256-byte aligned
 
@@ -67,6 +70,33 @@ def write_exact(fd, data, offset):
     put = 0
     while put < len(view):
         put += os.pwrite(fd, view[put:], offset + put)
+
+
+COPY_THREADS = None  # host_copy's thread count; None: default_copy_threads()
+
+
+def default_copy_threads():
+    """Threads for the host side of the staging copies: the cores this process may run
+    on less four (left to the HIP runtime and the thread that queues the DMAs), at most 8,
+    at least 1.  Measured on the MI355X box's 16 cores, streamed steps with CPU masters
+    and gradients: config 2 11.0-11.8 ms per step with 8 threads against 12.4-13.4 with
+    4, 11.9-12.2 with 12 and 12.0-12.6 with 16; config 5 139-140 ms with 8, 140-147
+    with 6, 142-143 with 12."""
+    return max(1, min(8, len(os.sched_getaffinity(0)) - 4))
+
+
+def host_copy(dst, src):
+    """dst <- src for two contiguous CPU tensors of one dtype and size, on the library's
+    copy pool (morph_host_copy) with COPY_THREADS threads."""
+    if dst.dtype != src.dtype or dst.numel() != src.numel():
+        raise ValueError("host_copy: dtype or size differs")
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ValueError("host_copy: tensors must be contiguous")
+    if dst.device.type != "cpu" or src.device.type != "cpu":
+        raise ValueError("host_copy: tensors must be on the CPU")
+    threads = COPY_THREADS if COPY_THREADS is not None else default_copy_threads()
+    check(lib().morph_host_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
+                                dst.numel() * dst.element_size(), int(threads)))
 
 
 def _align(x):
@@ -233,7 +263,7 @@ class HostStaging:
             buf = slot["buf"]
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
-                buf[at:at + e - s].copy_(src[i][s:e])
+                host_copy(buf[at:at + e - s], src[i][s:e])
             with torch.cuda.stream(self._copy):
                 self.flat[lo:hi].copy_(buf[:hi - lo], non_blocking=True)
                 slot["event"].record(self._copy)
@@ -278,7 +308,7 @@ class HostStaging:
             slot["event"].synchronize()
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
-                dst[i][s:e].copy_(slot["buf"][at:at + e - s])
+                host_copy(dst[i][s:e], slot["buf"][at:at + e - s])
             if k + 2 < len(chunks):
                 fetch(k + 2)  # this buffer is free again
         if pinned:
@@ -325,7 +355,7 @@ class HostStaging:
             slot["event"].synchronize()
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
-                host[i][s:e].copy_(slot["buf"][at:at + e - s])
+                host_copy(host[i][s:e], slot["buf"][at:at + e - s])
             free.append(slot)
 
         def service(block):
@@ -367,7 +397,7 @@ class HostStaging:
                 slot["event"].synchronize()  # the upload that last read this buffer is done
                 for i, s, e in pieces:
                     at = self.offsets[i] + s - lo
-                    slot["buf"][at:at + e - s].copy_(host[i][s:e])
+                    host_copy(slot["buf"][at:at + e - s], host[i][s:e])
                 with torch.cuda.stream(self._copy):
                     self.flat[lo:hi].copy_(slot["buf"][:hi - lo], non_blocking=True)
                     slot["event"].record(self._copy)

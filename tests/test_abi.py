@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_status_strings():
     from morph_amd import _lib
     lib = _lib.lib()
-    assert lib.morph_abi_version() == _lib.ABI_VERSION == 8
+    assert lib.morph_abi_version() == _lib.ABI_VERSION == 9
     assert lib.morph_strerror(0) == b"ok"
     for code in (-1, -2, -3, -4, -5):
         assert lib.morph_strerror(code) not in (b"ok", b"unknown morph status")
