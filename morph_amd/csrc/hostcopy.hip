@@ -31,7 +31,9 @@ namespace morph {
 namespace {
 
 constexpr int kMaxCopyThreads = 64;
-constexpr size_t kMinPieceBytes = size_t(1) << 20;  // smaller copies stay on the caller
+// Pieces of at least 1 MiB: waking a sleeping worker costs more than copying
+// a smaller piece on the calling thread.
+constexpr size_t kMinPieceBytes = size_t(1) << 20;
 
 struct CopyPool {
   std::mutex call;  // one copy at a time

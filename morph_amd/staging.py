@@ -8,12 +8,12 @@ Here the optimizer state stays resident in HBM and only the masters and the
 gradients cross PCIe: HostStaging keeps one flat device buffer holding a
 mirror of each host tensor (each at a 256-byte aligned offset) and moves data
 between the host tensors and the mirrors in chunks through two pinned buffers
-per direction, so the host-side copy of one chunk (pageable <-> pinned, torch's
-multi-threaded copy) overlaps the DMA of the other.  Tensors whose mirrors are
+per direction, so the host-side copy of one chunk (pageable <-> pinned, on the
+library's copy pool: host_copy) overlaps the DMA of the other.  Tensors whose mirrors are
 adjacent travel in one DMA per chunk.  A host tensor that is already in
 page-locked memory (pin_host_tensors, or a caller's own pinned allocation) is
 reached by the DMA directly: its chunks skip the pinned buffers and the host
-copy, which bounds the pageable transfers (about 72 GB/s of host memcpy).  pipeline() streams chunks through a
+copy, which bounds the pageable transfers.  pipeline() streams chunks through a
 device pass: chunk k goes up while chunk k - 1 comes back, on one copy stream
 per direction (PCIe carries both directions at once: 88 GB/s together against
 56 GB/s either way alone, measured on MI355X).
@@ -85,18 +85,40 @@ def default_copy_threads():
     return max(1, min(8, len(os.sched_getaffinity(0)) - 4))
 
 
+_SMALL_COPY_BYTES = 64 << 10  # under this, torch's copy_ stays below its parallel grain (inline)
+_default_threads = None
+
+
+def _copy_threads():
+    global _default_threads
+    if COPY_THREADS is not None:
+        return int(COPY_THREADS)
+    if _default_threads is None:
+        _default_threads = default_copy_threads()
+    return _default_threads
+
+
 def host_copy(dst, src):
-    """dst <- src for two contiguous CPU tensors of one dtype and size, on the library's
-    copy pool (morph_host_copy) with COPY_THREADS threads."""
+    """dst <- src for two contiguous CPU tensors of one dtype and size: on the library's
+    copy pool (morph_host_copy, COPY_THREADS threads), or inline on the calling thread
+    for a copy under 64 KiB, where a pool call costs more than the copy."""
     if dst.dtype != src.dtype or dst.numel() != src.numel():
         raise ValueError("host_copy: dtype or size differs")
-    if not (dst.is_contiguous() and src.is_contiguous()):
-        raise ValueError("host_copy: tensors must be contiguous")
     if dst.device.type != "cpu" or src.device.type != "cpu":
         raise ValueError("host_copy: tensors must be on the CPU")
-    threads = COPY_THREADS if COPY_THREADS is not None else default_copy_threads()
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ValueError("host_copy: tensors must be contiguous")
+    _copy(dst, src)
+
+
+def _copy(dst, src):
+    """host_copy without its checks, for tensors the staging has validated already."""
+    nbytes = dst.numel() * dst.element_size()
+    if nbytes < _SMALL_COPY_BYTES:
+        dst.copy_(src)
+        return
     check(lib().morph_host_copy(ctypes.c_void_p(dst.data_ptr()), ctypes.c_void_p(src.data_ptr()),
-                                dst.numel() * dst.element_size(), int(threads)))
+                                nbytes, _copy_threads()))
 
 
 def _align(x):
@@ -263,7 +285,7 @@ class HostStaging:
             buf = slot["buf"]
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
-                host_copy(buf[at:at + e - s], src[i][s:e])
+                _copy(buf[at:at + e - s], src[i][s:e])
             with torch.cuda.stream(self._copy):
                 self.flat[lo:hi].copy_(buf[:hi - lo], non_blocking=True)
                 slot["event"].record(self._copy)
@@ -308,7 +330,7 @@ class HostStaging:
             slot["event"].synchronize()
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
-                host_copy(dst[i][s:e], slot["buf"][at:at + e - s])
+                _copy(dst[i][s:e], slot["buf"][at:at + e - s])
             if k + 2 < len(chunks):
                 fetch(k + 2)  # this buffer is free again
         if pinned:
@@ -355,7 +377,7 @@ class HostStaging:
             slot["event"].synchronize()
             for i, s, e in pieces:
                 at = self.offsets[i] + s - lo
-                host_copy(host[i][s:e], slot["buf"][at:at + e - s])
+                _copy(host[i][s:e], slot["buf"][at:at + e - s])
             free.append(slot)
 
         def service(block):
@@ -397,7 +419,7 @@ class HostStaging:
                 slot["event"].synchronize()  # the upload that last read this buffer is done
                 for i, s, e in pieces:
                     at = self.offsets[i] + s - lo
-                    host_copy(slot["buf"][at:at + e - s], host[i][s:e])
+                    _copy(slot["buf"][at:at + e - s], host[i][s:e])
                 with torch.cuda.stream(self._copy):
                     self.flat[lo:hi].copy_(slot["buf"][:hi - lo], non_blocking=True)
                     slot["event"].record(self._copy)
