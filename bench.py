@@ -10,7 +10,7 @@ previous step (skip decision, loss scale, clocks), then the fused unscale +
 AdamW + FP16 export kernel -- all on the device, with no host round trip
 between steps.  Inputs are synthetic (seeded), resident in HBM before the
 timed region.  Other workloads: embedding (config 3), overflow (config 4),
-muon (config 5), grads, window, fp8, export, streamed, streamed_muon.
+muon (config 5), grads, window, disk, fp8, export, streamed, streamed_muon.
 
 Prints one JSON line.  `value` is whole-step throughput in Gparams/s;
 `roofline` is the fused AdamW kernel's algorithmic bandwidth (28 bytes per
@@ -577,6 +577,94 @@ def window_main(args):
         shutil.rmtree(root, ignore_errors=True)
 
 
+DISK_BYTES = 28  # DiskState.update's chunk pass: read g32 4 + w,m,v 12; write w,m,v 12 (no copy)
+DISK_CHUNK = 1 << 20  # DiskState.update's default chunk_elements (disk.py:203)
+
+
+def time_disk(steps, warmup, root):
+    """DiskState.update (a1, disk.py:203-223) through GpuDiskUpdate on the config-2 window's
+    [3, N] files: per parameter, each 1M-element chunk of the memmapped file is staged through
+    pinned memory, updated by one fused launch and written back, then flush and fsync."""
+    from morph_amd import kernels
+    from morph_amd.disk import GpuDiskUpdate
+    from morph_amd.hyper import disk_constants
+
+    class Store(GpuDiskUpdate, _FileStore):
+        pass
+
+    device = torch.device("cuda", 0)
+    names = ["ffn.gate.weight", "ffn.up.weight", "ffn.down.weight"]
+    store = Store(root, list(zip(names, CONFIG2_SHAPES)))
+    gen = torch.Generator(device=device).manual_seed(5)
+    grads = {n: torch.randn(s, generator=gen, device=device) * 1e-4 for n, s in zip(names, CONFIG2_SHAPES)}
+    step = 0
+    for _ in range(warmup):
+        step += 1
+        for n in names:
+            store.update(n, grads[n], step, 3e-4, 1.0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step += 1
+        for n in names:
+            store.update(n, grads[n], step, 3e-4, 1.0)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    # the chunk launch itself, back to back on device buffers of one chunk
+    w, m, v, g = (torch.randn(DISK_CHUNK, device=device) * .02 for _ in range(4))
+    hp = disk_constants(step=1, lr=3e-4, clip=1.0)
+    for _ in range(20):
+        kernels.adamw_step(w, m, v, g, hp)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(200):
+        kernels.adamw_step(w, m, v, g, hp)
+    e1.record()
+    torch.cuda.synchronize()
+    return dict(n=sum(store.entries[n]["size"] for n in names), elapsed=elapsed,
+                launch_s=e0.elapsed_time(e1) / 1e3 / 200)
+
+
+def disk_main(args):
+    import shutil
+    import tempfile
+    root = Path(tempfile.mkdtemp(prefix="morph_disk_"))
+    try:
+        (root / "gpu").mkdir()
+        r = time_disk(args.steps, args.warmup, root / "gpu")
+        n = r["n"]
+        achieved = DISK_BYTES * DISK_CHUNK / r["launch_s"] / 1e9
+        line = {
+            "metric": "DiskState.update Gparams/s (memmapped [3, N] files: chunked staging, fused "
+                      "update, write-back, flush, fsync), 5B SwiGLU window, 1 MI355X",
+            "value": round(n * args.steps / r["elapsed"] / 1e9, 3), "unit": "Gparams/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(r["elapsed"] / args.steps * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "config 2 window as three [3, N] float32 state files; per step "
+                                   "GpuDiskUpdate.update of every file (chunks of 1M elements "
+                                   "through pinned memory, flush, fsync); FP32 gradients on the GPU",
+                       "params": n, "shapes": CONFIG2_SHAPES, "chunk_elements": DISK_CHUNK,
+                       "state_dir": "tempfile.mkdtemp() on the GPU box"},
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                         "kernel": "adamw_multi_kernel<F32,NoOut,host> (one 1M-element chunk, "
+                                   "launches back to back)",
+                         "avg_launch_us": round(r["launch_s"] * 1e6, 2),
+                         "bytes_per_launch": DISK_BYTES * DISK_CHUNK},
+            "bound_by": "the host: reading and writing the memmapped files and their fsync; a "
+                        "chunk's launch is a few microseconds",
+        }
+        if not args.no_cpu_baseline:
+            (root / "cpu").mkdir()
+            line["cpu_baseline"] = cpu_baseline_window(root / "cpu")
+        else:
+            line["cpu_baseline"] = None
+        print(json.dumps(line), flush=True)
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+
+
 EXPORT_BYTES = 6  # the export's conversion: read the FP32 master 4, write FP16 2 (+ one flag per chunk)
 EXPORT_CHUNK = 1 << 20  # the reference's chunk (export.py:16): one conversion launch and flag each
 
@@ -1128,12 +1216,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("adamw", "embedding", "overflow", "muon", "grads",
-                                           "window", "fp8", "export", "streamed", "streamed_muon"),
+                                           "window", "disk", "fp8", "export", "streamed",
+                                           "streamed_muon"),
                     default="adamw",
                     help="adamw: the headline config-2 step (default); embedding: config 3; "
                          "overflow: config 4's skip sequence; muon: config 5; "
                          "grads: the stage-gradient window; window: the HBM-resident [3, N] "
-                         "state; fp8: block-scaled FP8 transport encoding; export: FP16 shard "
+                         "state; disk: DiskState.update on the memmapped [3, N] files; "
+                         "fp8: block-scaled FP8 transport encoding; export: FP16 shard "
                          "export of the window's state files; streamed / "
                          "streamed_muon: config 2 / config 5 with CPU FP32 masters, PCIe included")
     ap.add_argument("--pinned", action="store_true",
@@ -1184,6 +1274,8 @@ def main():
         return fp8_main(args)
     if args.workload == "export":
         return export_main(args)
+    if args.workload == "disk":
+        return disk_main(args)
     r = time_gpu(args.steps, args.warmup)
     n = r["n"]
     ms_per_step = r["elapsed"] / args.steps * 1e3

@@ -24,7 +24,7 @@ import torch
 
 from . import kernels
 from .hyper import disk_constants
-from .staging import shared_stream
+from .staging import host_copy, shared_stream
 
 
 class _Staging:
@@ -58,6 +58,11 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
         raise ValueError("chunk_elements must be positive")
     device = torch.device(device) if device is not None else torch.device(
         "cuda", torch.cuda.current_device())
+    # A writable C-ordered ndarray (the np.memmap of DiskState) is read and written row by row
+    # on the library's copy pool, whose threads take the file's page faults in parallel; any
+    # other array-like goes through its own indexing.
+    rows = (torch.from_numpy(mapped) if isinstance(mapped, np.ndarray)
+            and mapped.flags.c_contiguous and mapped.flags.writeable else None)
     hp = disk_constants(step=step, lr=lr, clip=clip)
     chunk = min(chunk_elements, max(size, 1))
     compute = torch.cuda.current_stream(device)
@@ -75,13 +80,17 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
         end = min(start + chunk_elements, size)
         n = end - start
         s.done.synchronize()  # the previous user of this slot has been written back
-        s.host_state[:, :n].copy_(torch.from_numpy(np.ascontiguousarray(mapped[:, start:end])))
+        if rows is not None:
+            for r in range(3):
+                host_copy(s.host_state[r, :n], rows[r, start:end])
+        else:
+            s.host_state[:, :n].copy_(torch.from_numpy(np.ascontiguousarray(mapped[:, start:end])))
         with torch.cuda.stream(copy_in):
             s.dev_state[:, :n].copy_(s.host_state[:, :n], non_blocking=True)
             if flat.device.type == "cuda":
                 s.dev_grad[:n].copy_(flat[start:end], non_blocking=True)
             else:
-                s.host_grad[:n].copy_(flat[start:end])
+                host_copy(s.host_grad[:n], flat[start:end])
                 s.dev_grad[:n].copy_(s.host_grad[:n], non_blocking=True)
             s.ready.record(copy_in)
         return s, start, end, n
@@ -98,7 +107,11 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
             if k + 1 < len(starts):
                 pending = stage_in(k + 1)  # overlaps the update and copy-back of chunk k
             s.done.synchronize()
-            mapped[:, start:end] = s.host_state[:, :n].numpy()
+            if rows is not None:
+                for r in range(3):
+                    host_copy(rows[r, start:end], s.host_state[r, :n])
+            else:
+                mapped[:, start:end] = s.host_state[:, :n].numpy()
             if fault is not None:
                 fault('partial_state_write')
     finally:
