@@ -40,11 +40,12 @@ class _Staging:
 
 
 def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fault=None,
-                    device=None):
+                    device=None, dispatch_timer=None):
     """Update a [3, N] float32 array-like (e.g. np.memmap) in place, chunk by chunk.
 
     gradient: FP32 tensor with N elements (CPU, pinned or on the GPU), already
     unscaled (disk.py:447).  Writes back each chunk before calling fault().
+    dispatch_timer: optional kernels.DispatchTimer; each chunk's launch stamps a pair.
     """
     if mapped.shape[0] != 3 or mapped.dtype != np.float32:
         raise ValueError("state must be a [3, N] float32 array")
@@ -101,7 +102,8 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
             s, start, end, n = pending
             compute.wait_event(s.ready)
             w, m, v = s.dev_state[0, :n], s.dev_state[1, :n], s.dev_state[2, :n]
-            kernels.adamw_step(w, m, v, s.dev_grad[:n], hp, stream=compute)
+            kernels.adamw_step(w, m, v, s.dev_grad[:n], hp, stream=compute,
+                               events=dispatch_timer.next() if dispatch_timer is not None else None)
             s.host_state[:, :n].copy_(s.dev_state[:, :n], non_blocking=True)
             s.done.record(compute)
             if k + 1 < len(starts):
@@ -129,6 +131,7 @@ class GpuDiskUpdate:
     """
 
     update_device = None  # None: the current CUDA device
+    dispatch_timer = None  # optional kernels.DispatchTimer: stamps each chunk's launch
 
     def update(self, name, gradient, step, lr, clip, chunk_elements=1048576):
         if getattr(self, "_cache", None) is not None and hasattr(self, "_cache_lock"):
@@ -140,7 +143,7 @@ class GpuDiskUpdate:
         path = self.root / entry['file']
         mapped = np.memmap(path, dtype='float32', mode='r+', shape=(3, entry['size']))
         gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements, self.fault,
-                        self.update_device)
+                        self.update_device, self.dispatch_timer)
         mapped.flush()
         del mapped
         _fsync(path)
@@ -172,7 +175,7 @@ class GpuDiskUpdate:
                         mapped[key] = val
 
                 gpu_disk_update(_WriteThrough(), gradient, step, lr, clip, chunk_elements,
-                                self.fault, self.update_device)
+                                self.fault, self.update_device, self.dispatch_timer)
                 mapped.flush()
                 del mapped
                 _fsync(path)
