@@ -39,16 +39,29 @@ class _Staging:
         self.done = torch.cuda.Event()
 
 
+def _rows(a):
+    """torch views sharing the memory of a writable C-ordered ndarray (an np.memmap of a state
+    file, or a cached copy), else None."""
+    if isinstance(a, np.ndarray) and a.flags.c_contiguous and a.flags.writeable:
+        return torch.from_numpy(a)
+    return None
+
+
 def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fault=None,
-                    device=None, dispatch_timer=None):
+                    device=None, dispatch_timer=None, write_through=None):
     """Update a [3, N] float32 array-like (e.g. np.memmap) in place, chunk by chunk.
 
     gradient: FP32 tensor with N elements (CPU, pinned or on the GPU), already
     unscaled (disk.py:447).  Writes back each chunk before calling fault().
     dispatch_timer: optional kernels.DispatchTimer; each chunk's launch stamps a pair.
+    write_through: optional second [3, N] float32 array-like that every chunk's result is
+    also written to, after `mapped` (CachedDiskState's cache and its file).
     """
     if mapped.shape[0] != 3 or mapped.dtype != np.float32:
         raise ValueError("state must be a [3, N] float32 array")
+    if write_through is not None and (tuple(write_through.shape) != tuple(mapped.shape)
+                                      or write_through.dtype != np.float32):
+        raise ValueError("write_through must be a [3, N] float32 array like the state")
     size = mapped.shape[1]
     flat = gradient.detach().reshape(-1)
     if flat.numel() != size:
@@ -62,8 +75,9 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
     # A writable C-ordered ndarray (the np.memmap of DiskState) is read and written row by row
     # on the library's copy pool, whose threads take the file's page faults in parallel; any
     # other array-like goes through its own indexing.
-    rows = (torch.from_numpy(mapped) if isinstance(mapped, np.ndarray)
-            and mapped.flags.c_contiguous and mapped.flags.writeable else None)
+    targets = [mapped] if write_through is None else [mapped, write_through]
+    views = [_rows(t) for t in targets]
+    rows = views[0]
     hp = disk_constants(step=step, lr=lr, clip=clip)
     chunk = min(chunk_elements, max(size, 1))
     compute = torch.cuda.current_stream(device)
@@ -109,11 +123,12 @@ def gpu_disk_update(mapped, gradient, step, lr, clip, chunk_elements=1048576, fa
             if k + 1 < len(starts):
                 pending = stage_in(k + 1)  # overlaps the update and copy-back of chunk k
             s.done.synchronize()
-            if rows is not None:
-                for r in range(3):
-                    host_copy(rows[r, start:end], s.host_state[r, :n])
-            else:
-                mapped[:, start:end] = s.host_state[:, :n].numpy()
+            for target, view in zip(targets, views):
+                if view is not None:
+                    for r in range(3):
+                        host_copy(view[r, start:end], s.host_state[r, :n])
+                else:
+                    target[:, start:end] = s.host_state[:, :n].numpy()
             if fault is not None:
                 fault('partial_state_write')
     finally:
@@ -163,19 +178,9 @@ class GpuDiskUpdate:
             path = self.root / entry["file"]
             try:
                 mapped = np.memmap(path, dtype=np.float32, mode="r+", shape=(3, entry["size"]))
-
-                class _WriteThrough:
-                    shape, dtype = values.shape, values.dtype
-
-                    def __getitem__(_, key):
-                        return values[key]
-
-                    def __setitem__(_, key, val):
-                        values[key] = val
-                        mapped[key] = val
-
-                gpu_disk_update(_WriteThrough(), gradient, step, lr, clip, chunk_elements,
-                                self.fault, self.update_device, self.dispatch_timer)
+                # the cached values are read, and each chunk's result goes to them, then the file
+                gpu_disk_update(values, gradient, step, lr, clip, chunk_elements, self.fault,
+                                self.update_device, self.dispatch_timer, write_through=mapped)
                 mapped.flush()
                 del mapped
                 _fsync(path)
