@@ -30,6 +30,7 @@ rollback (state_cache.py:147-156).
 import ctypes
 import os
 import time
+import warnings
 
 import numpy as np
 import torch
@@ -108,13 +109,11 @@ class ResidentWindow:
             dev = _state_rows(size, self.device)
             # allocated on the compute stream, which may still have work queued on this memory
             self._copy.wait_stream(compute)
-            # A private (copy-on-write) mapping of the file, only read here; like the
-            # reference's memmap it refuses a file shorter than [3, N].  The library's copy
-            # pool moves each chunk's rows into the pinned buffer, its threads taking the
-            # page faults in parallel (one 226 MB file: 3.4 ms against 10.4 ms by pread on
-            # one thread, on the MI355X box).
-            rows = torch.from_numpy(np.memmap(self._path(name), dtype=np.float32, mode="c",
-                                              shape=(3, size)))
+            # A read-only mapping of the file; like the reference's memmap it refuses a file
+            # shorter than [3, N].  The library's copy pool moves each chunk's rows into the
+            # pinned buffer, its threads taking the page faults in parallel (one 226 MB file:
+            # 2.9-3.4 ms against 10.4-10.8 ms by pread on one thread, on the MI355X box).
+            rows = _read_only_rows(self._path(name), size)
             for k, start in enumerate(range(0, size, self.chunk)):
                 end = min(start + self.chunk, size)
                 n = end - start
@@ -221,6 +220,15 @@ class ResidentWindow:
         finally:
             self._copy.synchronize()
             os.close(fd)
+
+
+def _read_only_rows(path, size):
+    """The [3, size] float32 file at `path` as a CPU tensor over a read-only mapping (nothing
+    writes through it; torch warns about any non-writable array, so that warning is muted)."""
+    mapped = np.memmap(path, dtype=np.float32, mode="r", shape=(3, size))
+    with warnings.catch_warnings():
+        warnings.filterwarnings("ignore", message="The given NumPy array is not writable")
+        return torch.from_numpy(mapped)
 
 
 def _state_rows(size, device):
