@@ -91,6 +91,49 @@ def test_random_parameters_bitexact_and_torch_close(tmp_path, n, chunk):
     assert np.abs(got[0] - ref[0]).max() <= 1e-6 * np.abs(ref[0]).max()
 
 
+class _Indexed:
+    """A [3, N] array-like with only shape, dtype and indexing (not an ndarray)."""
+
+    def __init__(self, a):
+        self.a, self.shape, self.dtype = a, a.shape, a.dtype
+
+    def __getitem__(self, key):
+        return self.a[key]
+
+    def __setitem__(self, key, value):
+        self.a[key] = value
+
+
+def test_states_the_copy_pool_cannot_take_go_through_indexing():
+    """A writable C-ordered ndarray is read and written on the copy pool; any other [3, N]
+    array-like (Fortran order, an object with indexing only) takes the indexing path, and a
+    write-through target gets every chunk's result too.  All end bit-exact vs the oracle."""
+    rng = np.random.RandomState(8)
+    n, chunk = 5003, 1000
+    w0 = (rng.randn(n) * .02).astype(np.float32)
+    ups = [((rng.randn(n) * 1e-2).astype(np.float32), s, .001, .6) for s in (1, 2)]
+    want = oracle_disk(w0, ups)
+
+    def fresh():
+        return np.stack([w0, np.zeros(n, np.float32), np.zeros(n, np.float32)])
+
+    fortran = np.asfortranarray(fresh())
+    indexed = _Indexed(fresh())
+    cache, mirror = fresh(), _Indexed(fresh())
+    for g, step, lr, clip in ups:
+        gpu_disk_update(fortran, torch.from_numpy(g), step, lr, clip, chunk)
+        gpu_disk_update(indexed, torch.from_numpy(g), step, lr, clip, chunk)
+        gpu_disk_update(cache, torch.from_numpy(g), step, lr, clip, chunk, write_through=mirror)
+    assert not fortran.flags.c_contiguous
+    assert_same_bits(np.ascontiguousarray(fortran), want, "Fortran-ordered state")
+    assert_same_bits(indexed.a, want, "indexed state")
+    assert_same_bits(cache, want, "state with a write-through target")
+    assert_same_bits(mirror.a, want, "write-through target")
+    with pytest.raises(ValueError, match="write_through"):
+        gpu_disk_update(fresh(), torch.from_numpy(ups[0][0]), 1, .001, .6, chunk,
+                        write_through=np.zeros((3, n + 1), np.float32))
+
+
 def test_updates_from_two_threads_at_once(tmp_path):
     """disk.py:287-300: the main thread calls update() while SlotPrefetch's worker works on
     other parameters.  Two threads updating their own stores at the same time (each
