@@ -35,6 +35,7 @@ TRAFFIC_PROFILE_C3 = ROOT / "profiles" / "adamw_config3_traffic.json"
 MFMA_PROFILE = ROOT / "profiles" / "muon_config5_mfma.json"
 TRAFFIC_PROFILE_MUON = ROOT / "profiles" / "muon_config5_traffic.json"
 TRAFFIC_PROFILE_GRADS = ROOT / "profiles" / "grads_config2_traffic.json"
+TRAFFIC_PROFILE_WINDOW = ROOT / "profiles" / "window_config2_traffic.json"
 # rocprofv3 counters cannot run inside this process: `traffic` is read from the committed
 # summary of the FETCH_SIZE / WRITE_SIZE passes over this same workload, not measured here
 TRAFFIC_SOURCE = "profiles/%s: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes of this workload (committed, not this run)"
@@ -562,7 +563,9 @@ def window_main(args):
             "write_back_gbs": round(12 * n * args.steps / r["elapsed"] / 1e9, 2),
             "host_seconds": r["timing"],
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic(TRAFFIC_PROFILE_WINDOW),
+                         "traffic_source": TRAFFIC_SOURCE % TRAFFIC_PROFILE_WINDOW.name,
                          "kernel": "adamw_multi_kernel<F32,F16,host> (resident [3, N] state)",
                          "avg_launch_us": round(r["avg_kernel_s"] * 1e6, 2),
                          "bytes_per_launch": WINDOW_BYTES * n // r["kernels"]},
@@ -1196,7 +1199,8 @@ def measured_mfma():
 
 
 def measured_traffic(path=TRAFFIC_PROFILE):
-    """HBM bytes per fused-AdamW launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes."""
+    """HBM bytes per launch of a workload's dominant kernel, from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE passes."""
     try:
         return json.loads(path.read_text())["traffic_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
