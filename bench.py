@@ -584,19 +584,39 @@ DISK_BYTES = 28  # DiskState.update's chunk pass: read g32 4 + w,m,v 12; write w
 DISK_CHUNK = 1 << 20  # DiskState.update's default chunk_elements (disk.py:203)
 
 
-def time_disk(steps, warmup, root):
+def time_disk(steps, warmup, root, cached=False):
     """DiskState.update (a1, disk.py:203-223) through GpuDiskUpdate on the config-2 window's
     [3, N] files: per parameter, each 1M-element chunk of the memmapped file is staged through
-    pinned memory, updated by one fused launch and written back, then flush and fsync."""
+    pinned memory, updated by one fused launch and written back, then flush and fsync.
+    cached=True: CachedDiskState.update (a2, state_cache.py:103-140) with every state in its RAM
+    cache, so each update is a hit: the chunks are read from the cache and written to the cache
+    and the file."""
+    import collections
+    import threading
+    import numpy as np
     from morph_amd import kernels
     from morph_amd.disk import GpuDiskUpdate
 
     class Store(GpuDiskUpdate, _FileStore):
         pass
 
+    class CachedStore(Store):
+        # the cache attributes of state_cache.py that update() uses (23, 103-140)
+        def __init__(self, *a):
+            super().__init__(*a)
+            self._cache_lock = threading.RLock()
+            self._cache = collections.OrderedDict()
+            self._cache_stats = dict(hits=0, misses=0, estimated_bytes_avoided=0)
+            for name, e in self.entries.items():
+                self._cache[name] = np.fromfile(self.root / e["file"], dtype=np.float32).reshape(
+                    3, e["size"])
+
+        def _drop(self, name):
+            self._cache.pop(name, None)
+
     device = torch.device("cuda", 0)
     names = ["ffn.gate.weight", "ffn.up.weight", "ffn.down.weight"]
-    store = Store(root, list(zip(names, CONFIG2_SHAPES)))
+    store = (CachedStore if cached else Store)(root, list(zip(names, CONFIG2_SHAPES)))
     gen = torch.Generator(device=device).manual_seed(5)
     grads = {n: torch.randn(s, generator=gen, device=device) * 1e-4 for n, s in zip(names, CONFIG2_SHAPES)}
     step = 0
@@ -617,8 +637,9 @@ def time_disk(steps, warmup, root):
     elapsed = time.perf_counter() - t0
     store.dispatch_timer = None
     kms = timer.elapsed_ms()
+    hits = store._cache_stats["hits"] if cached else None
     return dict(n=sum(store.entries[n]["size"] for n in names), elapsed=elapsed,
-                launch_s=sum(kms) / len(kms) / 1e3, launches=len(kms))
+                launch_s=sum(kms) / len(kms) / 1e3, launches=len(kms), cache_hits=hits)
 
 
 def disk_main(args):
@@ -627,12 +648,16 @@ def disk_main(args):
     root = Path(tempfile.mkdtemp(prefix="morph_disk_"))
     try:
         (root / "gpu").mkdir()
-        r = time_disk(args.steps, args.warmup, root / "gpu")
+        r = time_disk(args.steps, args.warmup, root / "gpu", cached=args.cached)
         n = r["n"]
         achieved = DISK_BYTES * DISK_CHUNK / r["launch_s"] / 1e9
+        metric = ("CachedDiskState.update Gparams/s on cache hits (chunks from the RAM cache, "
+                  "written to the cache and the file, flush, fsync), 5B SwiGLU window, 1 MI355X"
+                  if args.cached else
+                  "DiskState.update Gparams/s (memmapped [3, N] files: chunked staging, fused "
+                  "update, write-back, flush, fsync), 5B SwiGLU window, 1 MI355X")
         line = {
-            "metric": "DiskState.update Gparams/s (memmapped [3, N] files: chunked staging, fused "
-                      "update, write-back, flush, fsync), 5B SwiGLU window, 1 MI355X",
+            "metric": metric,
             "value": round(n * args.steps / r["elapsed"] / 1e9, 3), "unit": "Gparams/s",
             "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(r["elapsed"] / args.steps * 1e3, 3), "higher_is_better": True,
@@ -641,6 +666,7 @@ def disk_main(args):
                                    "GpuDiskUpdate.update of every file (chunks of 1M elements "
                                    "through pinned memory, flush, fsync); FP32 gradients on the GPU",
                        "params": n, "shapes": CONFIG2_SHAPES, "chunk_elements": DISK_CHUNK,
+                       "cached": bool(args.cached), "cache_hits": r["cache_hits"],
                        "state_dir": "tempfile.mkdtemp() on the GPU box"},
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
@@ -1230,6 +1256,8 @@ def main():
     ap.add_argument("--resident-masters", action="store_true",
                     help="streamed / streamed_muon: keep the masters' device mirrors between "
                          "steps (resident_masters=True), so only gradients cross PCIe upward")
+    ap.add_argument("--cached", action="store_true",
+                    help="disk: CachedDiskState.update with every state in its RAM cache (hits)")
     ap.add_argument("--device-grads", action="store_true",
                     help="streamed / streamed_muon: hand the gradients to step() as FP32 tensors "
                          "on the GPU (the engine's device stage buffers): no gradient upload")
